@@ -1,0 +1,145 @@
+/*
+ * seoulkv4_hip.h - C ABI of the MI355X (gfx950) SeoulKV4 sparse decode path.
+ *
+ * This library replaces the reference's runtime seam
+ *   src/seoulkv4/_runtime.py:36   initialize(ttnn, device, k, v, q, index, args)
+ *   src/seoulkv4/_runtime.py:180  bind_query(state, q, args)
+ *   src/seoulkv4/_runtime.py:189  enqueue(state)
+ *   src/seoulkv4/_runtime.py:197  metadata(state)
+ * plus the device reads done by the public API:
+ *   src/seoulkv4/api.py:112       synchronize()
+ *   src/seoulkv4/result.py:30     DecodeResult.to_torch()
+ *   src/seoulkv4/api.py:127       debug_snapshot()
+ *
+ * Plain pointers and sizes only.  Host arrays are read during the call and not
+ * retained.  Every function returns 0 on success or a SKV_E* code; after a
+ * failure skv_last_error() describes it.  One handle serves one immutable
+ * cache; calls on one handle must not overlap (reference docs/POC_API.md:15-17).
+ */
+#ifndef SEOULKV4_HIP_H
+#define SEOULKV4_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SKV_GROUPS 4       /* KV heads ("cells") */
+#define SKV_HEADS 4        /* query heads per KV head (GQA 4:1) */
+#define SKV_DIM 256        /* head dimension */
+#define SKV_TOPK 100       /* retrieval tokens per query head */
+
+enum {
+  SKV_OK = 0,
+  SKV_EINVAL = 1,          /* bad argument or shape */
+  SKV_EHIP = 2,            /* HIP runtime error */
+  SKV_ENOMEM = 3,          /* device allocation failed */
+  SKV_EPOOL_OVERFLOW = 4,  /* candidate pool above capacity (reference ingest err 4) */
+  SKV_EPOOL_UNDERFLOW = 5, /* candidate pool below 2048 (reference ingest err 5) */
+  SKV_ESTATE = 6           /* call out of order / handle closed */
+};
+
+/* One index cell (KV head) as produced by SeoulKV4Index
+ * (reference _codecs/index.py:294-312 field names). */
+typedef struct {
+  const uint8_t *upper;        /* [nc][64] 2-bit codes, bits 3..2 of the 4-bit code */
+  const uint8_t *lower;        /* [nc][64] 2-bit codes, bits 1..0 */
+  const float *scale;          /* [nc] fp32 group scale ("scale") */
+  const uint16_t *resid_f16;   /* [nc] fp16 "coarse_residual_norm" */
+  const uint16_t *gfs_f16;     /* [nc/32] fp16 "group_fine_scale" */
+  const int32_t *offsets;      /* [nc+1] CSR offsets */
+  const int32_t *values;       /* [offsets[nc]] CSR token IDs */
+  int32_t nprobe;              /* P: probes per query head */
+  float lam;                   /* coarse margin lambda */
+} skv_cell_desc;
+
+typedef struct {
+  int32_t context;             /* T, tokens per KV head */
+  int32_t sink;                /* S: tokens [0, S) always attended */
+  int32_t local;               /* L: tokens [T-L, T) always attended */
+  int32_t n_centroids;         /* nc per cell, multiple of 32, <= 65536 */
+  int32_t pool_min;            /* pool lower bound (2048 in the reference) */
+  int32_t pool_capacity;       /* pool upper bound; <= 0 means no bound */
+  int32_t debug;               /* nonzero: keep stage outputs readable */
+  skv_cell_desc cells[SKV_GROUPS];
+} skv_index_desc;
+
+/* Reference _runtime.initialize (_runtime.py:36-177): uploads the index, runs
+ * the key codec and packs FP8 [V||K] records on the device.
+ * k_bf16, v_bf16: host [4][T][256] BF16 bit patterns.  device: HIP ordinal.
+ * stream: hipStream_t to enqueue on (NULL = a stream owned by the handle). */
+int skv_create(const skv_index_desc *index, const uint16_t *k_bf16,
+               const uint16_t *v_bf16, int device, void *stream,
+               void **handle_out);
+
+/* Reference bind_query (_runtime.py:180-186): copies host Q [16][256] BF16
+ * (query head j belongs to KV head j/4) to the device, asynchronously. */
+int skv_bind_query(void *handle, const uint16_t *q_bf16);
+
+/* Device-resident variant: q_dev is a device pointer to [16][256] BF16. */
+int skv_bind_query_device(void *handle, const void *q_dev);
+
+/* Reference enqueue (_runtime.py:189-194): launches every stage of one decode
+ * step on the handle's stream.  No host synchronisation, no readback. */
+int skv_enqueue(void *handle);
+
+/* Reference synchronize (api.py:112-115).  Waits for the stream and, if
+ * status is non-NULL, stores the per-group device status words
+ * [4][8] (see skv_status fields in DESIGN.md: pool size, error code, counts). */
+int skv_sync(void *handle, int32_t *status);
+
+/* Device pointer of the output [16][256] BF16 (valid until skv_destroy;
+ * overwritten by the next skv_enqueue). */
+int skv_output_device(void *handle, void **dev_ptr);
+
+/* Reference DecodeResult.to_torch (result.py:30-38): sync + copy [16][256]. */
+int skv_read_output(void *handle, uint16_t *host_out);
+
+/* Reference debug_snapshot (api.py:127-134): sync + copy final token IDs
+ * [4 groups][4 heads][100], best first. */
+int skv_debug_ids(void *handle, uint32_t *host_out);
+
+/* Stage outputs for parity checks (sync + copy).  stage is one of SKV_STAGE_*;
+ * copies at most cap elements for one KV group, stores the element count. */
+enum {
+  SKV_STAGE_LOWER = 1,     /* uint16 [4][nc] BF16 lower bounds */
+  SKV_STAGE_UPPER = 2,     /* uint16 [4][nc] BF16 upper bounds */
+  SKV_STAGE_THRESH = 3,    /* uint32 [4] ordered-BF16 thresholds */
+  SKV_STAGE_MASKS = 4,     /* uint8  [nc] survivor head masks */
+  SKV_STAGE_FINE = 5,      /* uint16 [4][nc] BF16 fine scores (0xffff if not scored) */
+  SKV_STAGE_SELECTED = 6,  /* int32  [count] selected clusters, ascending */
+  SKV_STAGE_POOL = 7,      /* int32  [count] pool tokens, encounter order */
+  SKV_STAGE_S2 = 8,        /* uint16 [4][count] BF16 2-bit scores of the pool */
+  SKV_STAGE_U1 = 9,        /* int32  [count] union of top-1600, pool order */
+  SKV_STAGE_S4 = 10,       /* uint16 [4][count] BF16 4-bit scores of U1 */
+  SKV_STAGE_U2 = 11,       /* int32  [count] union of top-256, U1 order */
+  SKV_STAGE_S8 = 12,       /* uint16 [4][count] BF16 8-bit scores of U2 */
+  SKV_STAGE_TOP = 13,      /* int32  [4][100] final IDs, best first */
+  SKV_STAGE_QPREP = 14,    /* int32  [4][3][260] fixed-point query operands */
+  SKV_STAGE_KEYREC = 15,   /* uint8  [T][256] key records: 2-bit prefix plane |
+                              2-bit residual plane | 4-bit residual plane */
+  SKV_STAGE_KV8 = 16,      /* uint8  [T][512] FP8 [V||K] records (group) */
+  SKV_STAGE_KSCALE = 17    /* float  [256] key codec scales (group) */
+};
+int skv_read_stage(void *handle, int stage, int group, void *host_out,
+                   int64_t cap, int64_t *count_out);
+
+/* Reference metadata (_runtime.py:197-454), as a JSON text. */
+const char *skv_metadata(void *handle);
+
+/* Releases every device buffer of the handle (reference close, api.py:136). */
+void skv_destroy(void *handle);
+
+/* Text of the last error of this handle (or of the last failed create when
+ * handle is NULL).  Valid until the next call on the handle. */
+const char *skv_last_error(void *handle);
+
+/* Library build identification. */
+const char *skv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SEOULKV4_HIP_H */

@@ -1,0 +1,251 @@
+"""ctypes binding of ``libseoulkv4_hip.so`` — the runtime seam.
+
+Replaces the reference's ``_runtime`` module (``_runtime.py:36-454``):
+``initialize`` -> :meth:`Runtime.__init__` (``skv_create``), ``bind_query``
+-> :meth:`Runtime.bind_query`, ``enqueue`` -> :meth:`Runtime.enqueue`,
+``metadata`` -> :meth:`Runtime.metadata`.  There is no fallback: if the
+library is missing or cannot load, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+from pathlib import Path
+
+import numpy as np
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libseoulkv4_hip.so")
+HEADER = Path(__file__).resolve().parents[1] / "include" / "seoulkv4_hip.h"
+
+G, H, D, TOPK = 4, 4, 256, 100
+
+STAGES = {
+    "lower": 1, "upper": 2, "thresh": 3, "masks": 4, "fine": 5, "selected": 6,
+    "pool": 7, "s2": 8, "u1": 9, "s4": 10, "u2": 11, "s8": 12, "top": 13,
+    "qprep": 14, "keyrec": 15, "kv8": 16, "kscale": 17,
+}
+STATUS_FIELDS = ("pool", "err", "selected", "survivors", "u1", "u2", "scanned", "reserved")
+ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "out of device memory",
+          4: "pool above capacity", 5: "pool below minimum", 6: "invalid state"}
+
+
+class CellDesc(ctypes.Structure):
+    _fields_ = [
+        ("upper", ctypes.c_void_p),
+        ("lower", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("resid_f16", ctypes.c_void_p),
+        ("gfs_f16", ctypes.c_void_p),
+        ("offsets", ctypes.c_void_p),
+        ("values", ctypes.c_void_p),
+        ("nprobe", ctypes.c_int32),
+        ("lam", ctypes.c_float),
+    ]
+
+
+class IndexDesc(ctypes.Structure):
+    _fields_ = [
+        ("context", ctypes.c_int32),
+        ("sink", ctypes.c_int32),
+        ("local", ctypes.c_int32),
+        ("n_centroids", ctypes.c_int32),
+        ("pool_min", ctypes.c_int32),
+        ("pool_capacity", ctypes.c_int32),
+        ("debug", ctypes.c_int32),
+        ("cells", CellDesc * G),
+    ]
+
+
+_lib = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load the HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"SeoulKV4 HIP library missing at {LIB_PATH}; build it with "
+            "`python -m seoulkv_amd.build` (gfx950)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    sig = {
+        "skv_create": (i32, [ctypes.POINTER(IndexDesc), vp, vp, i32, vp, ctypes.POINTER(vp)]),
+        "skv_bind_query": (i32, [vp, vp]),
+        "skv_bind_query_device": (i32, [vp, vp]),
+        "skv_enqueue": (i32, [vp]),
+        "skv_sync": (i32, [vp, vp]),
+        "skv_output_device": (i32, [vp, ctypes.POINTER(vp)]),
+        "skv_read_output": (i32, [vp, vp]),
+        "skv_debug_ids": (i32, [vp, vp]),
+        "skv_read_stage": (i32, [vp, i32, i32, vp, i64, ctypes.POINTER(i64)]),
+        "skv_metadata": (ctypes.c_char_p, [vp]),
+        "skv_destroy": (None, [vp]),
+        "skv_last_error": (ctypes.c_char_p, [vp]),
+        "skv_version": (ctypes.c_char_p, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared by ``include/seoulkv4_hip.h``."""
+    import re
+
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(skv_[a-z_]+)\s*\(", text)))
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _np(t: torch.Tensor, dtype) -> np.ndarray:
+    t = t.contiguous().cpu()
+    if t.dtype == torch.bfloat16:
+        t = t.view(torch.int16)  # numpy has no BF16; keep the raw bits
+    return np.ascontiguousarray(t.numpy()).view(dtype)
+
+
+class Runtime:
+    """One device instance of the decode path (the reference's ``state``)."""
+
+    def __init__(self, device: int, k: torch.Tensor, v: torch.Tensor, index, *,
+                 pool_min: int, pool_capacity: int | None, debug: bool, stream=None):
+        self.lib = load_library()
+        cells = index.cells
+        zones = index.zones
+        keep = []  # numpy arrays must outlive skv_create
+        desc = IndexDesc()
+        desc.context = zones.context
+        desc.sink = zones.sink
+        desc.local = zones.local
+        desc.n_centroids = len(cells[0]["centroids"])
+        desc.pool_min = int(pool_min)
+        desc.pool_capacity = int(pool_capacity or 0)
+        desc.debug = int(bool(debug))
+        for g, cell in enumerate(cells):
+            arrays = dict(
+                upper=_np(cell["upper"], np.uint8),
+                lower=_np(cell["lower"], np.uint8),
+                scale=_np(cell["scale"].float(), np.float32),
+                resid_f16=_np(cell["coarse_residual_norm"].half(), np.uint16),
+                gfs_f16=_np(cell["group_fine_scale"].half(), np.uint16),
+                offsets=_np(cell["offsets"].int(), np.int32),
+                values=_np(cell["values"].int(), np.int32),
+            )
+            keep.append(arrays)
+            c = desc.cells[g]
+            for name, arr in arrays.items():
+                setattr(c, name, _ptr(arr))
+            c.nprobe = int(cell["p"])
+            c.lam = float(cell["lam"])
+        kb = _np(k, np.uint16)
+        vb = _np(v, np.uint16)
+        handle = ctypes.c_void_p()
+        code = self.lib.skv_create(
+            ctypes.byref(desc), _ptr(kb), _ptr(vb), int(device),
+            ctypes.c_void_p(stream or 0), ctypes.byref(handle),
+        )
+        if code != 0:
+            msg = self.lib.skv_last_error(None).decode()
+            raise RuntimeError(f"skv_create failed ({ERRORS.get(code, code)}): {msg}")
+        self.handle = handle
+        self.device = int(device)
+        self.nc = desc.n_centroids
+        self.context = desc.context
+        self.debug = bool(debug)
+        self._qbuf = np.zeros((16, D), dtype=np.uint16)
+
+    # -------------------------------------------------------------- checks
+    def _check(self, code: int, what: str) -> None:
+        if code != 0:
+            msg = self.lib.skv_last_error(self.handle).decode()
+            raise RuntimeError(f"{what} failed ({ERRORS.get(code, code)}): {msg}")
+
+    # ------------------------------------------------------------ the seam
+    def bind_query(self, q: torch.Tensor) -> None:
+        """Host Q [1, 1, 16, 256] BF16 -> device (async H2D, 8 KiB)."""
+        self._qbuf[...] = _np(q.reshape(16, D), np.uint16)
+        self._check(self.lib.skv_bind_query(self.handle, _ptr(self._qbuf)), "bind_query")
+
+    def bind_query_device(self, q_dev: torch.Tensor) -> None:
+        """Device-resident Q [16, 256] BF16 on this device."""
+        if q_dev.device.type != "cuda" or q_dev.dtype != torch.bfloat16 or q_dev.numel() != 16 * D:
+            raise ValueError("expected a device BF16 Q with 16 x 256 elements")
+        q_dev = q_dev.contiguous()
+        self._check(self.lib.skv_bind_query_device(self.handle, q_dev.data_ptr()), "bind_query")
+
+    def enqueue(self) -> None:
+        self._check(self.lib.skv_enqueue(self.handle), "enqueue")
+
+    def synchronize(self) -> dict:
+        st = np.zeros((G, 8), dtype=np.int32)
+        self._check(self.lib.skv_sync(self.handle, _ptr(st)), "synchronize")
+        return {f: st[:, i].tolist() for i, f in enumerate(STATUS_FIELDS)}
+
+    def read_output(self) -> torch.Tensor:
+        out = np.zeros((16, D), dtype=np.uint16)
+        self._check(self.lib.skv_read_output(self.handle, _ptr(out)), "read_output")
+        return torch.from_numpy(out.view(np.int16)).view(torch.bfloat16).reshape(1, 1, 16, D)
+
+    def output_device_ptr(self) -> int:
+        p = ctypes.c_void_p()
+        self._check(self.lib.skv_output_device(self.handle, ctypes.byref(p)), "output")
+        return int(p.value)
+
+    def debug_ids(self) -> torch.Tensor:
+        out = np.zeros((G, H, TOPK), dtype=np.uint32)
+        self._check(self.lib.skv_debug_ids(self.handle, _ptr(out)), "debug_ids")
+        return torch.from_numpy(out.view(np.int32).astype(np.int64))
+
+    def read_stage(self, name: str, group: int) -> np.ndarray:
+        """Copy one stage output of one KV group (for parity checks)."""
+        stage = STAGES[name]
+        nc, T = self.nc, self.context
+        caps = {
+            "lower": (H * nc, np.uint16), "upper": (H * nc, np.uint16),
+            "thresh": (H, np.uint32), "masks": (nc, np.uint8), "fine": (H * nc, np.uint16),
+            "selected": (nc, np.int32), "pool": (T, np.int32), "s2": (H * T, np.uint16),
+            "u1": (6400, np.int32), "s4": (H * 6400, np.uint16), "u2": (1024, np.int32),
+            "s8": (H * 1024, np.uint16), "top": (H * TOPK, np.int32),
+            "qprep": (3 * H * 260, np.int32), "keyrec": (T * 256, np.uint8),
+            "kv8": (T * 512, np.uint8), "kscale": (D, np.float32),
+        }
+        cap, dtype = caps[name]
+        buf = np.zeros(cap, dtype=dtype)
+        count = ctypes.c_int64()
+        self._check(
+            self.lib.skv_read_stage(self.handle, stage, group, _ptr(buf), cap, ctypes.byref(count)),
+            f"read_stage({name})",
+        )
+        n = count.value
+        if name in ("lower", "upper", "fine", "s2", "s4", "s8"):
+            return buf[: H * n].reshape(H, n)
+        if name == "top":
+            return buf[:n].reshape(H, TOPK)
+        if name == "qprep":
+            return buf.reshape(3, H, 260)
+        return buf[:n]
+
+    def metadata(self) -> dict:
+        return json.loads(self.lib.skv_metadata(self.handle).decode())
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.skv_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

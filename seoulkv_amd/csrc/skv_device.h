@@ -1,0 +1,218 @@
+// Device helpers shared by the SeoulKV4 gfx950 kernels.
+//
+// Score arithmetic (exact, order independent):
+//   a BF16 query vector x[256] is held as integers X[d] = trunc(x[d] * 2^-fx)
+//   with |X| < 2^22 (fx = exmax - 14, exmax the largest element exponent); a
+//   key score is D = sum_d X[d] * c[d] for the integer key code c, computed
+//   exactly, rounded once to FP32 (RNE) after scaling by 2^(fx + e), then the
+//   stage's FP32 operations (RNE, no contraction), then BF16 (RNE).
+//   X is split into three signed 8-bit limbs so the dot runs on the int8
+//   matrix cores: D = L0 + 256 L1 + 65536 L2, each limb dot exact in int32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace skv {
+
+constexpr int G = 4;          // KV heads (index cells)
+constexpr int H = 4;          // query heads per KV head
+constexpr int D = 256;        // head dimension
+constexpr int TOPK = 100;
+constexpr int M15 = 1600;     // ranks of the Stage-1.5 frontier entering the union
+constexpr int M16 = 256;      // Stage-1.6 survivors per head
+constexpr int U1_MAX = H * M15;
+constexpr int U2_MAX = H * M16;
+constexpr int FX_HEADROOM = 14;
+constexpr int WAVE = 64;
+
+// Query operand variants.
+enum { QV_RAW = 0, QV_Q15 = 1, QV_QS = 2, QV_COUNT = 3 };
+
+// Per (group, variant) query operand block, written by the query-prep kernel.
+struct QOperand {
+  // int8 MFMA B image: [chunk kc][lane][16 bytes]; lane l holds column l%16
+  // (head (l%16)/4, limb (l%16)%4, limb 3 = 0) for dims
+  // (l/16)*64 + kc*16 + [0,16).
+  uint32_t bimg[4][WAVE][4];
+  int64_t sum[H];   // S_h = sum_d X_h[d]
+  int32_t fx[H];    // scale exponent of X_h
+  float norm[H];    // ||q_h|| * lambda (RAW variant only)
+  int32_t X[H][D];  // the fixed-point integers (diagnostics / tests)
+};
+
+__host__ __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__host__ __device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+__device__ __forceinline__ uint32_t ordered16(uint32_t b) {
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b ^ 0x8000u);
+}
+
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// RNE_f32(Dv * 2^e) for |Dv| < 2^53.
+__device__ __forceinline__ float scaled_f32(int64_t Dv, int e) {
+  return __double2float_rn(ldexp((double)Dv, e));
+}
+
+// RNE_f32(sqrt(N) * 2^fx) by integer arithmetic: the root of N << 2k
+// (largest k keeping it below 2^62) carries >= 26 significant bits, a sticky
+// bit records an inexact root, and 24 bits are kept with round-half-even.
+__host__ __device__ inline float sqrt_rne_scaled(unsigned long long N, int fx) {
+  if (N == 0) return 0.f;
+  int bits = 0;
+  for (unsigned long long t = N; t; t >>= 1) ++bits;
+  const int k = (62 - bits) / 2;
+  const unsigned long long M = N << (2 * k);
+  unsigned long long s = (unsigned long long)sqrt((double)M);
+  while (s * s > M) --s;
+  while ((s + 1) * (s + 1) <= M) ++s;
+  const bool sticky = s * s != M;
+  int sb = 0;
+  for (unsigned long long t = s; t; t >>= 1) ++sb;
+  const int drop = sb - 24;
+  unsigned long long qv = s >> drop;
+  const unsigned long long rem = s & ((1ull << drop) - 1), half = 1ull << (drop - 1);
+  if (rem > half || (rem == half && (sticky || (qv & 1)))) ++qv;
+  return (float)ldexp((double)qv, drop - k + fx);
+}
+
+// FP8 e4m3fn (OCP: bias 7, no infinities, S.1111.111 = NaN) -> FP32, exact.
+__host__ __device__ inline float fp8_e4m3_to_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  if (e == 0) {
+    const float v = (float)m * 0.001953125f;  // m * 2^-9
+    return sign ? -v : v;
+  }
+  if (e == 15 && m == 7) return u2f(0x7fc00000u | sign);
+  return u2f(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// FP32 -> FP8 e4m3fn, round to nearest even; magnitudes above 464 (the
+// midpoint past 448) and NaN/Inf become NaN (0x7f | sign), as torch's
+// float8_e4m3fn cast does.
+__host__ __device__ inline uint32_t f32_to_fp8_e4m3(float f) {
+  uint32_t u = f2u(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  u &= 0x7fffffffu;
+  if (u > 0x7f800000u || u == 0x7f800000u) return sign | 0x7fu;
+  if (u < 0x3c800000u) {  // below 2^-6: subnormal grid of 2^-9
+    const float scaled = u2f(u) * 512.0f;  // exact
+    uint32_t m = (uint32_t)scaled;
+    const float frac = scaled - (float)m;
+    if (frac > 0.5f || (frac == 0.5f && (m & 1u))) ++m;
+    return sign | m;  // m == 8 is the smallest normal (0x08)
+  }
+  const uint32_t r = u + 0x7ffffu + ((u >> 20) & 1u);
+  const int e = (int)(r >> 23) - 127 + 7;
+  const uint32_t m = (r >> 20) & 7u;
+  if (e > 15 || (e == 15 && m == 7)) return sign | 0x7fu;
+  return sign | ((uint32_t)e << 3) | m;
+}
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+  for (int off = 1; off < WAVE; off <<= 1) {
+    int t = __shfl_up(v, off, WAVE);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = WAVE / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+  for (int off = WAVE / 2; off > 0; off >>= 1) {
+    int lo = __shfl_xor((int)(uint32_t)v, off, WAVE);
+    int hi = __shfl_xor((int)(uint32_t)((uint64_t)v >> 32), off, WAVE);
+    v += (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int off = WAVE / 2; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, WAVE));
+  return v;
+}
+
+// Exclusive block scan of one int per thread; returns the exclusive prefix
+// and stores the block total in *total.  scratch: >= blockDim/64 + 1 ints.
+__device__ __forceinline__ int block_excl_scan(int v, int* scratch, int* total) {
+  const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+  const int nw = (blockDim.x + WAVE - 1) / WAVE;
+  int inc = wave_incl_scan(v);
+  if (lane == WAVE - 1) scratch[wave] = inc;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < nw ? scratch[lane] : 0;
+    int winc = wave_incl_scan(w);
+    if (lane < nw) scratch[lane] = winc - w;
+    if (lane == nw - 1) scratch[nw] = winc;
+  }
+  __syncthreads();
+  int res = inc - v + scratch[wave];
+  *total = scratch[nw];
+  __syncthreads();
+  return res;
+}
+
+// ------------------------------------------------------- code expansion
+// Spread the four 2-bit codes of byte t into four bytes (values 0..3).
+__device__ __forceinline__ uint32_t spread2(uint32_t t) {
+  return (t | (t << 6) | (t << 12) | (t << 18)) & 0x03030303u;
+}
+// 16 little-endian 2-bit codes of w -> 4 words of 4 byte-codes each.
+__device__ __forceinline__ void expand2(uint32_t w, uint32_t out[4]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) out[m] = spread2((w >> (8 * m)) & 0xffu);
+}
+// 8 little-endian 4-bit codes of w -> 2 words of 4 byte-codes each.
+__device__ __forceinline__ void expand4(uint32_t w, uint32_t out[2]) {
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    uint32_t v = (w >> (16 * m)) & 0xffffu;
+    uint32_t x = v & 0x0f0fu;          // nibbles 0, 2
+    uint32_t y = (v >> 4) & 0x0f0fu;   // nibbles 1, 3
+    out[m] = (x & 0xffu) | ((y & 0xffu) << 8) | ((x >> 8) << 16) | ((y >> 8) << 24);
+  }
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// One 16-key x 16-column x 64-dim int8 matrix-core step.
+__device__ __forceinline__ v4i mfma_i8(const uint32_t a[4], const uint32_t b[4], v4i c) {
+  v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
+  v4i bv = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
+}
+
+// Reduce the limb columns of an MFMA accumulator to one exact dot per
+// (key, head).  Lane l holds rows 4*(l/16)+r, column l%16 = 4*head + limb.
+// After the call, lanes with (l % 4) == 0 hold in out[r] the sum
+// L0 + 256 L1 + 65536 L2 for head (l%16)/4 and key row 4*(l/16) + r.
+__device__ __forceinline__ void combine_limbs(v4i acc, int64_t out[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    int v0 = acc[r];
+    int v1 = __shfl_down(v0, 1, WAVE);
+    int v2 = __shfl_down(v0, 2, WAVE);
+    out[r] = (int64_t)v0 + ((int64_t)v1 << 8) + ((int64_t)v2 << 16);
+  }
+}
+
+}  // namespace skv

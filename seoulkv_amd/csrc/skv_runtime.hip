@@ -1,0 +1,627 @@
+// C ABI of the SeoulKV4 MI355X decode path (see include/seoulkv4_hip.h).
+//
+// skv_create is the reference's _runtime.initialize (_runtime.py:36-177): it
+// uploads the index once, derives the spill-2 mate table (reference
+// posting_mates, _kernels/common/seoulkv4_cluster_blocks.py:10-32), and runs
+// the prefill kernels on the device:
+//   * key codec (reference _codecs/keys.py:16-26): per-coordinate max-abs
+//     scale over all tokens, code8 = clamp(floor((k + s) / (2 s / 256)), 0, 255);
+//   * token-major key records [T][256 B] = 2-bit prefix plane | 2-bit
+//     residual plane | 4-bit residual plane (the three planes of
+//     _codecs/keys.py:29-44, contiguous per token so Stage 1.6 reads one 128 B
+//     line and Stage II the next);
+//   * cluster-block prefixes [postings][64 B]: the prefix plane copied in CSR
+//     order (reference pack_cluster_blocks, seoulkv4_cluster_blocks.py:55-104)
+//     so Stage 1.5 reads each selected cluster contiguously;
+//   * FP8 e4m3fn [V || K] records [T][512 B] (reference _runtime.py:76-92).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/seoulkv4_hip.h"
+#include "skv_device.h"
+#include "skv_step.h"
+
+using namespace skv;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+struct Arena {
+  char* base = nullptr;
+  size_t size = 0, used = 0;
+  void* take(size_t bytes) {
+    size_t at = (used + 255) & ~size_t(255);
+    used = at + bytes;
+    return base + at;
+  }
+};
+
+struct Handle {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  hipEvent_t q_copied = nullptr;
+  uint16_t* q_host = nullptr;  // pinned staging for bind_query
+  void* static_mem = nullptr;
+  void* work_mem = nullptr;
+  size_t static_bytes = 0, work_bytes = 0;
+  StepArgs a{};
+  StepWork w{};
+  uint64_t* bm_u1 = nullptr;
+  uint64_t* bm_u2 = nullptr;
+  bool bound = false, ran = false;
+  std::string error, meta;
+};
+
+int fail(Handle* h, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (h) h->error = buf; else g_create_error = buf;
+  return code;
+}
+
+#define HIPCHK(h, call)                                                          \
+  do {                                                                           \
+    hipError_t e_ = (call);                                                      \
+    if (e_ != hipSuccess)                                                        \
+      return fail((h), SKV_EHIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+// ------------------------------------------------------------- prefill kernels
+__global__ void k_init_kscale(const uint16_t* k, int T, uint32_t* bits) {
+  const int g = blockIdx.y, d = threadIdx.x;
+  uint32_t m = 0;
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
+    const uint32_t b = k[((size_t)g * T + t) * D + d] & 0x7fffu;  // |k| as bf16
+    m = max(m, b);
+  }
+  atomicMax(&bits[g * D + d], m << 16);  // positive floats order as integers
+}
+
+__global__ void k_init_kscale_final(const uint32_t* bits, float* kscale) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < G * D) kscale[i] = fmaxf(__uint_as_float(bits[i]), 1e-9f);
+}
+
+__device__ __forceinline__ uint32_t key_code8(float kf, float s) {
+  const float step8 = __fmul_rn(2.0f, s) * 0.00390625f;  // (2 s) / 256, exact
+  const float c = floorf(__fdiv_rn(__fadd_rn(kf, s), step8));
+  return (uint32_t)fminf(fmaxf(c, 0.0f), 255.0f);
+}
+
+// One thread per (group, token, 4-dim byte): writes byte b of the prefix and
+// residual-2 planes and bytes 2b, 2b+1 of the residual-4 plane.
+__global__ void k_init_keyrec(const uint16_t* k, const float* kscale, int T, uint8_t* keyrec) {
+  const size_t n = (size_t)G * T * 64;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int b = (int)(i & 63);
+    const size_t gt = i >> 6;
+    const int g = (int)(gt / T);
+    const uint16_t* row = k + gt * D;
+    uint32_t c[4];
+    for (int j = 0; j < 4; ++j) {
+      const int d = 4 * b + j;
+      c[j] = key_code8(bf16_f32(row[d]), kscale[g * D + d]);
+    }
+    uint8_t* rec = keyrec + gt * 256;
+    uint32_t p2 = 0, r2 = 0;
+    for (int j = 0; j < 4; ++j) {
+      p2 |= ((c[j] >> 6) & 3u) << (2 * j);
+      r2 |= ((c[j] >> 4) & 3u) << (2 * j);
+    }
+    rec[b] = (uint8_t)p2;
+    rec[64 + b] = (uint8_t)r2;
+    rec[128 + 2 * b] = (uint8_t)((c[0] & 15u) | ((c[1] & 15u) << 4));
+    rec[128 + 2 * b + 1] = (uint8_t)((c[2] & 15u) | ((c[3] & 15u) << 4));
+  }
+}
+
+// FP8 [V || K] records: one thread per (group, token, dim).
+__global__ void k_init_kv8(const uint16_t* k, const uint16_t* v, int T, uint8_t* kv8) {
+  const size_t n = (size_t)G * T * D;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t gt = i / D;
+    const int d = (int)(i % D);
+    kv8[gt * 512 + d] = (uint8_t)f32_to_fp8_e4m3(bf16_f32(v[i]));
+    kv8[gt * 512 + 256 + d] = (uint8_t)f32_to_fp8_e4m3(bf16_f32(k[i]));
+  }
+}
+
+// Cluster-block prefix rows: post_p2[g][j] = prefix plane of token values[j].
+__global__ void k_init_postp2(const int* post_tok, const uint8_t* keyrec, int T, int np_max,
+                              const int* np_count, uint8_t* post_p2) {
+  const size_t n = (size_t)G * np_max * 4;  // 16 B chunks
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int part = (int)(i & 3);
+    const size_t gj = i >> 2;
+    const int g = (int)(gj / np_max), j = (int)(gj % np_max);
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (j < np_count[g]) {
+      const int t = post_tok[gj];
+      val = *reinterpret_cast<const uint4*>(keyrec + ((size_t)g * T + t) * 256 + part * 16);
+    }
+    *reinterpret_cast<uint4*>(post_p2 + gj * 64 + part * 16) = val;
+  }
+}
+
+// IEEE half -> float on the host (exact).
+float half_bits_to_float(uint16_t b) {
+  const uint32_t sign = (uint32_t)(b & 0x8000u) << 16;
+  const uint32_t e = (b >> 10) & 31u, m = b & 1023u;
+  uint32_t u;
+  if (e == 0) {
+    if (m == 0) {
+      u = sign;
+    } else {  // subnormal: m * 2^-24
+      float v = (float)m * 5.9604644775390625e-08f;
+      memcpy(&u, &v, 4);
+      u |= sign;
+    }
+  } else if (e == 31) {
+    u = sign | 0x7f800000u | (m << 13);
+  } else {
+    u = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+std::string json_escape(const std::string& s) {
+  std::string o;
+  for (char c : s) {
+    if (c == '"' || c == '\\') o += '\\';
+    o += c;
+  }
+  return o;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* skv_version(void) { return "seoulkv4-hip gfx950 1"; }
+
+const char* skv_last_error(void* handle) {
+  if (!handle) return g_create_error.c_str();
+  return static_cast<Handle*>(handle)->error.c_str();
+}
+
+void skv_destroy(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return;
+  if (h->stream) (void)hipStreamSynchronize(h->stream);
+  if (h->q_copied) (void)hipEventDestroy(h->q_copied);
+  if (h->q_host) (void)hipHostFree(h->q_host);
+  if (h->static_mem) (void)hipFree(h->static_mem);
+  if (h->work_mem) (void)hipFree(h->work_mem);
+  if (h->own_stream && h->stream) (void)hipStreamDestroy(h->stream);
+  delete h;
+}
+
+int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
+               int device, void* stream, void** handle_out) {
+  if (!handle_out) return fail(nullptr, SKV_EINVAL, "handle_out is NULL");
+  *handle_out = nullptr;
+  if (!ix || !k_bf16 || !v_bf16) return fail(nullptr, SKV_EINVAL, "NULL index or K/V");
+  const int T = ix->context, nc = ix->n_centroids;
+  if (T <= 0 || T > (1 << 20)) return fail(nullptr, SKV_EINVAL, "context %d outside (0, 2^20]", T);
+  if (nc <= 0 || nc % 32 || nc > 65536)
+    return fail(nullptr, SKV_EINVAL, "n_centroids %d must be a multiple of 32 in [32, 65536]", nc);
+  if (ix->sink < 0 || ix->local < 0 || ix->sink + ix->local >= T)
+    return fail(nullptr, SKV_EINVAL, "sink/local %d/%d do not fit context %d", ix->sink, ix->local, T);
+  const int R = T - ix->sink - ix->local;
+
+  // ---- host-side validation and the spill-2 mate table
+  std::vector<std::vector<int>> mates(G);
+  std::vector<int> np(G);
+  int np_max = 1;
+  for (int g = 0; g < G; ++g) {
+    const skv_cell_desc& c = ix->cells[g];
+    if (!c.upper || !c.lower || !c.scale || !c.resid_f16 || !c.gfs_f16 || !c.offsets || !c.values)
+      return fail(nullptr, SKV_EINVAL, "cell %d has a NULL array", g);
+    if (c.nprobe < 1 || c.nprobe > nc)
+      return fail(nullptr, SKV_EINVAL, "cell %d nprobe %d outside [1, %d]", g, c.nprobe, nc);
+    if (c.offsets[0] != 0) return fail(nullptr, SKV_EINVAL, "cell %d CSR offsets[0] != 0", g);
+    for (int i = 0; i < nc; ++i)
+      if (c.offsets[i + 1] < c.offsets[i])
+        return fail(nullptr, SKV_EINVAL, "cell %d CSR offsets not monotone", g);
+    np[g] = c.offsets[nc];
+    np_max = std::max(np_max, np[g]);
+    std::vector<int> first_post(T, -1), first_cluster(T, -1), seen(T, 0);
+    std::vector<int>& m = mates[g];
+    m.assign(np[g], -1);
+    for (int cl = 0; cl < nc; ++cl)
+      for (int j = c.offsets[cl]; j < c.offsets[cl + 1]; ++j) {
+        const int t = c.values[j];
+        if (t < 0 || t >= T) return fail(nullptr, SKV_EINVAL, "cell %d invalid CSR token ID %d", g, t);
+        if (++seen[t] > 2)
+          return fail(nullptr, SKV_EINVAL, "local ownership requires at most two memberships/token");
+        if (first_post[t] < 0) {
+          first_post[t] = j;
+          first_cluster[t] = cl;
+        } else {
+          if (first_cluster[t] == cl)
+            return fail(nullptr, SKV_EINVAL, "duplicate token inside one cluster");
+          m[j] = first_cluster[t];
+          m[first_post[t]] = cl;
+        }
+      }
+  }
+
+  Handle* h = new Handle();
+  h->device = device;
+  auto bail = [&](int code) {
+    g_create_error = h->error;
+    skv_destroy(h);
+    return code;
+  };
+  if (hipSetDevice(device) != hipSuccess) {
+    fail(h, SKV_EHIP, "hipSetDevice(%d) failed", device);
+    return bail(SKV_EHIP);
+  }
+  if (stream) {
+    h->stream = static_cast<hipStream_t>(stream);
+  } else {
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+      fail(h, SKV_EHIP, "hipStreamCreate failed");
+      return bail(SKV_EHIP);
+    }
+    h->own_stream = true;
+  }
+
+  StepArgs& a = h->a;
+  a.T = T;
+  a.sink = ix->sink;
+  a.local = ix->local;
+  a.nc = nc;
+  a.np_max = np_max;
+  a.cap = std::max(R, 64);
+  a.pool_min = ix->pool_min;
+  a.pool_capacity = ix->pool_capacity;
+  a.debug = ix->debug;
+  for (int g = 0; g < G; ++g) {
+    a.P[g] = ix->cells[g].nprobe;
+    a.lam[g] = ix->cells[g].lam;
+  }
+  const int words1 = (a.cap + 63) / 64, words2 = (U1_MAX + 63) / 64;
+
+  // ---- static arena
+  Arena s;
+  auto plan_static = [&](Arena& ar) {
+    a.kscale = (float*)ar.take(G * D * 4);
+    a.cen_up = (uint8_t*)ar.take((size_t)G * nc * 64);
+    a.cen_lo = (uint8_t*)ar.take((size_t)G * nc * 64);
+    a.scale4 = (float*)ar.take((size_t)G * (nc / 32) * 4);
+    a.resid = (float*)ar.take((size_t)G * nc * 4);
+    a.gfs = (float*)ar.take((size_t)G * (nc / 32) * 4);
+    a.csr_off = (int*)ar.take((size_t)G * (nc + 1) * 4);
+    a.post_tok = (int*)ar.take((size_t)G * np_max * 4);
+    a.post_mate = (int*)ar.take((size_t)G * np_max * 4);
+    a.post_p2 = (uint8_t*)ar.take((size_t)G * np_max * 64);
+    a.keyrec = (uint8_t*)ar.take((size_t)G * T * 256);
+    a.kv8 = (uint8_t*)ar.take((size_t)G * T * 512);
+  };
+  plan_static(s);
+  h->static_bytes = s.used;
+  if (hipMalloc(&h->static_mem, s.used) != hipSuccess) {
+    fail(h, SKV_ENOMEM, "cannot allocate %zu bytes of static device memory", s.used);
+    return bail(SKV_ENOMEM);
+  }
+  s.base = (char*)h->static_mem;
+  s.used = 0;
+  plan_static(s);
+
+  // ---- workspace arena
+  Arena wk;
+  auto plan_work = [&](Arena& ar) {
+    a.q = (uint16_t*)ar.take(16 * D * 2);
+    a.qop = (QOperand*)ar.take(sizeof(QOperand) * G * QV_COUNT);
+    a.lower = (uint16_t*)ar.take((size_t)G * H * nc * 2);
+    a.upper = (uint16_t*)ar.take((size_t)G * H * nc * 2);
+    a.thr = (uint32_t*)ar.take(G * H * 4);
+    a.masks = (uint8_t*)ar.take((size_t)G * nc);
+    a.surv = (int*)ar.take((size_t)G * nc * 4);
+    a.fine_ord = (uint16_t*)ar.take((size_t)G * H * nc * 2);
+    a.fine_bits = (uint16_t*)ar.take((size_t)G * H * nc * 2);
+    a.sel = (int*)ar.take((size_t)G * nc * 4);
+    a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
+    a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
+    a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
+    a.u1_tok = (int*)ar.take((size_t)G * U1_MAX * 4);
+    a.s4 = (uint16_t*)ar.take((size_t)G * H * U1_MAX * 2);
+    a.u2_tok = (int*)ar.take((size_t)G * U2_MAX * 4);
+    a.s8 = (uint16_t*)ar.take((size_t)G * H * U2_MAX * 2);
+    a.top = (int*)ar.take(G * H * TOPK * 4);
+    a.status = (int*)ar.take(G * ST_WORDS * 4);
+    a.out = (uint16_t*)ar.take(16 * D * 2);
+    h->bm_u1 = (uint64_t*)ar.take((size_t)G * H * words1 * 8);
+    h->bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
+  };
+  plan_work(wk);
+  h->work_bytes = wk.used;
+  if (hipMalloc(&h->work_mem, wk.used) != hipSuccess) {
+    fail(h, SKV_ENOMEM, "cannot allocate %zu bytes of device workspace", wk.used);
+    return bail(SKV_ENOMEM);
+  }
+  wk.base = (char*)h->work_mem;
+  wk.used = 0;
+  plan_work(wk);
+  if (hipMemsetAsync(h->work_mem, 0, h->work_bytes, h->stream) != hipSuccess) {
+    fail(h, SKV_EHIP, "workspace clear failed");
+    return bail(SKV_EHIP);
+  }
+
+  // ---- index upload
+  std::vector<float> scale4((size_t)G * (nc / 32)), resid((size_t)G * nc), gfs((size_t)G * (nc / 32));
+  std::vector<uint8_t> up((size_t)G * nc * 64), lo((size_t)G * nc * 64);
+  std::vector<int> off((size_t)G * (nc + 1)), ptok((size_t)G * np_max, 0), pmate((size_t)G * np_max, -1);
+  for (int g = 0; g < G; ++g) {
+    const skv_cell_desc& c = ix->cells[g];
+    memcpy(&up[(size_t)g * nc * 64], c.upper, (size_t)nc * 64);
+    memcpy(&lo[(size_t)g * nc * 64], c.lower, (size_t)nc * 64);
+    for (int i = 0; i < nc; ++i) {
+      // bf16(fp16 residual norm) as fp32, like the reference's .bfloat16()
+      const float rf = half_bits_to_float(c.resid_f16[i]);
+      uint32_t u;
+      memcpy(&u, &rf, 4);
+      u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+      memcpy(&resid[(size_t)g * nc + i], &u, 4);
+    }
+    for (int i = 0; i < nc / 32; ++i) {
+      const float s0 = c.scale[i * 32];
+      for (int j = 1; j < 32; ++j)
+        if (c.scale[i * 32 + j] != s0) {
+          fail(h, SKV_EINVAL, "cell %d scale is not shared within 32-centroid group %d", g, i);
+          return bail(SKV_EINVAL);
+        }
+      scale4[(size_t)g * (nc / 32) + i] = s0 / 4.0f;
+      gfs[(size_t)g * (nc / 32) + i] = half_bits_to_float(c.gfs_f16[i]);
+    }
+    memcpy(&off[(size_t)g * (nc + 1)], c.offsets, (size_t)(nc + 1) * 4);
+    memcpy(&ptok[(size_t)g * np_max], c.values, (size_t)np[g] * 4);
+    memcpy(&pmate[(size_t)g * np_max], mates[g].data(), (size_t)np[g] * 4);
+  }
+  auto up_copy = [&](const void* dst, const void* src, size_t bytes) {
+    return hipMemcpy(const_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice);
+  };
+  if (up_copy(a.cen_up, up.data(), up.size()) || up_copy(a.cen_lo, lo.data(), lo.size()) ||
+      up_copy(a.scale4, scale4.data(), scale4.size() * 4) ||
+      up_copy(a.resid, resid.data(), resid.size() * 4) ||
+      up_copy(a.gfs, gfs.data(), gfs.size() * 4) ||
+      up_copy(a.csr_off, off.data(), off.size() * 4) ||
+      up_copy(a.post_tok, ptok.data(), ptok.size() * 4) ||
+      up_copy(a.post_mate, pmate.data(), pmate.size() * 4)) {
+    fail(h, SKV_EHIP, "index upload failed");
+    return bail(SKV_EHIP);
+  }
+
+  // ---- prefill: key codec, key records, cluster-block prefixes, FP8 records
+  {
+    const size_t kv_bytes = (size_t)G * T * D * 2;
+    uint16_t *dk = nullptr, *dv = nullptr;
+    uint32_t* sbits = nullptr;
+    int* dnp = nullptr;
+    if (hipMalloc(&dk, kv_bytes) != hipSuccess || hipMalloc(&dv, kv_bytes) != hipSuccess ||
+        hipMalloc(&sbits, G * D * 4) != hipSuccess || hipMalloc(&dnp, G * 4) != hipSuccess) {
+      (void)hipFree(dk); (void)hipFree(dv); (void)hipFree(sbits); (void)hipFree(dnp);
+      fail(h, SKV_ENOMEM, "cannot allocate prefill staging (%zu bytes)", 2 * kv_bytes);
+      return bail(SKV_ENOMEM);
+    }
+    bool ok = hipMemcpy(dk, k_bf16, kv_bytes, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(dv, v_bf16, kv_bytes, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(dnp, np.data(), G * 4, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemset(sbits, 0, G * D * 4) == hipSuccess;
+    if (ok) {
+      hipLaunchKernelGGL(k_init_kscale, dim3(std::min(T, 4096), G), dim3(D), 0, h->stream, dk, T, sbits);
+      hipLaunchKernelGGL(k_init_kscale_final, dim3((G * D + 255) / 256), dim3(256), 0, h->stream,
+                         sbits, (float*)a.kscale);
+      hipLaunchKernelGGL(k_init_keyrec, dim3(8192), dim3(256), 0, h->stream, dk, a.kscale, T,
+                         (uint8_t*)a.keyrec);
+      hipLaunchKernelGGL(k_init_kv8, dim3(8192), dim3(256), 0, h->stream, dk, dv, T, (uint8_t*)a.kv8);
+      hipLaunchKernelGGL(k_init_postp2, dim3(4096), dim3(256), 0, h->stream, a.post_tok, a.keyrec, T,
+                         np_max, dnp, (uint8_t*)a.post_p2);
+      ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(h->stream) == hipSuccess;
+    }
+    (void)hipFree(dk); (void)hipFree(dv); (void)hipFree(sbits); (void)hipFree(dnp);
+    if (!ok) {
+      fail(h, SKV_EHIP, "prefill kernels failed");
+      return bail(SKV_EHIP);
+    }
+  }
+
+  // ---- step plumbing
+  StepWork& w = h->w;
+  w.score_blocks = std::max(1, std::min((a.cap + 63) / 64, 512));
+  w.top_u1 = TopkArgs{a.s2, a.pool_tok, a.cap, M15, h->bm_u1, words1, a.status, ST_POOL};
+  w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, h->bm_u2, words2, a.status, ST_U1};
+  w.union_u1 = UnionArgs{h->bm_u1, words1, a.pool_tok, a.cap, a.u1_tok, U1_MAX, a.status, ST_POOL, ST_U1};
+  w.union_u2 = UnionArgs{h->bm_u2, words2, a.u1_tok, U1_MAX, a.u2_tok, U2_MAX, a.status, ST_U1, ST_U2};
+
+  if (hipHostMalloc((void**)&h->q_host, 16 * D * 2, hipHostMallocDefault) != hipSuccess ||
+      hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess) {
+    fail(h, SKV_EHIP, "pinned query staging failed");
+    return bail(SKV_EHIP);
+  }
+
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) memset(&prop, 0, sizeof prop);
+  char buf[1024];
+  snprintf(buf, sizeof buf,
+           "{\"device\": \"%s\", \"arch\": \"%s\", \"context\": %d, \"sink\": %d, \"local\": %d, "
+           "\"n_centroids\": %d, \"nprobe\": [%d, %d, %d, %d], \"pool_buffer\": %d, "
+           "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
+           "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
+           "\"kernels_per_step\": 15}",
+           json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), T, a.sink, a.local,
+           nc, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min, a.pool_capacity, np_max,
+           h->static_bytes, h->work_bytes);
+  h->meta = buf;
+  *handle_out = h;
+  return SKV_OK;
+}
+
+int skv_bind_query(void* handle, const uint16_t* q) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  if (!q) return fail(h, SKV_EINVAL, "NULL query");
+  HIPCHK(h, hipEventSynchronize(h->q_copied));  // previous upload has left the staging buffer
+  memcpy(h->q_host, q, 16 * D * 2);
+  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, h->q_host, 16 * D * 2, hipMemcpyHostToDevice, h->stream));
+  HIPCHK(h, hipEventRecord(h->q_copied, h->stream));
+  h->bound = true;
+  return SKV_OK;
+}
+
+int skv_bind_query_device(void* handle, const void* q_dev) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  if (!q_dev) return fail(h, SKV_EINVAL, "NULL device query");
+  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, q_dev, 16 * D * 2, hipMemcpyDeviceToDevice, h->stream));
+  h->bound = true;
+  return SKV_OK;
+}
+
+int skv_enqueue(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  if (!h->bound) return fail(h, SKV_ESTATE, "bind a query before enqueue");
+  HIPCHK(h, hipSetDevice(h->device));
+  launch_step(h->a, h->w, h->stream);
+  HIPCHK(h, hipGetLastError());
+  h->ran = true;
+  return SKV_OK;
+}
+
+int skv_sync(void* handle, int32_t* status) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  if (status) HIPCHK(h, hipMemcpy(status, h->a.status, G * ST_WORDS * 4, hipMemcpyDeviceToHost));
+  return SKV_OK;
+}
+
+int skv_output_device(void* handle, void** dev_ptr) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !dev_ptr) return SKV_EINVAL;
+  *dev_ptr = h->a.out;
+  return SKV_OK;
+}
+
+int skv_read_output(void* handle, uint16_t* host_out) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_out) return SKV_EINVAL;
+  if (!h->ran) return fail(h, SKV_ESTATE, "no decode step has run");
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  HIPCHK(h, hipMemcpy(host_out, h->a.out, 16 * D * 2, hipMemcpyDeviceToHost));
+  return SKV_OK;
+}
+
+int skv_debug_ids(void* handle, uint32_t* host_out) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_out) return SKV_EINVAL;
+  if (!h->ran) return fail(h, SKV_ESTATE, "no decode step has run");
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  HIPCHK(h, hipMemcpy(host_out, h->a.top, G * H * TOPK * 4, hipMemcpyDeviceToHost));
+  return SKV_OK;
+}
+
+int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t cap,
+                   int64_t* count_out) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_out || group < 0 || group >= G || cap < 0) return SKV_EINVAL;
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  const StepArgs& a = h->a;
+  int st[ST_WORDS];
+  HIPCHK(h, hipMemcpy(st, a.status + group * ST_WORDS, sizeof st, hipMemcpyDeviceToHost));
+  const int nc = a.nc;
+  auto copy_rows = [&](const void* base, size_t row_stride, size_t elem, int64_t n, int rows) -> int {
+    if ((int64_t)rows * n > cap) return fail(h, SKV_EINVAL, "stage buffer too small");
+    for (int r = 0; r < rows; ++r) {
+      hipError_t e = hipMemcpy((char*)host_out + (size_t)r * n * elem,
+                               (const char*)base + r * row_stride * elem, (size_t)n * elem,
+                               hipMemcpyDeviceToHost);
+      if (e != hipSuccess) return fail(h, SKV_EHIP, "stage copy failed: %s", hipGetErrorString(e));
+    }
+    if (count_out) *count_out = n;
+    return SKV_OK;
+  };
+  switch (stage) {
+    case SKV_STAGE_LOWER:
+      return copy_rows(a.lower + (size_t)group * H * nc, nc, 2, nc, H);
+    case SKV_STAGE_UPPER:
+      return copy_rows(a.upper + (size_t)group * H * nc, nc, 2, nc, H);
+    case SKV_STAGE_THRESH:
+      return copy_rows(a.thr + group * H, 0, 4, H, 1);
+    case SKV_STAGE_MASKS:
+      return copy_rows(a.masks + (size_t)group * nc, 0, 1, nc, 1);
+    case SKV_STAGE_FINE:
+      if (!a.debug) return fail(h, SKV_ESTATE, "fine scores need debug=1");
+      return copy_rows(a.fine_bits + (size_t)group * H * nc, nc, 2, nc, H);
+    case SKV_STAGE_SELECTED:
+      return copy_rows(a.sel + (size_t)group * nc, 0, 4, st[ST_SEL], 1);
+    case SKV_STAGE_POOL:
+      return copy_rows(a.pool_tok + (size_t)group * a.cap, 0, 4, st[ST_POOL], 1);
+    case SKV_STAGE_S2:
+      return copy_rows(a.s2 + (size_t)group * H * a.cap, a.cap, 2, st[ST_POOL], H);
+    case SKV_STAGE_U1:
+      return copy_rows(a.u1_tok + (size_t)group * U1_MAX, 0, 4, st[ST_U1], 1);
+    case SKV_STAGE_S4:
+      return copy_rows(a.s4 + (size_t)group * H * U1_MAX, U1_MAX, 2, st[ST_U1], H);
+    case SKV_STAGE_U2:
+      return copy_rows(a.u2_tok + (size_t)group * U2_MAX, 0, 4, st[ST_U2], 1);
+    case SKV_STAGE_S8:
+      return copy_rows(a.s8 + (size_t)group * H * U2_MAX, U2_MAX, 2, st[ST_U2], H);
+    case SKV_STAGE_TOP:
+      return copy_rows(a.top + group * H * TOPK, 0, 4, H * TOPK, 1);
+    case SKV_STAGE_QPREP: {
+      // [variant][head][X[256], fx, S lo, S hi, norm bits]
+      if (cap < QV_COUNT * H * 260) return fail(h, SKV_EINVAL, "stage buffer too small");
+      std::vector<QOperand> q(QV_COUNT);
+      HIPCHK(h, hipMemcpy(q.data(), a.qop + group * QV_COUNT, sizeof(QOperand) * QV_COUNT,
+                          hipMemcpyDeviceToHost));
+      int32_t* o = (int32_t*)host_out;
+      for (int v = 0; v < QV_COUNT; ++v)
+        for (int hh = 0; hh < H; ++hh) {
+          int32_t* r = o + (v * H + hh) * 260;
+          memcpy(r, q[v].X[hh], D * 4);
+          r[256] = q[v].fx[hh];
+          r[257] = (int32_t)(uint32_t)((uint64_t)q[v].sum[hh] & 0xffffffffu);
+          r[258] = (int32_t)(uint32_t)((uint64_t)q[v].sum[hh] >> 32);
+          memcpy(&r[259], &q[v].norm[hh], 4);
+        }
+      if (count_out) *count_out = QV_COUNT * H * 260;
+      return SKV_OK;
+    }
+    case SKV_STAGE_KEYREC: {
+      if (cap < (int64_t)a.T * 256) return fail(h, SKV_EINVAL, "stage buffer too small");
+      return copy_rows(a.keyrec + (size_t)group * a.T * 256, 0, 1, (int64_t)a.T * 256, 1);
+    }
+    case SKV_STAGE_KV8:
+      return copy_rows(a.kv8 + (size_t)group * a.T * 512, 0, 1, (int64_t)a.T * 512, 1);
+    case SKV_STAGE_KSCALE:
+      return copy_rows(a.kscale + group * D, 0, 4, D, 1);
+    default:
+      return fail(h, SKV_EINVAL, "unknown stage %d", stage);
+  }
+}
+
+const char* skv_metadata(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  return h ? h->meta.c_str() : "{}";
+}
+
+}  // extern "C"

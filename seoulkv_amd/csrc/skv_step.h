@@ -1,0 +1,114 @@
+// Argument blocks of the decode-step kernels and their reference stages.
+//
+//   kernel           reference stage (src/seoulkv4/...)
+//   k_qprep          _kernels/query_prepare/host.py:26-51 (q15, qs, ||q|| lambda)
+//   k_coarse         codegen/coarse_compute.py:61-119 (2-bit interval scores)
+//   k_thresh         _kernels/stage1_coarse/seoulkv4_coarse_select.py:297-310
+//   k_survivors      _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379
+//   k_fine           codegen/fine_postscale_codegen.py:6-71, codegen/fine.py:1848-1861
+//   k_select_pool    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73,
+//                    codegen/stage15.py:275-345 (mate-ownership dedup)
+//   k_score2         codegen/stage15.py:886-995
+//   k_topk_members   codegen/stage15.py:1027-1180 (top-2048, first 1600 used),
+//   + k_union        codegen/stage15.py:1519-1597; codegen/refinement_fusion.py:142-186
+//   k_score4         _kernels/stage16/seoulkv4_stage16_matrix.py:21-60
+//   k_score8         _kernels/stage16/seoulkv4_union_matrix.py:58-139
+//   k_top100         codegen/refinement_fusion.py:296-300,495-531
+//   k_sdpa           codegen/attention.py:35-201 (+ TTNN sparse_sdpa compute)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "skv_device.h"
+
+namespace skv {
+
+// status words per KV group
+enum {
+  ST_POOL = 0,     // pool size (clamped to the buffer)
+  ST_ERR = 1,      // 0 ok, 4 pool above capacity, 5 pool below minimum
+  ST_SEL = 2,      // selected clusters
+  ST_SURV = 3,     // coarse survivors
+  ST_U1 = 4,       // |U1|
+  ST_U2 = 5,       // |U2|
+  ST_SCANNED = 6,  // postings scanned by the pool builder
+  ST_WORDS = 8
+};
+
+struct StepArgs {
+  // shapes
+  int T, sink, local, nc, np_max, cap;
+  int P[G];
+  float lam[G];
+  int pool_min, pool_capacity, debug;
+  // static device data
+  const uint16_t* q;        // [16][256] bf16 (bound query)
+  const float* kscale;      // [G][256]
+  const uint8_t* cen_up;    // [G][nc][64]
+  const uint8_t* cen_lo;    // [G][nc][64]
+  const float* scale4;      // [G][nc/32]
+  const float* resid;       // [G][nc]
+  const float* gfs;         // [G][nc/32]
+  const int* csr_off;       // [G][nc+1]
+  const int* post_tok;      // [G][np_max]
+  const int* post_mate;     // [G][np_max] (-1: no mate)
+  const uint8_t* post_p2;   // [G][np_max][64]
+  const uint8_t* keyrec;    // [G][T][256]: p2 | r2 | r4 planes
+  const uint8_t* kv8;       // [G][T][512]: fp8 V | fp8 K
+  // per-step workspace
+  QOperand* qop;            // [G][QV_COUNT]
+  uint16_t* lower;          // [G][H][nc]
+  uint16_t* upper;          // [G][H][nc]
+  uint32_t* thr;            // [G][H]
+  uint8_t* masks;           // [G][nc]
+  int* surv;                // [G][nc]
+  uint16_t* fine_ord;       // [G][H][nc] (by survivor index)
+  uint16_t* fine_bits;      // [G][H][nc] (by centroid, debug)
+  int* sel;                 // [G][nc]
+  int* pool_tok;            // [G][cap]
+  int* pool_post;           // [G][cap]
+  uint16_t* s2;             // [G][H][cap] ordered
+  int* u1_tok;              // [G][U1_MAX]
+  uint16_t* s4;             // [G][H][U1_MAX] ordered
+  int* u2_tok;              // [G][U2_MAX]
+  uint16_t* s8;             // [G][H][U2_MAX] ordered
+  int* top;                 // [G][H][TOPK]
+  int* status;              // [G][ST_WORDS]
+  uint16_t* out;            // [16][256] bf16
+};
+
+struct TopkArgs {
+  const uint16_t* scores;   // [G][H][stride] ordered
+  const int* tokens;        // [G][stride]
+  int stride;
+  int k;
+  uint64_t* bitmap;         // [G][H][words]
+  int words;
+  int* status;
+  int count_slot;
+  __device__ const int* count_ptr(int g) const { return status + g * ST_WORDS + count_slot; }
+};
+
+struct UnionArgs {
+  const uint64_t* bitmap;   // [G][H][words]
+  int words;
+  const int* tokens_in;
+  int stride_in;
+  int* tokens_out;
+  int stride_out;
+  int* status;
+  int slot_in, slot_out;
+  __device__ const int* count_in(int g) const { return status + g * ST_WORDS + slot_in; }
+  __device__ int* count_out(int g) const { return status + g * ST_WORDS + slot_out; }
+};
+
+struct StepWork {
+  TopkArgs top_u1, top_u2;
+  UnionArgs union_u1, union_u2;
+  int score_blocks;
+};
+
+void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st);
+
+}  // namespace skv

@@ -1,0 +1,19 @@
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    config.addinivalue_line("markers", "slow: long-running (full benchmark sizes)")
+
+
+def pytest_collection_modifyitems(config, items):
+    # GPU tests need the built HIP library and a visible device; fail loudly
+    # (not skip) when the library is missing so a silent fallback is impossible.
+    pass

@@ -1,0 +1,117 @@
+"""Stage-by-stage parity of the HIP decode step against the CPU oracle.
+
+Bit-exact: key codec records, FP8 records, query operands, coarse intervals,
+thresholds, survivor masks, fine scores, selected clusters, the pool (in
+encounter order), 2/4/8-bit scores, U1, U2 and the final top-100 IDs.
+Attention output: max-abs <= 2e-2 and cosine >= 0.999 per query head against
+the oracle's float64 softmax over the same FP8 records.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import arith
+from oracle import decode as od
+from seoulkv_amd import _hip
+from tests.helpers import bits, case, cosine, oracle_inputs, oracle_step, unorder
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "t8192_clustered": dict(context=8192, components=256, nc=512, nprobe=64),
+    "t8192_iid_p128": dict(context=8192, components=1, nc=512, nprobe=128, clustered=False),
+    "t8192_p16_sink0": dict(context=8192, components=64, nc=256, nprobe=16, sink=0, local=64),
+    "t16384_nc1024_p256": dict(context=16384, components=512, nc=1024, nprobe=256, seed_shift=7),
+}
+
+
+@pytest.fixture(scope="module")
+def runtimes():
+    made = {}
+    yield made
+    for rt in made.values():
+        rt.close()
+
+
+def runtime_for(runtimes, name):
+    if name not in runtimes:
+        p = CASES[name]
+        index, k, v, _ = case(**p)
+        print(f"[gpu] create runtime {name}", flush=True)
+        runtimes[name] = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    return runtimes[name]
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_prefill_records(runtimes, name):
+    p = CASES[name]
+    rt = runtime_for(runtimes, name)
+    _, code8, scales, _, _ = oracle_inputs(**p)
+    index, k, v, _ = case(**p)
+    kb, vb = bits(k), bits(v)
+    for g in range(4):
+        np.testing.assert_array_equal(rt.read_stage("kscale", g), scales[g])
+        rec = rt.read_stage("keyrec", g).reshape(-1, 256)
+        c = code8[g].astype(np.uint32)
+        planes = torch.from_numpy(c.astype(np.uint8))
+        from seoulkv_amd._codecs import encode_planes
+
+        ref = encode_planes(planes[None])
+        np.testing.assert_array_equal(rec[:, :64], ref["prefix2"][0].numpy())
+        np.testing.assert_array_equal(rec[:, 64:128], ref["residual2"][0].numpy())
+        np.testing.assert_array_equal(rec[:, 128:], ref["residual4"][0].numpy())
+        kv8 = rt.read_stage("kv8", g).reshape(-1, 512)
+        kt = torch.from_numpy(kb[g].view(np.int16)).view(torch.bfloat16).float()
+        vt = torch.from_numpy(vb[g].view(np.int16)).view(torch.bfloat16).float()
+        np.testing.assert_array_equal(
+            kv8[:, 256:], kt.to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+        np.testing.assert_array_equal(
+            kv8[:, :256], vt.to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+
+
+@pytest.mark.parametrize("qi", [0, 1])
+@pytest.mark.parametrize("name", list(CASES))
+def test_step_parity(runtimes, name, qi):
+    p = CASES[name]
+    rt = runtime_for(runtimes, name)
+    _, _, _, qs = case(**p)
+    q = qs[qi]
+    print(f"[gpu] step {name} q{qi}", flush=True)
+    rt.bind_query(q)
+    rt.enqueue()
+    status = rt.synchronize()
+    traces, out = oracle_step(p, q)
+    for g, tr in enumerate(traces):
+        qp = tr.extra["qprep"]
+        dq = rt.read_stage("qprep", g)
+        for v, (X, fx) in enumerate([(qp.X0, qp.fx0), (qp.X15, qp.fx15), (qp.Xs, qp.fxs)]):
+            np.testing.assert_array_equal(dq[v, :, :256], X, err_msg=f"g{g} X variant {v}")
+            np.testing.assert_array_equal(dq[v, :, 256], fx, err_msg=f"g{g} fx variant {v}")
+            S = (dq[v, :, 257].astype(np.int64) & 0xFFFFFFFF) | (dq[v, :, 258].astype(np.int64) << 32)
+            np.testing.assert_array_equal(S, X.sum(-1), err_msg=f"g{g} S variant {v}")
+        np.testing.assert_array_equal(dq[0, :, 259].view(np.float32), qp.norm, err_msg=f"g{g} norm")
+        np.testing.assert_array_equal(rt.read_stage("lower", g), tr.lower, err_msg=f"g{g} lower")
+        np.testing.assert_array_equal(rt.read_stage("upper", g), tr.upper, err_msg=f"g{g} upper")
+        np.testing.assert_array_equal(rt.read_stage("thresh", g), tr.thr, err_msg=f"g{g} thr")
+        np.testing.assert_array_equal(rt.read_stage("masks", g), tr.masks, err_msg=f"g{g} masks")
+        fine = rt.read_stage("fine", g)[:, tr.survivors]
+        elig = ((tr.masks[tr.survivors][None, :] >> np.arange(4)[:, None]) & 1).astype(bool)
+        np.testing.assert_array_equal(fine[elig], tr.fine[elig], err_msg=f"g{g} fine")
+        assert (fine[~elig] == 0xFFFF).all()
+        np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected,
+                                      err_msg=f"g{g} selected")
+        np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool, err_msg=f"g{g} pool")
+        assert status["pool"][g] == len(tr.pool)
+        np.testing.assert_array_equal(unorder(rt.read_stage("s2", g)), tr.s2, err_msg=f"g{g} s2")
+        np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1, err_msg=f"g{g} u1")
+        np.testing.assert_array_equal(unorder(rt.read_stage("s4", g)), tr.s4, err_msg=f"g{g} s4")
+        np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2, err_msg=f"g{g} u2")
+        np.testing.assert_array_equal(unorder(rt.read_stage("s8", g)), tr.s8, err_msg=f"g{g} s8")
+        np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100, err_msg=f"g{g} top100")
+    got = rt.read_output().float().numpy().reshape(16, 256)
+    for j in range(16):
+        assert np.abs(got[j] - out[j]).max() <= 2e-2, f"head {j} max-abs"
+        assert cosine(got[j], out[j]) >= 0.999, f"head {j} cosine"
