@@ -126,6 +126,16 @@ enum {
 int skv_read_stage(void *handle, int stage, int group, void *host_out,
                    int64_t cap, int64_t *count_out);
 
+/* Per-kernel timing (the reference's SKV4_* device markers,
+ * codegen/profiling.py:4-64): while enabled, skv_enqueue records a HIP event
+ * before every kernel of the step on the handle's stream.  skv_profile
+ * (re)starts the accumulation; skv_profile_read syncs and returns the mean
+ * milliseconds of each kernel over the profiled steps (n >= skv_kernel_count()). */
+int skv_profile(void *handle, int enable);
+int skv_profile_read(void *handle, float *mean_ms, int n, int32_t *steps);
+int skv_kernel_count(void);
+const char *skv_kernel_name(int i);
+
 /* Reference metadata (_runtime.py:197-454), as a JSON text. */
 const char *skv_metadata(void *handle);
 

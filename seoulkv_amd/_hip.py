@@ -83,6 +83,10 @@ def load_library() -> ctypes.CDLL:
         "skv_read_output": (i32, [vp, vp]),
         "skv_debug_ids": (i32, [vp, vp]),
         "skv_read_stage": (i32, [vp, i32, i32, vp, i64, ctypes.POINTER(i64)]),
+        "skv_profile": (i32, [vp, i32]),
+        "skv_profile_read": (i32, [vp, vp, i32, vp]),
+        "skv_kernel_count": (i32, []),
+        "skv_kernel_name": (ctypes.c_char_p, [i32]),
         "skv_metadata": (ctypes.c_char_p, [vp]),
         "skv_destroy": (None, [vp]),
         "skv_last_error": (ctypes.c_char_p, [vp]),
@@ -238,6 +242,20 @@ class Runtime:
 
     def metadata(self) -> dict:
         return json.loads(self.lib.skv_metadata(self.handle).decode())
+
+    def profile(self, enable: bool) -> None:
+        """(Re)start per-kernel HIP-event timing of every enqueued step."""
+        self._check(self.lib.skv_profile(self.handle, int(enable)), "profile")
+
+    def profile_read(self) -> tuple[dict, int]:
+        """Mean milliseconds per kernel over the profiled steps."""
+        n = self.lib.skv_kernel_count()
+        ms = np.zeros(n, dtype=np.float32)
+        steps = ctypes.c_int32()
+        self._check(self.lib.skv_profile_read(self.handle, _ptr(ms), n, ctypes.byref(steps)),
+                    "profile_read")
+        names = [self.lib.skv_kernel_name(i).decode() for i in range(n)]
+        return dict(zip(names, ms.tolist())), steps.value
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -88,11 +88,16 @@ class SeoulKV4:
 
     def _initialize(self, q):
         k, v = self._host_kv
+        # Steps are enqueued on the caller's current PyTorch stream of the
+        # device when it is a created stream; on the legacy default stream
+        # the library uses a stream of its own (synchronize() orders both).
+        stream = torch.cuda.current_stream(self._device).cuda_stream
         state = _hip.Runtime(
             self._device, k, v, self._index,
             pool_min=self._args.stage15_m,
             pool_capacity=self._args.stage15_capacity,
             debug=self._args.debug,
+            stream=stream or None,
         )
         try:
             # First step is checked like the reference's initialisation

@@ -66,16 +66,14 @@ __device__ __forceinline__ float scaled_f32(int64_t Dv, int e) {
 // bit records an inexact root, and 24 bits are kept with round-half-even.
 __host__ __device__ inline float sqrt_rne_scaled(unsigned long long N, int fx) {
   if (N == 0) return 0.f;
-  int bits = 0;
-  for (unsigned long long t = N; t; t >>= 1) ++bits;
+  const int bits = 64 - __builtin_clzll(N);
   const int k = (62 - bits) / 2;
   const unsigned long long M = N << (2 * k);
   unsigned long long s = (unsigned long long)sqrt((double)M);
   while (s * s > M) --s;
   while ((s + 1) * (s + 1) <= M) ++s;
   const bool sticky = s * s != M;
-  int sb = 0;
-  for (unsigned long long t = s; t; t >>= 1) ++sb;
+  const int sb = 64 - __builtin_clzll(s);
   const int drop = sb - 24;
   unsigned long long qv = s >> drop;
   const unsigned long long rem = s & ((1ull << drop) - 1), half = 1ull << (drop - 1);

@@ -1,114 +1,132 @@
 // SeoulKV4 sparse decode step for MI355X (gfx950).
 //
-// One decode step = query prep -> coarse 2-bit centroid intervals -> per-head
-// P-th lower bound -> survivor masks -> fine 4-bit centroid scores -> per-head
-// top-P + union -> spill-2 pool (mate-ownership dedup, encounter order) ->
-// 2-bit key scores -> per-head top-1600 + union U1 -> 4-bit scores -> per-head
-// top-256 + union U2 -> 8-bit scores -> per-head top-100 -> sparse FP8 SDPA.
+// One decode step, per KV group g (4 query heads each):
+//   qprep       q, q15 = bf16(q s / 64), qs = bf16(q s / 256) -> fixed-point
+//               int8 limb images (+ ||q|| lambda); clears per-step counters
+//   coarse      2-bit centroid intervals [lower, upper] for every centroid
+//   thresh      per head: the P-th largest lower bound
+//   fine        per centroid: survivor mask (upper >= threshold) and the
+//               4-bit fine score of every eligible (centroid, head)
+//   fine_select per head: top-P eligible centroids -> selected bitmap (union)
+//   pool_count  per selected cluster: postings owned under spill-2 mate rule
+//   pool_emit   selected list + pool tokens in encounter order, fused with
+//               the 2-bit scores of the owned postings (cluster-block rows)
+//   top1600     per head: top-1600 of the pool -> membership bitmap
+//   union_u1    U1 = union over heads, pool order
+//   score4      4-bit scores of U1
+//   top256      per head: top-256 of U1 -> bitmap;  union_u2 -> U2
+//   score8      8-bit scores of U2
+//   top100      per head: best-first top-100 token IDs
+//   sdpa        FP8 sparse attention over sink + local + top-100, split into
+//               64-key slices; sdpa_merge combines the slices of each head
 // Reference stages: see the table in skv_step.h.
 //
 // Selection keys are (ordered BF16 score, lowest ID first); all score dots
 // are exact integers on the int8 matrix cores (see skv_device.h).
 
 #include "skv_device.h"
+#include "skv_select.h"
 #include "skv_step.h"
 
 namespace skv {
 
 // ============================================================ query prep
-// One block per KV group, 1024 threads: thread t owns head t/256, dim t%256.
-__global__ __launch_bounds__(1024) void k_qprep(StepArgs a) {
-  const int g = blockIdx.x;
-  const int t = threadIdx.x, h = t >> 8, d = t & 255;
-  const int lane = t & 63, wave = t >> 6;  // 4 waves per head
-  __shared__ int s_X[QV_COUNT][H][D];
-  __shared__ int s_red[16];
-  __shared__ long long s_red64[16];
+// Grid (G, QV_COUNT), 256 threads: thread d owns dim d of the 4 heads.
+__global__ __launch_bounds__(256) void k_qprep(StepArgs a) {
+  const int g = blockIdx.x, v = blockIdx.y, d = threadIdx.x;
+  const int lane = d & 63, wave = d >> 6;
+  __shared__ int s_X[H][D];
+  __shared__ int s_max[H][4];
+  __shared__ long long s_sum[H][4], s_sq[H][4];
 
-  const uint32_t qb = a.q[(g * H + h) * D + d];
-  const float qf = bf16_f32(qb);
-  const float ks = a.kscale[g * D + d];
-  const float prod = __fmul_rn(qf, ks);
-  uint32_t vb[QV_COUNT];
-  vb[QV_RAW] = qb;
-  vb[QV_Q15] = bf16_rne(__fmul_rn(prod, 0.015625f));    // q s / 64
-  vb[QV_QS] = bf16_rne(__fmul_rn(prod, 0.00390625f));   // q s / 256
-
-  for (int v = 0; v < QV_COUNT; ++v) {
-    const uint32_t b = vb[v];
+  {  // per-step counters: pool histograms, selected bitmap, SDPA tickets
+    const int blk = g * QV_COUNT + v, nblk = G * QV_COUNT;
+    for (size_t i = (size_t)blk * 256 + d; i < a.zero_words; i += (size_t)nblk * 256)
+      a.zero_base[i] = 0;
+  }
+  QOperand* out = &a.qop[g * QV_COUNT + v];
+  int X[H], ex[H], sig[H];
+  uint32_t bits[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const uint32_t qb = a.q[(g * H + h) * D + d];
+    uint32_t b = qb;
+    if (v != QV_RAW) {
+      const float prod = __fmul_rn(bf16_f32(qb), a.kscale[g * D + d]);
+      b = bf16_rne(__fmul_rn(prod, v == QV_Q15 ? 0.015625f : 0.00390625f));
+    }
+    bits[h] = b;
     const int expf = (b >> 7) & 0xff, mant = b & 0x7f;
-    const int sig = expf ? (mant | 0x80) : mant;
-    const int ex = expf ? expf - 134 : -133;
-    int m = wave_max(sig ? ex : -(1 << 20));
-    if (lane == 0) s_red[wave] = m;
-    __syncthreads();
-    int exmax = max(max(s_red[h * 4 + 0], s_red[h * 4 + 1]), max(s_red[h * 4 + 2], s_red[h * 4 + 3]));
-    __syncthreads();
-    if (exmax == -(1 << 20)) exmax = 0;
-    const int shift = ex - exmax + FX_HEADROOM;
-    int mag = shift >= 0 ? (sig << shift) : (shift <= -9 ? 0 : (sig >> -shift));
-    const int X = (b & 0x8000u) ? -mag : mag;
-    s_X[v][h][d] = X;
-    a.qop[g * QV_COUNT + v].X[h][d] = X;
-    // S_h and (RAW) the squared norm, exact in int64.
-    long long sx = wave_sum64((long long)X);
-    long long sq = wave_sum64((long long)X * X);
-    if (lane == 0) s_red64[wave] = sx;
-    __syncthreads();
-    if (d == 0) {
-      long long S = s_red64[h * 4] + s_red64[h * 4 + 1] + s_red64[h * 4 + 2] + s_red64[h * 4 + 3];
-      a.qop[g * QV_COUNT + v].sum[h] = S;
-      a.qop[g * QV_COUNT + v].fx[h] = exmax - FX_HEADROOM;
-    }
-    __syncthreads();
-    if (v == QV_RAW) {
-      if (lane == 0) s_red64[wave] = sq;
-      __syncthreads();
-      if (d == 0) {
-        unsigned long long N = (unsigned long long)(s_red64[h * 4] + s_red64[h * 4 + 1] +
-                                                    s_red64[h * 4 + 2] + s_red64[h * 4 + 3]);
-        float norm = sqrt_rne_scaled(N, exmax - FX_HEADROOM);
-        a.qop[g * QV_COUNT + QV_RAW].norm[h] = __fmul_rn(norm, a.lam[g]);
-      }
-      __syncthreads();
-    }
+    sig[h] = expf ? (mant | 0x80) : mant;
+    ex[h] = expf ? expf - 134 : -133;
+    const int m = wave_max(sig[h] ? ex[h] : -(1 << 20));
+    if (lane == 0) s_max[h][wave] = m;
   }
   __syncthreads();
-  // B images: bimg[kc][lane][m] bytes = limb (col%4) of X_{col/4}[dim],
-  // col = lane%16, dim = (lane/16)*64 + kc*16 + 4m + byte.
-  for (int w = t; w < QV_COUNT * 4 * WAVE * 4; w += blockDim.x) {
-    const int v = w / (4 * WAVE * 4);
-    const int r = w % (4 * WAVE * 4);
-    const int kc = r / (WAVE * 4), l = (r / 4) % WAVE, m = r % 4;
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    int exmax = max(max(s_max[h][0], s_max[h][1]), max(s_max[h][2], s_max[h][3]));
+    if (exmax == -(1 << 20)) exmax = 0;
+    const int shift = ex[h] - exmax + FX_HEADROOM;
+    const int mag = shift >= 0 ? (sig[h] << shift) : (shift <= -9 ? 0 : (sig[h] >> -shift));
+    X[h] = (bits[h] & 0x8000u) ? -mag : mag;
+    s_X[h][d] = X[h];
+    out->X[h][d] = X[h];
+    const long long sx = wave_sum64((long long)X[h]);
+    const long long sq = wave_sum64((long long)X[h] * X[h]);
+    if (lane == 0) {
+      s_sum[h][wave] = sx;
+      s_sq[h][wave] = sq;
+    }
+    if (d == 0) out->fx[h] = exmax - FX_HEADROOM;
+  }
+  __syncthreads();
+  if (d < H) {
+    const int h = d;
+    out->sum[h] = s_sum[h][0] + s_sum[h][1] + s_sum[h][2] + s_sum[h][3];
+    if (v == QV_RAW) {
+      const unsigned long long N =
+          (unsigned long long)(s_sq[h][0] + s_sq[h][1] + s_sq[h][2] + s_sq[h][3]);
+      out->norm[h] = __fmul_rn(sqrt_rne_scaled(N, out->fx[h]), a.lam[g]);
+    } else {
+      out->norm[h] = 0.f;
+    }
+  }
+  // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
+  // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int w = d + 256 * i;  // 0..1023
+    const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
     const int col = l & 15, hh = col >> 2, limb = col & 3;
     uint32_t word = 0;
+#pragma unroll
     for (int byte = 0; byte < 4; ++byte) {
-      const int dim = (l >> 4) * 64 + kc * 16 + 4 * m + byte;
-      const int X = s_X[v][hh][dim];
-      const int l0 = (int)(int8_t)(X & 0xff);
-      const int x1 = (X - l0) >> 8;
+      const int x = s_X[hh][(l >> 4) * 64 + kc * 16 + 4 * m + byte];
+      const int l0 = (int)(int8_t)(x & 0xff);
+      const int x1 = (x - l0) >> 8;
       const int l1 = (int)(int8_t)(x1 & 0xff);
       const int l2 = (x1 - l1) >> 8;
       const int limbv = limb == 0 ? l0 : limb == 1 ? l1 : limb == 2 ? l2 : 0;
       word |= (uint32_t)(limbv & 0xff) << (8 * byte);
     }
-    a.qop[g * QV_COUNT + v].bimg[kc][l][m] = word;
+    out->bimg[kc][l][m] = word;
   }
 }
 
-// Load the 16-register B operand of variant v for this lane.
+// Load the 16-register B operand of a query variant for this lane.
 __device__ __forceinline__ void load_b(const QOperand* q, uint32_t b[4][4]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
-    uint4 w = *reinterpret_cast<const uint4*>(&q->bimg[kc][lane][0]);
+    const uint4 w = *reinterpret_cast<const uint4*>(&q->bimg[kc][lane][0]);
     b[kc][0] = w.x; b[kc][1] = w.y; b[kc][2] = w.z; b[kc][3] = w.w;
   }
 }
 
 // ============================================================ coarse
 // Wave tile: 16 centroids x 4 heads.  lower/upper = bf16(value -/+ margin),
-// value = RNE(sum q (2u - 3) ) * scale/4, margin = ||q|| lambda bf16(resid).
+// value = RNE(sum q (2u - 3)) * scale/4, margin = ||q|| lambda bf16(resid).
 __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -119,10 +137,8 @@ __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
   uint32_t b[4][4];
   load_b(q, b);
   const int row = lane & 15, kb = lane >> 4;
-  const int c_in = tile * 16 + row;
-  uint4 w = make_uint4(0, 0, 0, 0);
-  if (c_in < nc)
-    w = *reinterpret_cast<const uint4*>(a.cen_up + ((size_t)g * nc + c_in) * 64 + kb * 16);
+  const uint4 w = *reinterpret_cast<const uint4*>(
+      a.cen_up + ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16);
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
   v4i acc = {0, 0, 0, 0};
 #pragma unroll
@@ -141,9 +157,7 @@ __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int c = tile * 16 + 4 * kb + r;
-      if (c >= nc) continue;
-      const int64_t Dv = 2 * dot[r] - 3 * S;
-      const float val = scaled_f32(Dv, fx);
+      const float val = scaled_f32(2 * dot[r] - 3 * S, fx);
       const float value = __fmul_rn(val, a.scale4[(size_t)g * (nc / 32) + c / 32]);
       const float margin = __fmul_rn(norm, a.resid[(size_t)g * nc + c]);
       const size_t o = ((size_t)g * H + h) * nc + c;
@@ -153,300 +167,364 @@ __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
   }
 }
 
-// ============================================================ selection helpers
-// Find, over values val(i) in [0, 2^bits) (given by functor), the digit path
-// of the k-th largest value counting multiplicities.  Items with
-// valid(i) == false are ignored.  Radix 8 per pass.  Returns the k-th largest
-// value and (in *above) how many valid items are strictly greater.
-template <int BITS, typename ValFn>
-__device__ uint64_t block_kth(int n, int k, ValFn val, uint32_t* hist, int* scratch,
-                              int* above_out) {
-  uint64_t prefix = 0;
-  int remaining = k, above = 0;
-  for (int shift = BITS - 8; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    const int hs = shift + 8;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      uint64_t v;
-      if (!val(i, &v)) continue;
-      if (hs < BITS && (v >> hs) != (prefix >> hs)) continue;
-      atomicAdd(&hist[(v >> shift) & 255], 1u);
-    }
-    __syncthreads();
-    // Thread 0..255: suffix counts over bins; locate the digit.
-    if (threadIdx.x < 64) {
-      // each of 64 lanes owns 4 bins (lane 0: 252..255 high end)
-      const int lane = threadIdx.x;
-      const int base = 255 - 4 * lane;  // bins base, base-1, base-2, base-3
-      int c4 = hist[base] + hist[base - 1] + hist[base - 2] + hist[base - 3];
-      int inc = wave_incl_scan(c4);
-      int exc = inc - c4;
-      // the lane whose range contains the remaining-th item
-      if (exc < remaining && remaining <= inc) {
-        int acc = exc;
-        int digit = base;
-        for (int j = 0; j < 4; ++j) {
-          int cnt = hist[base - j];
-          if (acc + cnt >= remaining) { digit = base - j; break; }
-          acc += cnt;
-        }
-        scratch[0] = digit;
-        scratch[1] = acc;  // count strictly above the digit, within prefix
-      }
-      if (lane == 63 && inc < remaining) {  // fewer than k items: take all
-        scratch[0] = -1;
-        scratch[1] = inc;
-      }
-    }
-    __syncthreads();
-    const int digit = scratch[0];
-    const int acc = scratch[1];
-    __syncthreads();
-    if (digit < 0) {  // n_valid < k within this prefix: no k-th element
-      *above_out = above + acc;
-      return 0;
-    }
-    above += acc;
-    remaining -= acc;
-    prefix |= (uint64_t)digit << shift;
-  }
-  *above_out = above;
-  return prefix;
-}
-
 // ============================================================ thresholds
-__global__ __launch_bounds__(1024) void k_thresh(StepArgs a) {
+// Per (group, head): the P-th largest lower bound (its value only).
+__global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
   const int g = blockIdx.x / H, h = blockIdx.x % H;
-  __shared__ uint32_t hist[256];
-  __shared__ int scratch[4];
+  __shared__ SelectScratch s;
+  extern __shared__ __align__(16) uint16_t so[];  // nc ordered lower bounds
   const uint16_t* lo = a.lower + ((size_t)g * H + h) * a.nc;
-  int above;
-  auto val = [&](int i, uint64_t* v) { *v = ordered16(lo[i]); return true; };
-  uint64_t kth = block_kth<16>(a.nc, a.P[g], val, hist, scratch, &above);
-  if (threadIdx.x == 0) a.thr[g * H + h] = (uint32_t)kth;
-}
-
-// ============================================================ survivors
-// Survivor c iff some head h has ordered(upper_h(c)) >= threshold_h.  The
-// list is ascending (each thread owns a contiguous centroid range).
-__global__ __launch_bounds__(1024) void k_survivors(StepArgs a) {
-  const int g = blockIdx.x, nc = a.nc;
-  __shared__ int scratch[40];
-  const int per = (nc + blockDim.x - 1) / blockDim.x;
-  const int c0 = threadIdx.x * per, c1 = min(nc, c0 + per);
-  uint32_t thr[H];
-  for (int h = 0; h < H; ++h) thr[h] = a.thr[g * H + h];
-  auto mask_of = [&](int c) {
-    uint32_t m = 0;
-    for (int h = 0; h < H; ++h)
-      m |= (uint32_t)(ordered16(a.upper[((size_t)g * H + h) * nc + c]) >= thr[h]) << h;
-    return m;
-  };
-  int cnt = 0;
-  for (int c = c0; c < c1; ++c) {
-    const uint32_t m = mask_of(c);
-    a.masks[(size_t)g * nc + c] = (uint8_t)m;
-    cnt += m != 0;
-  }
-  int total;
-  int pos = block_excl_scan(cnt, scratch, &total);
-  for (int c = c0; c < c1; ++c)
-    if (a.masks[(size_t)g * nc + c]) a.surv[(size_t)g * nc + pos++] = c;
-  if (threadIdx.x == 0) a.status[g * 8 + ST_SURV] = total;
+  // a non-NaN bound never maps to ordered 0, the "excluded" mark
+  load_lds_scores(so, lo, a.nc, [](uint32_t b) { return ordered16(b); });
+  __syncthreads();
+  const Selection sel = block_select(so, a.nc, a.P[g], [](int i) { return (uint32_t)i; }, s);
+  if (threadIdx.x == 0) a.thr[g * H + h] = sel.all ? 0u : sel.v;
 }
 
 // ============================================================ fine
-// 4-bit centroid score of survivors: bf16(RNE(sum q (2 code4 - 15)) * gfs).
-// fine_ord[g][h][i] = ordered score if survivor i is eligible for head h, else 0.
+// Every centroid: survivor mask (bit h iff ordered(upper_h) >= threshold_h)
+// and the 4-bit score bf16(RNE(sum q (2 code4 - 15)) * group_fine_scale) of
+// each eligible head.  fine_ord[g][h][c] = ordered score, or 0 if ineligible.
 __global__ __launch_bounds__(256) void k_fine(StepArgs a) {
   const int g = blockIdx.y, nc = a.nc;
   const int lane = threadIdx.x & 63;
-  const int n = a.status[g * 8 + ST_SURV];
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile * 16 >= nc) return;
   const QOperand* q = &a.qop[g * QV_COUNT + QV_RAW];
   uint32_t b[4][4];
-  bool loaded = false;
-  for (int tile = blockIdx.x * 4 + (threadIdx.x >> 6); tile * 16 < n; tile += gridDim.x * 4) {
-    if (!loaded) { load_b(q, b); loaded = true; }
-    const int row = lane & 15, kb = lane >> 4;
-    const int i_in = tile * 16 + row;
-    uint4 wu = make_uint4(0, 0, 0, 0), wl = wu;
-    if (i_in < n) {
-      const int c = a.surv[(size_t)g * nc + i_in];
-      wu = *reinterpret_cast<const uint4*>(a.cen_up + ((size_t)g * nc + c) * 64 + kb * 16);
-      wl = *reinterpret_cast<const uint4*>(a.cen_lo + ((size_t)g * nc + c) * 64 + kb * 16);
-    }
-    const uint32_t up[4] = {wu.x, wu.y, wu.z, wu.w};
-    const uint32_t lo[4] = {wl.x, wl.y, wl.z, wl.w};
-    v4i acc = {0, 0, 0, 0};
+  load_b(q, b);
+  const int row = lane & 15, kb = lane >> 4;
+  const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
+  const uint4 wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
+  const uint4 wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
+  const uint32_t up[4] = {wu.x, wu.y, wu.z, wu.w};
+  const uint32_t lo[4] = {wl.x, wl.y, wl.z, wl.w};
+  v4i acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      uint32_t eu[4], el[4], av[4];
-      expand2(up[kc], eu);
-      expand2(lo[kc], el);
+  for (int kc = 0; kc < 4; ++kc) {
+    uint32_t eu[4], el[4], av[4];
+    expand2(up[kc], eu);
+    expand2(lo[kc], el);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) av[m] = (eu[m] << 2) | el[m];
-      acc = mfma_i8(av, b[kc], acc);
-    }
-    int64_t dot[4];
-    combine_limbs(acc, dot);
+    for (int m = 0; m < 4; ++m) av[m] = (eu[m] << 2) | el[m];
+    acc = mfma_i8(av, b[kc], acc);
+  }
+  int64_t dot[4];
+  combine_limbs(acc, dot);
+  const int h = (lane & 15) >> 2;
+  const uint32_t thr = a.thr[g * H + h];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int c = tile * 16 + 4 * kb + r;
+    const bool ok = ordered16(a.upper[((size_t)g * H + h) * nc + c]) >= thr;
+    uint32_t m = (uint32_t)ok << h;  // gather the 4 heads' bits (lanes ^4, ^8)
+    m |= __shfl_xor(m, 4, WAVE);
+    m |= __shfl_xor(m, 8, WAVE);
     if ((lane & 3) == 0) {
-      const int h = (lane & 15) >> 2;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = tile * 16 + 4 * kb + r;
-        if (i >= n) continue;
-        const int c = a.surv[(size_t)g * nc + i];
-        const int64_t Dv = 2 * dot[r] - 15 * q->sum[h];
-        const float val = scaled_f32(Dv, q->fx[h]);
-        const uint32_t bits = bf16_rne(__fmul_rn(val, a.gfs[(size_t)g * (nc / 32) + c / 32]));
-        const bool ok = (a.masks[(size_t)g * nc + c] >> h) & 1;
-        a.fine_ord[((size_t)g * H + h) * nc + i] = ok ? (uint16_t)ordered16(bits) : 0;
-        if (a.debug) a.fine_bits[((size_t)g * H + h) * nc + c] = ok ? (uint16_t)bits : 0xffff;
-      }
+      const float val = scaled_f32(2 * dot[r] - 15 * q->sum[h], q->fx[h]);
+      const uint32_t bits = bf16_rne(__fmul_rn(val, a.gfs[(size_t)g * (nc / 32) + c / 32]));
+      const size_t o = ((size_t)g * H + h) * nc + c;
+      a.fine_ord[o] = ok ? (uint16_t)ordered16(bits) : 0;
+      if (a.debug) a.fine_bits[o] = ok ? (uint16_t)bits : 0xffff;
+      if (h == 0) a.masks[(size_t)g * nc + c] = (uint8_t)m;
     }
   }
 }
 
-// ============================================================ select + pool
-// Per group: each head's top-P eligible survivors by (score desc, id asc);
-// selected = union, ascending; pool = postings of selected clusters in
-// order, keeping a token iff its mate cluster is larger or unselected.
-__global__ __launch_bounds__(1024) void k_select_pool(StepArgs a) {
-  const int g = blockIdx.x, nc = a.nc;
-  extern __shared__ uint32_t dyn[];
-  uint32_t* selbits = dyn;                 // nc / 32 words
-  __shared__ uint32_t hist[256];
-  __shared__ int scratch[40];
-  __shared__ uint64_t kth[H];
-  const int n = a.status[g * 8 + ST_SURV];
-  const int* surv = a.surv + (size_t)g * nc;
-  for (int h = 0; h < H; ++h) {
-    const uint16_t* f = a.fine_ord + ((size_t)g * H + h) * nc;
-    auto val = [&](int i, uint64_t* v) {
-      const uint32_t o = f[i];
-      *v = ((uint64_t)o << 16) | (0xffffu - (uint32_t)surv[i]);
-      return o != 0;
-    };
-    int above;
-    uint64_t k = block_kth<32>(n, a.P[g], val, hist, scratch, &above);
-    if (threadIdx.x == 0) kth[h] = k;
-    __syncthreads();
-  }
-  for (int w = threadIdx.x; w < nc / 32; w += blockDim.x) selbits[w] = 0;
+// ============================================================ fine select
+// Per (group, head): the P eligible centroids with the best (fine score,
+// lowest ID); members set their bit in the group's selected-cluster bitmap.
+__global__ __launch_bounds__(SEL_BLOCK) void k_fine_select(StepArgs a) {
+  const int g = blockIdx.x / H, h = blockIdx.x % H, nc = a.nc;
+  __shared__ SelectScratch s;
+  extern __shared__ __align__(16) uint16_t so[];  // nc ordered fine scores
+  const uint16_t* f = a.fine_ord + ((size_t)g * H + h) * nc;
+  load_lds_scores(so, f, nc, [](uint32_t o) { return o; });
   __syncthreads();
-  // Selected survivors; survivors are ascending so the list is ascending.
-  const int per = (n + blockDim.x - 1) / blockDim.x;
-  const int i0 = threadIdx.x * per, i1 = min(n, i0 + per);
-  auto selected = [&](int i) {
-    const uint32_t c = surv[i];
-    bool s = false;
-    for (int h = 0; h < H; ++h) {
-      const uint32_t o = a.fine_ord[((size_t)g * H + h) * nc + i];
-      const uint64_t key = ((uint64_t)o << 16) | (0xffffu - c);
-      s |= o != 0 && key >= kth[h];
+  const Selection sel = block_select(so, nc, a.P[g], [](int c) { return (uint32_t)c; }, s);
+  uint32_t* selbm = a.selbm + (size_t)g * (nc / 32);
+  for_scores(so, nc, [&](int c, uint32_t o) {
+    if (sel.member(o, (uint32_t)c)) atomicOr(&selbm[c >> 5], 1u << (c & 31));
+  });
+  if (h == 0) {  // survivors: centroids with a nonzero head mask
+    __shared__ int s_cnt[SEL_WAVES + 1];
+    const uint32_t* m4 = reinterpret_cast<const uint32_t*>(a.masks + (size_t)g * nc);
+    int surv = 0;
+    for (int i = threadIdx.x; i < nc / 4; i += SEL_BLOCK) {
+      const uint32_t w = m4[i];
+      surv += ((w & 0xffu) != 0) + ((w & 0xff00u) != 0) + ((w & 0xff0000u) != 0) + ((w >> 24) != 0);
     }
-    return s;
-  };
-  int cnt = 0;
-  for (int i = i0; i < i1; ++i) cnt += selected(i);
-  int total;
-  int pos = block_excl_scan(cnt, scratch, &total);
-  int* sel = a.sel + (size_t)g * nc;
-  for (int i = i0; i < i1; ++i)
-    if (selected(i)) {
-      const int c = surv[i];
-      sel[pos++] = c;
-      atomicOr(&selbits[c >> 5], 1u << (c & 31));
-    }
-  __syncthreads();
-  const int nsel = total;
-  // Pool emission: owned postings of selected clusters, encounter order.
-  const int* off = a.csr_off + (size_t)g * (nc + 1);
-  const int* tok = a.post_tok + (size_t)g * a.np_max;
-  const int* mate = a.post_mate + (size_t)g * a.np_max;
-  const int per_c = (nsel + blockDim.x - 1) / blockDim.x;
-  const int s0 = threadIdx.x * per_c, s1 = min(nsel, s0 + per_c);
-  auto owned = [&](int j, uint32_t c) {
-    const uint32_t m = (uint32_t)mate[j];
-    return m > c || !((selbits[m >> 5] >> (m & 31)) & 1u);
-  };
-  int own = 0, scanned = 0;
-  for (int s = s0; s < s1; ++s) {
-    const uint32_t c = sel[s];
-    for (int j = off[c]; j < off[c + 1]; ++j) own += owned(j, c);
-    scanned += off[c + 1] - off[c];
+    int total;
+    block_excl_scan(surv, s_cnt, &total);
+    if (threadIdx.x == 0) a.status[g * ST_WORDS + ST_SURV] = total;
   }
-  int pool_n;
-  int p = block_excl_scan(own, scratch, &pool_n);
-  int scanned_total;
-  block_excl_scan(scanned, scratch, &scanned_total);
-  int* ptok = a.pool_tok + (size_t)g * a.cap;
-  int* ppost = a.pool_post + (size_t)g * a.cap;
-  const int limit = min(pool_n, a.cap);
-  for (int s = s0; s < s1; ++s) {
-    const uint32_t c = sel[s];
-    for (int j = off[c]; j < off[c + 1]; ++j)
-      if (owned(j, c)) {
-        if (p < limit) { ptok[p] = tok[j]; ppost[p] = j; }
-        ++p;
+}
+
+// ============================================================ pool
+// Pool blocks own ranges of 32 consecutive centroids (one selected-bitmap
+// word); their selected clusters are handled one per wave in ascending order.
+__device__ __forceinline__ int nth_set_bit(uint32_t m, int r) {
+  for (int i = 0; i < r; ++i) m &= m - 1;
+  return __ffs(m) - 1;
+}
+
+// Posting j of cluster c is owned iff its mate cluster is larger (or absent)
+// or not selected: the first occurrence in encounter order keeps the token.
+__device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint32_t c) {
+  return mate > c || !((selbm[mate >> 5] >> (mate & 31)) & 1u);
+}
+
+// Stage the group's selected bitmap and the range's 33 CSR offsets in LDS.
+__device__ __forceinline__ void stage_range(const StepArgs& a, int g, int b, uint32_t* s_bm,
+                                            int* s_off) {
+  const uint32_t* bm = a.selbm + (size_t)g * (a.nc / 32);
+  for (int i = threadIdx.x; i < a.nc / 32; i += blockDim.x) s_bm[i] = bm[i];
+  if (threadIdx.x <= 32) s_off[threadIdx.x] = a.csr_off[(size_t)g * (a.nc + 1) + b * 32 + threadIdx.x];
+}
+
+__global__ __launch_bounds__(256) void k_pool_count(StepArgs a) {
+  const int g = blockIdx.y, b = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  extern __shared__ uint32_t s_bm[];
+  __shared__ int s_off[33];
+  __shared__ int s_own[4], s_scan[4];
+  stage_range(a, g, b, s_bm, s_off);
+  __syncthreads();
+  const uint32_t M = s_bm[b];
+  const int nsel = __popc(M);
+  const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
+  int own_w = 0, scan_w = 0;
+  for (int rk = wave; rk < nsel; rk += 4) {
+    const int cl = nth_set_bit(M, rk);
+    const uint32_t c = b * 32 + cl;
+    const int j0 = s_off[cl], j1 = s_off[cl + 1];
+    int own = 0;
+    for (int jc = j0; jc < j1; jc += 64) {
+      const int j = jc + lane;
+      const bool o = j < j1 && owned(s_bm, (uint32_t)mate[j], c);
+      own += __popcll(__ballot(o));
+    }
+    if (lane == 0) a.own_cnt[(size_t)g * a.nc + c] = own;
+    own_w += own;
+    scan_w += j1 - j0;
+  }
+  if (lane == 0) {
+    s_own[wave] = own_w;
+    s_scan[wave] = scan_w;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    a.range_cnt[(size_t)g * a.pool_blocks + b] =
+        make_int4(nsel, s_own[0] + s_own[1] + s_own[2] + s_own[3],
+                  s_scan[0] + s_scan[1] + s_scan[2] + s_scan[3], 0);
+}
+
+// Emit the selected list and the pool in encounter order, and score every
+// owned posting on the matrix cores from its cluster-block prefix row:
+// s2 = bf16(16 RNE(sum q15 (2 p2 - 3))).
+__global__ __launch_bounds__(256) void k_pool_emit(StepArgs a) {
+  const int g = blockIdx.y, b = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  extern __shared__ uint32_t s_bm[];
+  __shared__ int s_off[33];
+  __shared__ int s_cl[32];
+  stage_range(a, g, b, s_bm, s_off);
+  const int4* rc = a.range_cnt + (size_t)g * a.pool_blocks;
+  if (wave == 0) {
+    // prefix over the preceding ranges (the last range also writes totals),
+    // and the owned counts of this range's selected clusters
+    const bool last = b == a.pool_blocks - 1;
+    const uint32_t M = a.selbm[(size_t)g * (a.nc / 32) + b];
+    const int own_raw = lane < 32 ? a.own_cnt[(size_t)g * a.nc + b * 32 + lane] : 0;
+    int ps = 0, po = 0, ts = 0, to = 0, tn = 0;
+    for (int i = lane; i <= b; i += 64) {
+      const int4 x = rc[i];
+      if (i < b) { ps += x.x; po += x.y; }
+      ts += x.x; to += x.y; tn += x.z;
+    }
+    ps = wave_sum(ps);
+    po = wave_sum(po);
+    if (last) {
+      ts = wave_sum(ts);
+      to = wave_sum(to);
+      tn = wave_sum(tn);
+      if (lane == 0) {
+        int err = 0;
+        if (a.pool_capacity > 0 && to > a.pool_capacity) err = 4;
+        else if (to < a.pool_min) err = 5;
+        a.status[g * ST_WORDS + ST_POOL] = min(to, a.cap);
+        a.status[g * ST_WORDS + ST_ERR] = err;
+        a.status[g * ST_WORDS + ST_SEL] = ts;
+        a.status[g * ST_WORDS + ST_SCANNED] = tn;
       }
+    }
+    // rank of this lane's centroid among the range's selected clusters
+    const bool is_sel = lane < 32 && ((M >> lane) & 1u);
+    const int rank = __popc(M & ((1u << (lane & 31)) - 1u));
+    const int own = is_sel ? own_raw : 0;
+    const int inc = wave_incl_scan(own);  // lanes in centroid order = selection order
+    if (is_sel) {
+      s_cl[rank] = po + inc - own;
+      a.sel[(size_t)g * a.nc + ps + rank] = b * 32 + lane;
+    }
   }
-  if (threadIdx.x == 0) {
-    int err = 0;
-    if (a.pool_capacity > 0 && pool_n > a.pool_capacity) err = 4;
-    else if (pool_n < a.pool_min) err = 5;
-    a.status[g * 8 + ST_POOL] = limit;
-    a.status[g * 8 + ST_ERR] = err;
-    a.status[g * 8 + ST_SEL] = nsel;
-    a.status[g * 8 + ST_SCANNED] = scanned_total;
+  __syncthreads();
+  const uint32_t M = s_bm[b];
+  const int nsel = __popc(M);
+  if (nsel <= wave) return;
+  const QOperand* q = &a.qop[g * QV_COUNT + QV_Q15];
+  uint32_t bq[4][4];
+  load_b(q, bq);
+  const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
+  const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
+  const uint8_t* __restrict__ p2 = a.post_p2 + (size_t)g * a.np_max * 64;
+  int* pool = a.pool_tok + (size_t)g * a.cap;
+  uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
+  const int row = lane & 15, kb = lane >> 4, h = (lane & 15) >> 2;
+  const int64_t S = q->sum[h];
+  const int fx = q->fx[h] + 4;
+  for (int rk = wave; rk < nsel; rk += 4) {
+    const int cl = nth_set_bit(M, rk);
+    const uint32_t c = b * 32 + cl;
+    const int j0 = s_off[cl], j1 = s_off[cl + 1];
+    int pos = s_cl[rk];
+    for (int jc = j0; jc < j1; jc += 64) {
+      const int j = jc + lane;
+      // all global reads of this chunk are issued before any is consumed
+      const int mj = j < j1 ? mate[j] : -1;
+      const int tj = j < j1 ? ptok[j] : 0;
+      uint4 w[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int jr = jc + 16 * t + row;
+        w[t] = jr < j1 ? *reinterpret_cast<const uint4*>(p2 + (size_t)jr * 64 + kb * 16)
+                       : make_uint4(0, 0, 0, 0);
+      }
+      const bool o = j < j1 && owned(s_bm, (uint32_t)mj, c);
+      const uint64_t om = __ballot(o);
+      const int prank = __popcll(om & ((1ull << lane) - 1));
+      if (o && pos + prank < a.cap) pool[pos + prank] = tj;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (jc + 16 * t >= j1) break;  // wave-uniform
+        const uint32_t words[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          uint32_t av[4];
+          expand2(words[kc], av);
+          acc = mfma_i8(av, bq[kc], acc);
+        }
+        int64_t dot[4];
+        combine_limbs(acc, dot);
+        if ((lane & 3) == 0) {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int idx = 16 * t + 4 * kb + rr;  // posting index within chunk
+            if (!((om >> idx) & 1ull)) continue;
+            const int p = pos + __popcll(om & ((1ull << idx) - 1));
+            if (p >= a.cap) continue;
+            s2[(size_t)h * a.cap + p] =
+                (uint16_t)ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
+          }
+        }
+      }
+      pos += __popcll(om);
+    }
   }
+}
+
+// ============================================================ token top-k
+// Per (group, head): members = top-k by (ordered score, lowest token) of the
+// n items; writes the membership bitmap.  LDS-resident when n <= lds_items,
+// otherwise 8-bit radix passes over the full 40-bit keys in memory.
+__global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
+  const int g = blockIdx.x / H, h = blockIdx.x % H;
+  __shared__ SelectScratch s;
+  extern __shared__ __align__(16) uint16_t so[];
+  const int n = t.status[g * ST_WORDS + t.count_slot];
+  const uint16_t* sc = t.scores + ((size_t)g * H + h) * t.stride;
+  const int* tok = t.tokens + (size_t)g * t.stride;
+  uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
+  auto id = [&](int i) { return (uint32_t)tok[i]; };
+  if (n <= t.lds_items) {
+    load_lds_scores(so, sc, n, [](uint32_t o) { return o; });
+    __syncthreads();
+    const Selection sel = block_select(so, n, t.k, id, s);
+    write_members(so, n, sel, id, bm);
+    return;
+  }
+  auto val = [&](int i, uint64_t* v) {
+    *v = ((uint64_t)sc[i] << 20) | (0xfffffu - (uint32_t)tok[i]);
+    return true;
+  };
+  const uint64_t kth = n <= t.k ? 0 : block_kth<40>(n, t.k, val, s.k);
+  const int lane = threadIdx.x & 63;
+  for (int base = threadIdx.x & ~63; base < n; base += SEL_BLOCK) {
+    const int i = base + lane;
+    uint64_t v = 0;
+    const bool m = i < n && val(i, &v) && v >= kth;
+    const uint64_t ball = __ballot(m);
+    if (lane == 0) bm[base >> 6] = ball;
+  }
+}
+
+// ============================================================ unions
+// Union of the four heads' member bitmaps in item order -> compact tokens.
+// Word popcounts are scanned in LDS; then thread t handles items t + 1024 j.
+__global__ __launch_bounds__(1024) void k_union(UnionArgs u) {
+  const int g = blockIdx.x;
+  extern __shared__ uint32_t s_dyn[];
+  __shared__ int s_scan[17];
+  const int n = u.status[g * ST_WORDS + u.slot_in];
+  const int words = (n + 63) / 64;
+  const bool in_lds = words <= u.lds_words;
+  uint64_t* s_word = reinterpret_cast<uint64_t*>(s_dyn);
+  int* s_base = reinterpret_cast<int*>(s_dyn + 2 * (in_lds ? words : 0));
+  const uint64_t* __restrict__ bm = u.bitmap + (size_t)g * H * u.words;
+  auto word = [&](int w) {
+    return bm[w] | bm[u.words + w] | bm[2 * u.words + w] | bm[3 * u.words + w];
+  };
+  const int per = (words + blockDim.x - 1) / blockDim.x;
+  const int w0 = threadIdx.x * per, w1 = min(words, w0 + per);
+  int cnt = 0;
+  for (int w = w0; w < w1; ++w) {
+    const uint64_t m = word(w);
+    if (in_lds) s_word[w] = m;
+    s_base[w] = cnt;
+    cnt += __popcll(m);
+  }
+  int total;
+  const int pre = block_excl_scan(cnt, s_scan, &total);
+  for (int w = w0; w < w1; ++w) s_base[w] += pre;
+  __syncthreads();
+  const int* __restrict__ in = u.tokens_in + (size_t)g * u.stride_in;
+  int* __restrict__ out = u.tokens_out + (size_t)g * u.stride_out;
+  constexpr int U = 16;  // independent loads in flight per thread
+  for (int base = threadIdx.x; base < n; base += U * blockDim.x) {
+    int val[U], pos[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * blockDim.x;
+      pos[k] = -1;
+      if (i < n) {
+        const int w = i >> 6, bit = i & 63;
+        const uint64_t m = in_lds ? s_word[w] : word(w);
+        if ((m >> bit) & 1ull) {
+          pos[k] = s_base[w] + __popcll(m & ((1ull << bit) - 1));
+          val[k] = in[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+      if (pos[k] >= 0 && pos[k] < u.stride_out) out[pos[k]] = val[k];
+  }
+  if (threadIdx.x == 0) u.status[g * ST_WORDS + u.slot_out] = min(total, u.stride_out);
 }
 
 // ============================================================ key scores
-// 2-bit pool scores: bf16(16 * RNE(sum q15 (2 p2 - 3))), p2 from the
-// posting's cluster-block prefix row.
-__global__ __launch_bounds__(256) void k_score2(StepArgs a) {
-  const int g = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int n = a.status[g * 8 + ST_POOL];
-  const QOperand* q = &a.qop[g * QV_COUNT + QV_Q15];
-  uint32_t b[4][4];
-  bool loaded = false;
-  const int row = lane & 15, kb = lane >> 4;
-  for (int tile = blockIdx.x * 4 + (threadIdx.x >> 6); tile * 16 < n; tile += gridDim.x * 4) {
-    if (!loaded) { load_b(q, b); loaded = true; }
-    const int i_in = tile * 16 + row;
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (i_in < n) {
-      const int j = a.pool_post[(size_t)g * a.cap + i_in];
-      w = *reinterpret_cast<const uint4*>(a.post_p2 + ((size_t)g * a.np_max + j) * 64 + kb * 16);
-    }
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-    v4i acc = {0, 0, 0, 0};
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      uint32_t av[4];
-      expand2(words[kc], av);
-      acc = mfma_i8(av, b[kc], acc);
-    }
-    int64_t dot[4];
-    combine_limbs(acc, dot);
-    if ((lane & 3) == 0) {
-      const int h = (lane & 15) >> 2;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = tile * 16 + 4 * kb + r;
-        if (i >= n) continue;
-        const int64_t Dv = 2 * dot[r] - 3 * q->sum[h];
-        a.s2[((size_t)g * H + h) * a.cap + i] =
-            (uint16_t)ordered16(bf16_rne(scaled_f32(Dv, q->fx[h] + 4)));
-      }
-    }
-  }
-}
-
-// Code4 (p2 << 2 | r2) A operand words of key token t for chunk kc.
+// Code4 (p2 << 2 | r2) A-operand words of one key record for all 4 chunks.
 __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t out[4][4]) {
   const uint4 p = *reinterpret_cast<const uint4*>(rec + kb * 16);
   const uint4 r = *reinterpret_cast<const uint4*>(rec + 64 + kb * 16);
@@ -461,38 +539,36 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
   }
 }
 
-// 4-bit U1 scores: bf16(16 * RNE(sum qs (2 code4 - 15))).
+// 4-bit U1 scores: bf16(16 RNE(sum qs (2 code4 - 15))).
 __global__ __launch_bounds__(256) void k_score4(StepArgs a) {
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int n = a.status[g * 8 + ST_U1];
+  const int n = a.status[g * ST_WORDS + ST_U1];
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile * 16 >= n) return;
   const QOperand* q = &a.qop[g * QV_COUNT + QV_QS];
-  const int row = lane & 15, kb = lane >> 4;
   uint32_t b[4][4];
-  bool loaded = false;
-  for (int tile = blockIdx.x * 4 + (threadIdx.x >> 6); tile * 16 < n; tile += gridDim.x * 4) {
-    if (!loaded) { load_b(q, b); loaded = true; }
-    const int i_in = tile * 16 + row;
-    uint32_t av[4][4] = {};
-    if (i_in < n) {
-      const int t = a.u1_tok[(size_t)g * U1_MAX + i_in];
-      load_code4(a.keyrec + ((size_t)g * a.T + t) * 256, kb, av);
-    }
-    v4i acc = {0, 0, 0, 0};
+  load_b(q, b);
+  const int row = lane & 15, kb = lane >> 4;
+  const int i_in = tile * 16 + row;
+  uint32_t av[4][4] = {};
+  if (i_in < n) {
+    const int t = a.u1_tok[(size_t)g * U1_MAX + i_in];
+    load_code4(a.keyrec + ((size_t)g * a.T + t) * 256, kb, av);
+  }
+  v4i acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(av[kc], b[kc], acc);
-    int64_t dot[4];
-    combine_limbs(acc, dot);
-    if ((lane & 3) == 0) {
-      const int h = (lane & 15) >> 2;
+  for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(av[kc], b[kc], acc);
+  int64_t dot[4];
+  combine_limbs(acc, dot);
+  if ((lane & 3) == 0) {
+    const int h = (lane & 15) >> 2;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = tile * 16 + 4 * kb + r;
-        if (i >= n) continue;
-        const int64_t Dv = 2 * dot[r] - 15 * q->sum[h];
-        a.s4[((size_t)g * H + h) * U1_MAX + i] =
-            (uint16_t)ordered16(bf16_rne(scaled_f32(Dv, q->fx[h] + 4)));
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int i = tile * 16 + 4 * kb + r;
+      if (i >= n) continue;
+      a.s4[((size_t)g * H + h) * U1_MAX + i] = (uint16_t)ordered16(
+          bf16_rne(scaled_f32(2 * dot[r] - 15 * q->sum[h], q->fx[h] + 4)));
     }
   }
 }
@@ -501,195 +577,170 @@ __global__ __launch_bounds__(256) void k_score4(StepArgs a) {
 __global__ __launch_bounds__(256) void k_score8(StepArgs a) {
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int n = a.status[g * 8 + ST_U2];
+  const int n = a.status[g * ST_WORDS + ST_U2];
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile * 16 >= n) return;
   const QOperand* q = &a.qop[g * QV_COUNT + QV_QS];
-  const int row = lane & 15, kb = lane >> 4;
   uint32_t b[4][4];
-  bool loaded = false;
-  for (int tile = blockIdx.x * 4 + (threadIdx.x >> 6); tile * 16 < n; tile += gridDim.x * 4) {
-    if (!loaded) { load_b(q, b); loaded = true; }
-    const int i_in = tile * 16 + row;
-    uint32_t hi[4][4] = {}, lo[4][4] = {};
-    if (i_in < n) {
-      const int t = a.u2_tok[(size_t)g * U2_MAX + i_in];
-      const uint8_t* rec = a.keyrec + ((size_t)g * a.T + t) * 256;
-      load_code4(rec, kb, hi);
-      const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
-      const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
-      const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        expand4(rw[2 * kc], &lo[kc][0]);
-        expand4(rw[2 * kc + 1], &lo[kc][2]);
-      }
-    }
-    v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+  load_b(q, b);
+  const int row = lane & 15, kb = lane >> 4;
+  const int i_in = tile * 16 + row;
+  uint32_t hi[4][4] = {}, lo[4][4] = {};
+  if (i_in < n) {
+    const int t = a.u2_tok[(size_t)g * U2_MAX + i_in];
+    const uint8_t* rec = a.keyrec + ((size_t)g * a.T + t) * 256;
+    load_code4(rec, kb, hi);
+    const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
+    const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
+    const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
-      acc_hi = mfma_i8(hi[kc], b[kc], acc_hi);
-      acc_lo = mfma_i8(lo[kc], b[kc], acc_lo);
+      expand4(rw[2 * kc], &lo[kc][0]);
+      expand4(rw[2 * kc + 1], &lo[kc][2]);
     }
-    int64_t dh[4], dl[4];
-    combine_limbs(acc_hi, dh);
-    combine_limbs(acc_lo, dl);
-    if ((lane & 3) == 0) {
-      const int h = (lane & 15) >> 2;
+  }
+  v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = tile * 16 + 4 * kb + r;
-        if (i >= n) continue;
-        const int64_t Dv = 2 * (16 * dh[r] + dl[r]) - 255 * q->sum[h];
-        a.s8[((size_t)g * H + h) * U2_MAX + i] =
-            (uint16_t)ordered16(bf16_rne(scaled_f32(Dv, q->fx[h])));
-      }
+  for (int kc = 0; kc < 4; ++kc) {
+    acc_hi = mfma_i8(hi[kc], b[kc], acc_hi);
+    acc_lo = mfma_i8(lo[kc], b[kc], acc_lo);
+  }
+  int64_t dh[4], dl[4];
+  combine_limbs(acc_hi, dh);
+  combine_limbs(acc_lo, dl);
+  if ((lane & 3) == 0) {
+    const int h = (lane & 15) >> 2;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = tile * 16 + 4 * kb + r;
+      if (i >= n) continue;
+      a.s8[((size_t)g * H + h) * U2_MAX + i] = (uint16_t)ordered16(
+          bf16_rne(scaled_f32(2 * (16 * dh[r] + dl[r]) - 255 * q->sum[h], q->fx[h])));
     }
   }
-}
-
-// ============================================================ token top-k
-// Per (group, head): members = top-k by (ordered score desc, token asc) of
-// n items; writes a membership bitmap (one bit per item).
-__global__ __launch_bounds__(1024) void k_topk_members(TopkArgs t) {
-  const int g = blockIdx.x / H, h = blockIdx.x % H;
-  __shared__ uint32_t hist[256];
-  __shared__ int scratch[40];
-  const int n = *t.count_ptr(g);
-  const uint16_t* s = t.scores + ((size_t)g * H + h) * t.stride;
-  const int* tok = t.tokens + (size_t)g * t.stride;
-  auto val = [&](int i, uint64_t* v) {
-    *v = ((uint64_t)s[i] << 20) | (0xfffffu - (uint32_t)tok[i]);
-    return true;
-  };
-  int above;
-  const uint64_t kth = block_kth<40>(n, t.k, val, hist, scratch, &above);
-  const bool take_all = n <= t.k;
-  uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
-  const uint32_t kord = (uint32_t)(kth >> 20);
-  for (int base = threadIdx.x & ~63; base < t.words * 64; base += blockDim.x) {
-    const int i = base + (threadIdx.x & 63);
-    bool m = false;
-    if (i < n) {
-      const uint32_t o = s[i];
-      m = take_all || o > kord ||
-          (o == kord && (((uint64_t)o << 20) | (0xfffffu - (uint32_t)tok[i])) >= kth);
-    }
-    const uint64_t ball = __ballot(m);
-    if ((threadIdx.x & 63) == 0) bm[base >> 6] = ball;
-  }
-}
-
-// Union of the four heads' members in item order -> compact token list.
-__global__ __launch_bounds__(1024) void k_union(UnionArgs u) {
-  const int g = blockIdx.x;
-  __shared__ int scratch[40];
-  const int n = *u.count_in(g);
-  const int words = (n + 63) / 64;
-  const uint64_t* bm = u.bitmap + (size_t)g * H * u.words;
-  const int per = (words + blockDim.x - 1) / blockDim.x;
-  const int w0 = threadIdx.x * per, w1 = min(words, w0 + per);
-  int cnt = 0;
-  for (int w = w0; w < w1; ++w)
-    cnt += __popcll(bm[w] | bm[u.words + w] | bm[2 * u.words + w] | bm[3 * u.words + w]);
-  int total;
-  int pos = block_excl_scan(cnt, scratch, &total);
-  const int* in = u.tokens_in + (size_t)g * u.stride_in;
-  int* out = u.tokens_out + (size_t)g * u.stride_out;
-  for (int w = w0; w < w1; ++w) {
-    uint64_t m = bm[w] | bm[u.words + w] | bm[2 * u.words + w] | bm[3 * u.words + w];
-    while (m) {
-      const int bit = __ffsll((unsigned long long)m) - 1;
-      m &= m - 1;
-      if (pos < u.stride_out) out[pos] = in[w * 64 + bit];
-      ++pos;
-    }
-  }
-  if (threadIdx.x == 0) *u.count_out(g) = min(total, u.stride_out);
 }
 
 // ============================================================ final top-100
-// Per (group, head): sort the U2 items by key (bitonic, 1024 slots) and keep
-// the best 100 token IDs in order.
-__global__ __launch_bounds__(256) void k_top100(StepArgs a) {
+// Per (group, head): the 100 best of U2, written best first; the rank of a
+// member is the number of members with a larger (score, -token) key.
+__global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   const int g = blockIdx.x / H, h = blockIdx.x % H;
-  __shared__ uint64_t keys[U2_MAX];
-  const int n = a.status[g * 8 + ST_U2];
-  const uint16_t* s = a.s8 + ((size_t)g * H + h) * U2_MAX;
+  __shared__ SelectScratch s;
+  __shared__ uint64_t s_key[TOPK];
+  __shared__ int s_cnt;
+  const int n = a.status[g * ST_WORDS + ST_U2];
+  const uint16_t* sc = a.s8 + ((size_t)g * H + h) * U2_MAX;
   const int* tok = a.u2_tok + (size_t)g * U2_MAX;
-  for (int i = threadIdx.x; i < U2_MAX; i += blockDim.x)
-    keys[i] = i < n ? (((uint64_t)s[i] << 20) | (0xfffffu - (uint32_t)tok[i])) : 0;
+  auto id = [&](int i) { return (uint32_t)tok[i]; };
+  __shared__ __align__(16) uint16_t so[U2_MAX];
+  load_lds_scores(so, sc, n, [](uint32_t o) { return o; });
+  if (threadIdx.x == 0) s_cnt = 0;
   __syncthreads();
-  for (int size = 2; size <= U2_MAX; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < U2_MAX; i += blockDim.x) {
-        const int j = i ^ stride;
-        if (j > i) {
-          const bool desc = (i & size) == 0;  // overall descending
-          const uint64_t x = keys[i], y = keys[j];
-          if ((x < y) == desc) { keys[i] = y; keys[j] = x; }
-        }
-      }
-      __syncthreads();
+  const Selection sel = block_select(so, n, TOPK, id, s);
+  for_scores(so, n, [&](int i, uint32_t o) {
+    if (!o || !(sel.all || o >= sel.v)) return;
+    const uint32_t t = tok[i];
+    if (sel.member(o, t)) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < TOPK) s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
     }
-  }
-  for (int r = threadIdx.x; r < TOPK; r += blockDim.x) {
-    const uint64_t k = keys[r];
-    a.top[(g * H + h) * TOPK + r] = (r < n) ? (int)(0xfffffu - (uint32_t)(k & 0xfffffu)) : -1;
+  });
+  __syncthreads();
+  const int m = min(s_cnt, TOPK);
+  int* out = a.top + (g * H + h) * TOPK;
+  if ((int)threadIdx.x < m) {
+    const uint64_t key = s_key[threadIdx.x];
+    int rank = 0;
+    for (int j = 0; j < m; ++j) rank += s_key[j] > key;
+    out[rank] = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
+  } else if (threadIdx.x < TOPK) {
+    out[threadIdx.x] = -1;
   }
 }
 
 // ============================================================ sparse SDPA
-// One block per query head; 4 waves split the S + L + 100 keys; lane l owns
-// dims 4l..4l+3.  Online softmax in FP32, scale 1/16, FP8 e4m3 records.
+// Grid (SDPA_SPLIT, 16 query heads), 4 waves per block, 16 consecutive keys
+// of the head's list [sink | local | top-100] per wave.  Lane l owns dims
+// 4l..4l+3.  All 16 keys' records are loaded before any is used; partial
+// (max, sum, unnormalised output) per slice go to k_sdpa_merge.
+// Four FP8 e4m3 values -> FP32 with the gfx950 converter (OCP e4m3fn; exact).
 __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) f[i] = fp8_e4m3_to_f32((w >> (8 * i)) & 0xffu);
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
 }
 
+constexpr int SDPA_WAVE_KEYS = 16;
+
 __global__ __launch_bounds__(256) void k_sdpa(StepArgs a) {
-  const int j = blockIdx.x, g = j / H, h = j % H;
+  const int s = blockIdx.x, j = blockIdx.y, g = j / H, h = j % H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ float s_m[4], s_l[4];
   __shared__ float s_o[4][D];
+  const int total = a.sink + a.local + TOPK;
+  const int k0 = (s * 4 + wave) * SDPA_WAVE_KEYS;  // slices cover total keys
+  const int* top = a.top + (g * H + h) * TOPK;
+  int tk = -1;  // lane < 16: token of key k0 + lane
+  if (lane < SDPA_WAVE_KEYS && k0 + lane < total) {
+    const int i = k0 + lane;
+    tk = i < a.sink ? i : i < a.sink + a.local ? a.T - a.local + (i - a.sink)
+                                               : top[i - a.sink - a.local];
+  }
   float q[4];
   {
     const uint2 qw = *reinterpret_cast<const uint2*>(a.q + j * D + 4 * lane);
     q[0] = bf16_f32(qw.x & 0xffff); q[1] = bf16_f32(qw.x >> 16);
     q[2] = bf16_f32(qw.y & 0xffff); q[3] = bf16_f32(qw.y >> 16);
   }
-  const int S = a.sink, L = a.local, total = S + L + TOPK;
-  float m = -INFINITY, l = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
   const uint8_t* kv = a.kv8 + (size_t)g * a.T * 512;
-  for (int i = wave; i < total; i += 4) {
-    int t;
-    if (i < S) t = i;
-    else if (i < S + L) t = a.T - L + (i - S);
-    else t = a.top[(g * H + h) * TOPK + (i - S - L)];
-    if (t < 0) continue;
-    const uint8_t* rec = kv + (size_t)t * 512;
-    const uint32_t kw = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
-    const uint32_t vw = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
-    float kf[4], vf[4];
-    fp8x4_to_f32(kw, kf);
-    fp8x4_to_f32(vw, vf);
-    float part = q[0] * kf[0] + q[1] * kf[1] + q[2] * kf[2] + q[3] * kf[3];
+  int t[SDPA_WAVE_KEYS];
+  uint32_t kw[SDPA_WAVE_KEYS], vw[SDPA_WAVE_KEYS];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, WAVE);
-    const float logit = part * 0.0625f;
-    const float mn = fmaxf(m, logit);
-    const float scale = __expf(m - mn);
-    const float p = __expf(logit - mn);
-    l = l * scale + p;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) o[d] = o[d] * scale + p * vf[d];
-    m = mn;
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+    t[b] = __shfl(tk, b, WAVE);
+    kw[b] = vw[b] = 0;
+    if (t[b] >= 0) {
+      const uint8_t* rec = kv + (size_t)t[b] * 512;
+      kw[b] = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
+      vw[b] = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
+    }
   }
-  if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+  float logit[SDPA_WAVE_KEYS];
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+    float kf[4];
+    fp8x4_to_f32(kw[b], kf);
+    logit[b] = q[0] * kf[0] + q[1] * kf[1] + q[2] * kf[2] + q[3] * kf[3];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int b = 0; b < SDPA_WAVE_KEYS; ++b) logit[b] += __shfl_xor(logit[b], off, WAVE);
+  float m = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b)
+    if (t[b] >= 0) m = fmaxf(m, logit[b] * 0.0625f);
+  float l = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+    if (t[b] < 0) continue;
+    const float p = __expf(logit[b] * 0.0625f - m);
+    float vf[4];
+    fp8x4_to_f32(vw[b], vf);
+    l += p;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] += p * vf[d];
+  }
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
 #pragma unroll
   for (int d = 0; d < 4; ++d) s_o[wave][4 * lane + d] = o[d];
   __syncthreads();
-  // combine the 4 waves: thread t owns dim t
   const int d = threadIdx.x;
-  float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
   float lsum = 0.f, acc = 0.f;
   for (int w = 0; w < 4; ++w) {
     if (s_m[w] == -INFINITY) continue;
@@ -697,27 +748,83 @@ __global__ __launch_bounds__(256) void k_sdpa(StepArgs a) {
     lsum += s_l[w] * sc;
     acc += s_o[w][d] * sc;
   }
+  float* part = a.attn_part + ((size_t)j * a.sdpa_split + s) * (D + 2);
+  part[d] = acc;
+  if (d == 0) {
+    part[D] = M;
+    part[D + 1] = lsum;
+  }
+}
+
+// Merge the slices of each query head: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+__global__ __launch_bounds__(256) void k_sdpa_merge(StepArgs a) {
+  const int j = blockIdx.x, d = threadIdx.x;
+  const float* parts = a.attn_part + (size_t)j * a.sdpa_split * (D + 2);
+  float M = -INFINITY;
+  for (int p = 0; p < a.sdpa_split; ++p) M = fmaxf(M, parts[p * (D + 2) + D]);
+  float lsum = 0.f, acc = 0.f;
+  for (int p = 0; p < a.sdpa_split; ++p) {
+    const float mp = parts[p * (D + 2) + D];
+    if (mp == -INFINITY) continue;
+    const float sc = __expf(mp - M);
+    lsum += parts[p * (D + 2) + D + 1] * sc;
+    acc += parts[p * (D + 2) + d] * sc;
+  }
   a.out[j * D + d] = (uint16_t)bf16_rne(acc / lsum);
 }
 
 // ============================================================ launcher
-void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st) {
-  const int groups_tiles = (a.nc + 63) / 64;
-  hipLaunchKernelGGL(k_qprep, dim3(G), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(k_coarse, dim3(groups_tiles, G), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_thresh, dim3(G * H), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(k_survivors, dim3(G), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(k_fine, dim3(min(groups_tiles, 256), G), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_select_pool, dim3(G), dim3(1024), (size_t)(a.nc / 32) * 4, st, a);
-  hipLaunchKernelGGL(k_score2, dim3(w.score_blocks, G), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_topk_members, dim3(G * H), dim3(1024), 0, st, w.top_u1);
-  hipLaunchKernelGGL(k_union, dim3(G), dim3(1024), 0, st, w.union_u1);
+const char* const kKernelNames[N_STEP_KERNELS] = {
+    "qprep", "coarse", "thresh", "fine", "fine_select", "pool_count", "pool_emit",
+    "top1600", "union_u1", "score4", "top256", "union_u2", "score8", "top100", "sdpa",
+    "sdpa_merge"};
+
+// Launch every kernel of one decode step on stream st.  If ev is non-NULL
+// (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
+// ev[N_STEP_KERNELS] after the last one.
+void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev) {
+  const int tiles_blocks = (a.nc + 63) / 64;
+  const size_t bm_lds = (size_t)(a.nc / 32) * 4;
+  int k = 0;
+  auto mark = [&]() {
+    if (ev) (void)hipEventRecord(ev[k], st);
+    ++k;
+  };
+  mark();
+  hipLaunchKernelGGL(k_qprep, dim3(G, QV_COUNT), dim3(256), 0, st, a);
+  mark();
+  hipLaunchKernelGGL(k_coarse, dim3(tiles_blocks, G), dim3(256), 0, st, a);
+  mark();
+  hipLaunchKernelGGL(k_thresh, dim3(G * H), dim3(SEL_BLOCK), (size_t)a.nc * 2, st, a);
+  mark();
+  hipLaunchKernelGGL(k_fine, dim3(tiles_blocks, G), dim3(256), 0, st, a);
+  mark();
+  hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), (size_t)a.nc * 2, st, a);
+  mark();
+  hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(256), bm_lds, st, a);
+  mark();
+  hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(256), bm_lds, st, a);
+  mark();
+  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), (size_t)w.top_u1.lds_items * 2, st,
+                     w.top_u1);
+  mark();
+  hipLaunchKernelGGL(k_union, dim3(G), dim3(1024), w.union_u1_lds, st, w.union_u1);
+  mark();
   hipLaunchKernelGGL(k_score4, dim3(U1_MAX / 64, G), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_topk_members, dim3(G * H), dim3(1024), 0, st, w.top_u2);
-  hipLaunchKernelGGL(k_union, dim3(G), dim3(1024), 0, st, w.union_u2);
+  mark();
+  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), (size_t)w.top_u2.lds_items * 2, st,
+                     w.top_u2);
+  mark();
+  hipLaunchKernelGGL(k_union, dim3(G), dim3(1024), w.union_u2_lds, st, w.union_u2);
+  mark();
   hipLaunchKernelGGL(k_score8, dim3(U2_MAX / 64, G), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_sdpa, dim3(G * H), dim3(256), 0, st, a);
+  mark();
+  hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), 0, st, a);
+  mark();
+  hipLaunchKernelGGL(k_sdpa, dim3(a.sdpa_split, G * H), dim3(256), 0, st, a);
+  mark();
+  hipLaunchKernelGGL(k_sdpa_merge, dim3(G * H), dim3(256), 0, st, a);
+  mark();
 }
 
 }  // namespace skv

@@ -25,6 +25,7 @@
 
 #include "../../include/seoulkv4_hip.h"
 #include "skv_device.h"
+#include "skv_select.h"
 #include "skv_step.h"
 
 using namespace skv;
@@ -54,9 +55,13 @@ struct Handle {
   size_t static_bytes = 0, work_bytes = 0;
   StepArgs a{};
   StepWork w{};
-  uint64_t* bm_u1 = nullptr;
-  uint64_t* bm_u2 = nullptr;
   bool bound = false, ran = false;
+  size_t lds_per_block = 0;
+  // per-kernel event timing (skv_profile)
+  bool profiling = false, prof_pending = false;
+  hipEvent_t prof_ev[N_STEP_KERNELS + 1] = {};
+  double prof_ms[N_STEP_KERNELS] = {};
+  int prof_steps = 0;
   std::string error, meta;
 };
 
@@ -205,6 +210,8 @@ void skv_destroy(void* handle) {
   if (!h) return;
   if (h->stream) (void)hipStreamSynchronize(h->stream);
   if (h->q_copied) (void)hipEventDestroy(h->q_copied);
+  for (hipEvent_t e : h->prof_ev)
+    if (e) (void)hipEventDestroy(e);
   if (h->q_host) (void)hipHostFree(h->q_host);
   if (h->static_mem) (void)hipFree(h->static_mem);
   if (h->work_mem) (void)hipFree(h->work_mem);
@@ -273,6 +280,15 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     fail(h, SKV_EHIP, "hipSetDevice(%d) failed", device);
     return bail(SKV_EHIP);
   }
+  {
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
+        hipSuccess || lds <= 0) {
+      fail(h, SKV_EHIP, "cannot query the LDS size of device %d", device);
+      return bail(SKV_EHIP);
+    }
+    h->lds_per_block = (size_t)lds;
+  }
   if (stream) {
     h->stream = static_cast<hipStream_t>(stream);
   } else {
@@ -289,7 +305,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   a.local = ix->local;
   a.nc = nc;
   a.np_max = np_max;
-  a.cap = std::max(R, 64);
+  a.cap = (std::max(R, 64) + 63) / 64 * 64;  // 16-byte aligned score rows
   a.pool_min = ix->pool_min;
   a.pool_capacity = ix->pool_capacity;
   a.debug = ix->debug;
@@ -298,6 +314,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.lam[g] = ix->cells[g].lam;
   }
   const int words1 = (a.cap + 63) / 64, words2 = (U1_MAX + 63) / 64;
+  a.words_u1 = words1;
+  a.words_u2 = words2;
+  a.pool_blocks = nc / 32;
+  a.sdpa_split = (a.sink + a.local + TOPK + 63) / 64;
 
   // ---- static arena
   Arena s;
@@ -334,13 +354,18 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.upper = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.thr = (uint32_t*)ar.take(G * H * 4);
     a.masks = (uint8_t*)ar.take((size_t)G * nc);
-    a.surv = (int*)ar.take((size_t)G * nc * 4);
     a.fine_ord = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.fine_bits = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.sel = (int*)ar.take((size_t)G * nc * 4);
+    a.own_cnt = (int*)ar.take((size_t)G * nc * 4);
+    a.range_cnt = (int4*)ar.take((size_t)G * a.pool_blocks * 16);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
-    a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
+    a.attn_part = (float*)ar.take((size_t)G * H * a.sdpa_split * (D + 2) * 4);
+    // one contiguous range cleared by k_qprep every step
+    a.zero_words = (size_t)G * (nc / 32);
+    a.zero_base = (uint32_t*)ar.take(a.zero_words * 4);
+    a.selbm = a.zero_base;
     a.u1_tok = (int*)ar.take((size_t)G * U1_MAX * 4);
     a.s4 = (uint16_t*)ar.take((size_t)G * H * U1_MAX * 2);
     a.u2_tok = (int*)ar.take((size_t)G * U2_MAX * 4);
@@ -348,8 +373,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.top = (int*)ar.take(G * H * TOPK * 4);
     a.status = (int*)ar.take(G * ST_WORDS * 4);
     a.out = (uint16_t*)ar.take(16 * D * 2);
-    h->bm_u1 = (uint64_t*)ar.take((size_t)G * H * words1 * 8);
-    h->bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
+    a.bm_u1 = (uint64_t*)ar.take((size_t)G * H * words1 * 8);
+    a.bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
   };
   plan_work(wk);
   h->work_bytes = wk.used;
@@ -445,11 +470,27 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
 
   // ---- step plumbing
   StepWork& w = h->w;
-  w.score_blocks = std::max(1, std::min((a.cap + 63) / 64, 512));
-  w.top_u1 = TopkArgs{a.s2, a.pool_tok, a.cap, M15, h->bm_u1, words1, a.status, ST_POOL};
-  w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, h->bm_u2, words2, a.status, ST_U1};
-  w.union_u1 = UnionArgs{h->bm_u1, words1, a.pool_tok, a.cap, a.u1_tok, U1_MAX, a.status, ST_POOL, ST_U1};
-  w.union_u2 = UnionArgs{h->bm_u2, words2, a.u1_tok, U1_MAX, a.u2_tok, U2_MAX, a.status, ST_U1, ST_U2};
+  // LDS-resident selection: 16-bit scores beside the selection scratch
+  const size_t sel_static = sizeof(SelectScratch) + 1024;
+  const int lds_items = (int)std::min<size_t>(
+      65536, (h->lds_per_block - std::min(h->lds_per_block, sel_static)) / 2 / 8 * 8);
+  if (nc > lds_items) {
+    fail(h, SKV_EINVAL, "n_centroids %d exceeds the LDS selection capacity %d", nc, lds_items);
+    return bail(SKV_EINVAL);
+  }
+  w.top_u1 = TopkArgs{a.s2, a.pool_tok, a.cap, M15, a.bm_u1, words1, a.status, ST_POOL,
+                      std::min(lds_items, a.cap)};
+  w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, a.bm_u2, words2, a.status, ST_U1, U1_MAX};
+  // OR-ed bitmap words stay in LDS while words * 12 B fits 96 KiB; the word
+  // bases (4 B each) always do (<= 64 KiB at 2^20 tokens).
+  const int lds1 = words1 * 12 <= 96 * 1024 ? words1 : 0;
+  const int lds2 = words2 * 12 <= 96 * 1024 ? words2 : 0;
+  w.union_u1 = UnionArgs{a.bm_u1, words1, lds1, a.pool_tok, a.cap, a.u1_tok, U1_MAX,
+                         a.status, ST_POOL, ST_U1};
+  w.union_u2 = UnionArgs{a.bm_u2, words2, lds2, a.u1_tok, U1_MAX, a.u2_tok, U2_MAX,
+                         a.status, ST_U1, ST_U2};
+  w.union_u1_lds = (size_t)words1 * (lds1 ? 12 : 4);
+  w.union_u2_lds = (size_t)words2 * (lds2 ? 12 : 4);
 
   if (hipHostMalloc((void**)&h->q_host, 16 * D * 2, hipHostMallocDefault) != hipSuccess ||
       hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess) {
@@ -465,10 +506,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
            "\"n_centroids\": %d, \"nprobe\": [%d, %d, %d, %d], \"pool_buffer\": %d, "
            "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
            "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
-           "\"kernels_per_step\": 15}",
+           "\"kernels_per_step\": 16, \"lds_per_block\": %zu, \"pool_lds_items\": %d}",
            json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), T, a.sink, a.local,
            nc, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min, a.pool_capacity, np_max,
-           h->static_bytes, h->work_bytes);
+           h->static_bytes, h->work_bytes, h->lds_per_block, w.top_u1.lds_items);
   h->meta = buf;
   *handle_out = h;
   return SKV_OK;
@@ -500,10 +541,62 @@ int skv_enqueue(void* handle) {
   if (!h) return SKV_ESTATE;
   if (!h->bound) return fail(h, SKV_ESTATE, "bind a query before enqueue");
   HIPCHK(h, hipSetDevice(h->device));
-  launch_step(h->a, h->w, h->stream);
+  if (h->profiling) {
+    if (h->prof_pending) {  // fold the previous step's events in first
+      HIPCHK(h, hipEventSynchronize(h->prof_ev[N_STEP_KERNELS]));
+      for (int i = 0; i < N_STEP_KERNELS; ++i) {
+        float ms = 0.f;
+        HIPCHK(h, hipEventElapsedTime(&ms, h->prof_ev[i], h->prof_ev[i + 1]));
+        h->prof_ms[i] += ms;
+      }
+      ++h->prof_steps;
+    }
+    launch_step(h->a, h->w, h->stream, h->prof_ev);
+    h->prof_pending = true;
+  } else {
+    launch_step(h->a, h->w, h->stream, nullptr);
+  }
   HIPCHK(h, hipGetLastError());
   h->ran = true;
   return SKV_OK;
+}
+
+int skv_profile(void* handle, int enable) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  if (enable && !h->prof_ev[0])
+    for (int i = 0; i <= N_STEP_KERNELS; ++i) HIPCHK(h, hipEventCreate(&h->prof_ev[i]));
+  h->profiling = enable != 0;
+  h->prof_pending = false;
+  h->prof_steps = 0;
+  for (double& v : h->prof_ms) v = 0.0;
+  return SKV_OK;
+}
+
+int skv_profile_read(void* handle, float* mean_ms, int n, int32_t* steps) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !mean_ms || n < N_STEP_KERNELS) return SKV_EINVAL;
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  if (h->profiling && h->prof_pending) {
+    for (int i = 0; i < N_STEP_KERNELS; ++i) {
+      float ms = 0.f;
+      HIPCHK(h, hipEventElapsedTime(&ms, h->prof_ev[i], h->prof_ev[i + 1]));
+      h->prof_ms[i] += ms;
+    }
+    ++h->prof_steps;
+    h->prof_pending = false;
+  }
+  for (int i = 0; i < N_STEP_KERNELS; ++i)
+    mean_ms[i] = h->prof_steps ? (float)(h->prof_ms[i] / h->prof_steps) : 0.f;
+  if (steps) *steps = h->prof_steps;
+  return SKV_OK;
+}
+
+int skv_kernel_count(void) { return N_STEP_KERNELS; }
+
+const char* skv_kernel_name(int i) {
+  return (i >= 0 && i < N_STEP_KERNELS) ? kKernelNames[i] : "";
 }
 
 int skv_sync(void* handle, int32_t* status) {

@@ -4,14 +4,15 @@
 //   k_qprep          _kernels/query_prepare/host.py:26-51 (q15, qs, ||q|| lambda)
 //   k_coarse         codegen/coarse_compute.py:61-119 (2-bit interval scores)
 //   k_thresh         _kernels/stage1_coarse/seoulkv4_coarse_select.py:297-310
-//   k_survivors      _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379
-//   k_fine           codegen/fine_postscale_codegen.py:6-71, codegen/fine.py:1848-1861
-//   k_select_pool    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73,
-//                    codegen/stage15.py:275-345 (mate-ownership dedup)
-//   k_score2         codegen/stage15.py:886-995
-//   k_topk_members   codegen/stage15.py:1027-1180 (top-2048, first 1600 used),
-//   + k_union        codegen/stage15.py:1519-1597; codegen/refinement_fusion.py:142-186
+//   k_fine           _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379 (masks),
+//                    codegen/fine_postscale_codegen.py:6-71, codegen/fine.py:1848-1861
+//   k_fine_select    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73
+//   k_pool_count     codegen/stage15.py:275-345 (mate-ownership dedup)
+//   k_pool_emit      codegen/stage15.py:275-345 + 886-995 (2-bit scores)
+//   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
+//   k_union          codegen/stage15.py:1519-1597; codegen/refinement_fusion.py:142-186
 //   k_score4         _kernels/stage16/seoulkv4_stage16_matrix.py:21-60
+//   k_top256         codegen/refinement_fusion.py:263-266,402-455
 //   k_score8         _kernels/stage16/seoulkv4_union_matrix.py:58-139
 //   k_top100         codegen/refinement_fusion.py:296-300,495-531
 //   k_sdpa           codegen/attention.py:35-201 (+ TTNN sparse_sdpa compute)
@@ -36,12 +37,16 @@ enum {
   ST_WORDS = 8
 };
 
+
 struct StepArgs {
   // shapes
   int T, sink, local, nc, np_max, cap;
   int P[G];
   float lam[G];
   int pool_min, pool_capacity, debug;
+  int pool_blocks;          // nc / 32: 32-centroid ranges of the pool kernels
+  int words_u1, words_u2;   // bitmap words per (group, head)
+  int sdpa_split;           // 64-key slices per query head: ceil((S + L + 100) / 64)
   // static device data
   const uint16_t* q;        // [16][256] bf16 (bound query)
   const float* kscale;      // [G][256]
@@ -61,14 +66,21 @@ struct StepArgs {
   uint16_t* lower;          // [G][H][nc]
   uint16_t* upper;          // [G][H][nc]
   uint32_t* thr;            // [G][H]
-  uint8_t* masks;           // [G][nc]
-  int* surv;                // [G][nc]
-  uint16_t* fine_ord;       // [G][H][nc] (by survivor index)
-  uint16_t* fine_bits;      // [G][H][nc] (by centroid, debug)
-  int* sel;                 // [G][nc]
+  uint8_t* masks;           // [G][nc] survivor head masks
+  uint16_t* fine_ord;       // [G][H][nc] ordered fine score, 0 = ineligible
+  uint16_t* fine_bits;      // [G][H][nc] BF16 fine score (debug)
+  int* sel;                 // [G][nc] selected clusters, ascending
+  int* own_cnt;             // [G][nc] owned postings per selected cluster
+  int4* range_cnt;          // [G][pool_blocks] {selected, owned, scanned, 0}
   int* pool_tok;            // [G][cap]
-  int* pool_post;           // [G][cap]
   uint16_t* s2;             // [G][H][cap] ordered
+  uint64_t* bm_u1;          // [G][H][words_u1] top-1600 members
+  uint64_t* bm_u2;          // [G][H][words_u2] top-256 members
+  float* attn_part;         // [16][sdpa_split][D + 2] partial (o, max, sum)
+  // zeroed by k_qprep every step (one contiguous range)
+  uint32_t* zero_base;
+  size_t zero_words;
+  uint32_t* selbm;          // [G][nc/32] selected-cluster bitmap
   int* u1_tok;              // [G][U1_MAX]
   uint16_t* s4;             // [G][H][U1_MAX] ordered
   int* u2_tok;              // [G][U2_MAX]
@@ -86,29 +98,31 @@ struct TopkArgs {
   uint64_t* bitmap;         // [G][H][words]
   int words;
   int* status;
-  int count_slot;
-  __device__ const int* count_ptr(int g) const { return status + g * ST_WORDS + count_slot; }
+  int count_slot;           // status word holding the item count
+  int lds_items;            // scores held in LDS when count <= lds_items
 };
 
 struct UnionArgs {
   const uint64_t* bitmap;   // [G][H][words]
   int words;
+  int lds_words;            // keep OR-ed words in LDS when words <= lds_words
   const int* tokens_in;
   int stride_in;
   int* tokens_out;
   int stride_out;
   int* status;
   int slot_in, slot_out;
-  __device__ const int* count_in(int g) const { return status + g * ST_WORDS + slot_in; }
-  __device__ int* count_out(int g) const { return status + g * ST_WORDS + slot_out; }
 };
 
 struct StepWork {
   TopkArgs top_u1, top_u2;
   UnionArgs union_u1, union_u2;
-  int score_blocks;
+  size_t union_u1_lds, union_u2_lds;  // dynamic LDS bytes of the union kernels
 };
 
-void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st);
+constexpr int N_STEP_KERNELS = 16;
+extern const char* const kKernelNames[N_STEP_KERNELS];
+
+void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev);
 
 }  // namespace skv
