@@ -16,9 +16,9 @@
 //   score4      4-bit scores of U1
 //   top256      per head: top-256 of U1 -> bitmap;  union_u2 -> U2
 //   score8      8-bit scores of U2
-//   top100      per head: best-first top-100 token IDs
-//   sdpa        FP8 sparse attention over sink + local + top-100, split into
-//               64-key slices; sdpa_merge combines the slices of each head
+//   top100      per head: best-first top-100 token IDs, then FP8 attention over
+//               them merged with the sink/local attention slices (computed
+//               by extra blocks of the thresh launch; they depend only on Q)
 // Reference stages: see the table in skv_step.h.
 //
 // Selection keys are (ordered BF16 score, lowest ID first); all score dots
@@ -124,6 +124,134 @@ __device__ __forceinline__ void load_b(const QOperand* q, uint32_t b[4][4]) {
   }
 }
 
+// ============================================================ sparse SDPA
+// Attention of query head j = 4g + h over its KV group's FP8 [V || K] records
+// for the keys [sink | local | top-100] (softmax over all of them, scale 1/16).
+// The sink/local part depends only on Q: extra blocks of the k_thresh launch
+// compute it as 128-key slices (partial max, sum, unnormalised output), and
+// k_top100 attends the head's 100 selected keys and merges everything.
+constexpr int SDPA_WAVE_KEYS = 16;
+constexpr int DENSE_BLOCK_KEYS = (SEL_BLOCK / WAVE) * SDPA_WAVE_KEYS;
+
+// Four FP8 e4m3 values -> FP32 with the gfx950 converter (OCP e4m3fn; exact).
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
+}
+
+__device__ __forceinline__ void load_q4(const StepArgs& a, int j, float q[4]) {
+  const int lane = threadIdx.x & 63;
+  const uint2 qw = *reinterpret_cast<const uint2*>(a.q + j * D + 4 * lane);
+  q[0] = bf16_f32(qw.x & 0xffff); q[1] = bf16_f32(qw.x >> 16);
+  q[2] = bf16_f32(qw.y & 0xffff); q[3] = bf16_f32(qw.y >> 16);
+}
+
+// One wave over up to 16 keys: lane b < 16 holds the token of key b in tk
+// (-1: none); lane l owns dims 4l..4l+3.  All records are loaded before any
+// is used.  Returns the wave's max logit m, softmax sum l and output o.
+__device__ __forceinline__ void wave_attend(const uint8_t* __restrict__ kv, const float q[4],
+                                            int tk, float& m, float& l, float o[4]) {
+  const int lane = threadIdx.x & 63;
+  int t[SDPA_WAVE_KEYS];
+  uint32_t kw[SDPA_WAVE_KEYS], vw[SDPA_WAVE_KEYS];
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+    t[b] = __shfl(tk, b, WAVE);
+    const uint8_t* rec = kv + (size_t)max(t[b], 0) * 512;
+    kw[b] = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
+    vw[b] = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
+  }
+  float logit[SDPA_WAVE_KEYS];
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+    float kf[4];
+    fp8x4_to_f32(kw[b], kf);
+    logit[b] = q[0] * kf[0] + q[1] * kf[1] + q[2] * kf[2] + q[3] * kf[3];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int b = 0; b < SDPA_WAVE_KEYS; ++b) logit[b] += __shfl_xor(logit[b], off, WAVE);
+  m = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b)
+    if (t[b] >= 0) m = fmaxf(m, logit[b] * 0.0625f);
+  l = 0.f;
+  o[0] = o[1] = o[2] = o[3] = 0.f;
+#pragma unroll
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+    if (t[b] < 0) continue;
+    const float p = __expf(logit[b] * 0.0625f - m);
+    float vf[4];
+    fp8x4_to_f32(vw[b], vf);
+    l += p;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] += p * vf[d];
+  }
+}
+
+struct AttnScratch {
+  float m[SEL_BLOCK / WAVE], l[SEL_BLOCK / WAVE];
+  float o[SEL_BLOCK / WAVE][D];
+};
+
+// Publish a wave partial to LDS; after a barrier, merge_waves gives thread
+// d < 256 the block's (max, sum, output[d]).
+__device__ __forceinline__ void stash_wave(AttnScratch& s, float m, float l, const float o[4]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    s.m[wave] = m;
+    s.l[wave] = l;
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) s.o[wave][4 * lane + d] = o[d];
+}
+
+__device__ __forceinline__ void merge_waves(const AttnScratch& s, int d, float& M, float& L,
+                                            float& O) {
+  constexpr int NW = SEL_BLOCK / WAVE;
+  M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) M = fmaxf(M, s.m[w]);
+  L = 0.f;
+  O = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    if (s.m[w] == -INFINITY) continue;
+    const float sc = __expf(s.m[w] - M);
+    L += s.l[w] * sc;
+    O += s.o[w][d] * sc;
+  }
+}
+
+// Dense slice r of query head j: keys r*128 .. r*128+127 of [sink | local].
+__device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
+  const int j = blk / a.dense_slices, r = blk % a.dense_slices, g = j / H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ndense = a.sink + a.local;
+  float q[4];
+  load_q4(a, j, q);
+  int tk = -1;
+  const int i = r * DENSE_BLOCK_KEYS + wave * SDPA_WAVE_KEYS + lane;
+  if (lane < SDPA_WAVE_KEYS && i < ndense) tk = i < a.sink ? i : a.T - a.local + (i - a.sink);
+  float m, l, o[4];
+  wave_attend(a.kv8 + (size_t)g * a.T * 512, q, tk, m, l, o);
+  stash_wave(s, m, l, o);
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float M, L, O;
+    merge_waves(s, threadIdx.x, M, L, O);
+    float* part = a.dense_part + ((size_t)j * a.dense_slices + r) * (D + 2);
+    part[threadIdx.x] = O;
+    if (threadIdx.x == 0) {
+      part[D] = M;
+      part[D + 1] = L;
+    }
+  }
+}
+
 // ============================================================ coarse
 // Wave tile: 16 centroids x 4 heads.  lower/upper = bf16(value -/+ margin),
 // value = RNE(sum q (2u - 3)) * scale/4, margin = ||q|| lambda bf16(resid).
@@ -168,8 +296,14 @@ __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
 }
 
 // ============================================================ thresholds
-// Per (group, head): the P-th largest lower bound (its value only).
+// Per (group, head): the P-th largest lower bound (its value only).  Blocks
+// beyond the 16 (group, head) pairs compute the sink/local attention slices.
 __global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
+  if (blockIdx.x >= G * H) {  // sink/local attention slices (depend only on Q)
+    __shared__ AttnScratch att;
+    dense_attend(a, blockIdx.x - G * H, att);
+    return;
+  }
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
   extern __shared__ __align__(16) uint16_t so[];  // nc ordered lower bounds
@@ -337,10 +471,15 @@ __global__ __launch_bounds__(256) void k_pool_emit(StepArgs a) {
     const uint32_t M = a.selbm[(size_t)g * (a.nc / 32) + b];
     const int own_raw = lane < 32 ? a.own_cnt[(size_t)g * a.nc + b * 32 + lane] : 0;
     int ps = 0, po = 0, ts = 0, to = 0, tn = 0;
-    for (int i = lane; i <= b; i += 64) {
-      const int4 x = rc[i];
-      if (i < b) { ps += x.x; po += x.y; }
-      ts += x.x; to += x.y; tn += x.z;
+    for (int i0 = lane; i0 <= b; i0 += 256) {
+      int4 x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = i0 + 64 * u <= b ? rc[i0 + 64 * u] : make_int4(0, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (i0 + 64 * u < b) { ps += x[u].x; po += x[u].y; }
+        ts += x[u].x; to += x[u].y; tn += x[u].z;
+      }
     }
     ps = wave_sum(ps);
     po = wave_sum(po);
@@ -507,13 +646,11 @@ __global__ __launch_bounds__(1024) void k_union(UnionArgs u) {
     for (int k = 0; k < U; ++k) {
       const int i = base + k * blockDim.x;
       pos[k] = -1;
+      val[k] = i < n ? in[i] : 0;  // unconditional: all loads issue together
       if (i < n) {
         const int w = i >> 6, bit = i & 63;
         const uint64_t m = in_lds ? s_word[w] : word(w);
-        if ((m >> bit) & 1ull) {
-          pos[k] = s_base[w] + __popcll(m & ((1ull << bit) - 1));
-          val[k] = in[i];
-        }
+        if ((m >> bit) & 1ull) pos[k] = s_base[w] + __popcll(m & ((1ull << bit) - 1));
       }
     }
 #pragma unroll
@@ -621,13 +758,16 @@ __global__ __launch_bounds__(256) void k_score8(StepArgs a) {
 }
 
 // ============================================================ final top-100
-// Per (group, head): the 100 best of U2, written best first; the rank of a
-// member is the number of members with a larger (score, -token) key.
+// Per (group, head): the 100 best of U2, written best first (the rank of a
+// member is the number of members with a larger (score, -token) key), then
+// the head's attention over them merged with its sink/local slices.
 __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
   __shared__ uint64_t s_key[TOPK];
+  __shared__ int s_tok[TOPK];
   __shared__ int s_cnt;
+  __shared__ AttnScratch att;
   const int n = a.status[g * ST_WORDS + ST_U2];
   const uint16_t* sc = a.s8 + ((size_t)g * H + h) * U2_MAX;
   const int* tok = a.u2_tok + (size_t)g * U2_MAX;
@@ -651,133 +791,54 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   if ((int)threadIdx.x < m) {
     const uint64_t key = s_key[threadIdx.x];
     int rank = 0;
-    for (int j = 0; j < m; ++j) rank += s_key[j] > key;
-    out[rank] = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
+    for (int jj = 0; jj < m; ++jj) rank += s_key[jj] > key;
+    const int t = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
+    out[rank] = t;
+    s_tok[rank] = t;
   } else if (threadIdx.x < TOPK) {
     out[threadIdx.x] = -1;
+    s_tok[threadIdx.x] = -1;
   }
-}
-
-// ============================================================ sparse SDPA
-// Grid (SDPA_SPLIT, 16 query heads), 4 waves per block, 16 consecutive keys
-// of the head's list [sink | local | top-100] per wave.  Lane l owns dims
-// 4l..4l+3.  All 16 keys' records are loaded before any is used; partial
-// (max, sum, unnormalised output) per slice go to k_sdpa_merge.
-// Four FP8 e4m3 values -> FP32 with the gfx950 converter (OCP e4m3fn; exact).
-__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
-  typedef float v2f __attribute__((ext_vector_type(2)));
-  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
-}
-
-constexpr int SDPA_WAVE_KEYS = 16;
-
-__global__ __launch_bounds__(256) void k_sdpa(StepArgs a) {
-  const int s = blockIdx.x, j = blockIdx.y, g = j / H, h = j % H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __shared__ float s_m[4], s_l[4];
-  __shared__ float s_o[4][D];
-  const int total = a.sink + a.local + TOPK;
-  const int k0 = (s * 4 + wave) * SDPA_WAVE_KEYS;  // slices cover total keys
-  const int* top = a.top + (g * H + h) * TOPK;
-  int tk = -1;  // lane < 16: token of key k0 + lane
-  if (lane < SDPA_WAVE_KEYS && k0 + lane < total) {
-    const int i = k0 + lane;
-    tk = i < a.sink ? i : i < a.sink + a.local ? a.T - a.local + (i - a.sink)
-                                               : top[i - a.sink - a.local];
-  }
-  float q[4];
-  {
-    const uint2 qw = *reinterpret_cast<const uint2*>(a.q + j * D + 4 * lane);
-    q[0] = bf16_f32(qw.x & 0xffff); q[1] = bf16_f32(qw.x >> 16);
-    q[2] = bf16_f32(qw.y & 0xffff); q[3] = bf16_f32(qw.y >> 16);
-  }
-  const uint8_t* kv = a.kv8 + (size_t)g * a.T * 512;
-  int t[SDPA_WAVE_KEYS];
-  uint32_t kw[SDPA_WAVE_KEYS], vw[SDPA_WAVE_KEYS];
-#pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
-    t[b] = __shfl(tk, b, WAVE);
-    kw[b] = vw[b] = 0;
-    if (t[b] >= 0) {
-      const uint8_t* rec = kv + (size_t)t[b] * 512;
-      kw[b] = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
-      vw[b] = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
-    }
-  }
-  float logit[SDPA_WAVE_KEYS];
-#pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
-    float kf[4];
-    fp8x4_to_f32(kw[b], kf);
-    logit[b] = q[0] * kf[0] + q[1] * kf[1] + q[2] * kf[2] + q[3] * kf[3];
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-    for (int b = 0; b < SDPA_WAVE_KEYS; ++b) logit[b] += __shfl_xor(logit[b], off, WAVE);
-  float m = -INFINITY;
-#pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b)
-    if (t[b] >= 0) m = fmaxf(m, logit[b] * 0.0625f);
-  float l = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
-    if (t[b] < 0) continue;
-    const float p = __expf(logit[b] * 0.0625f - m);
-    float vf[4];
-    fp8x4_to_f32(vw[b], vf);
-    l += p;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) o[d] += p * vf[d];
-  }
-  if (lane == 0) {
-    s_m[wave] = m;
-    s_l[wave] = l;
-  }
-#pragma unroll
-  for (int d = 0; d < 4; ++d) s_o[wave][4 * lane + d] = o[d];
   __syncthreads();
-  const int d = threadIdx.x;
-  const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-  float lsum = 0.f, acc = 0.f;
-  for (int w = 0; w < 4; ++w) {
-    if (s_m[w] == -INFINITY) continue;
-    const float sc = __expf(s_m[w] - M);
-    lsum += s_l[w] * sc;
-    acc += s_o[w][d] * sc;
+  // attention over the selected keys, merged with the sink/local slices
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = g * H + h;
+  float q[4];
+  load_q4(a, j, q);
+  const int i = wave * SDPA_WAVE_KEYS + lane;
+  const int tk = (lane < SDPA_WAVE_KEYS && i < TOPK) ? s_tok[i] : -1;
+  float mw, lw, ow[4];
+  wave_attend(a.kv8 + (size_t)g * a.T * 512, q, tk, mw, lw, ow);
+  stash_wave(att, mw, lw, ow);
+  __syncthreads();
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    float M, L, O;
+    merge_waves(att, d, M, L, O);
+    const float* parts = a.dense_part + (size_t)j * a.dense_slices * (D + 2);
+    float Mt = M;
+    for (int r = 0; r < a.dense_slices; ++r) Mt = fmaxf(Mt, parts[r * (D + 2) + D]);
+    float Lt = 0.f, Ot = 0.f;
+    if (M != -INFINITY) {
+      const float sc = __expf(M - Mt);
+      Lt = L * sc;
+      Ot = O * sc;
+    }
+    for (int r = 0; r < a.dense_slices; ++r) {
+      const float mr = parts[r * (D + 2) + D];
+      if (mr == -INFINITY) continue;
+      const float sc = __expf(mr - Mt);
+      Lt += parts[r * (D + 2) + D + 1] * sc;
+      Ot += parts[r * (D + 2) + d] * sc;
+    }
+    a.out[j * D + d] = (uint16_t)bf16_rne(Ot / Lt);
   }
-  float* part = a.attn_part + ((size_t)j * a.sdpa_split + s) * (D + 2);
-  part[d] = acc;
-  if (d == 0) {
-    part[D] = M;
-    part[D + 1] = lsum;
-  }
-}
-
-// Merge the slices of each query head: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
-__global__ __launch_bounds__(256) void k_sdpa_merge(StepArgs a) {
-  const int j = blockIdx.x, d = threadIdx.x;
-  const float* parts = a.attn_part + (size_t)j * a.sdpa_split * (D + 2);
-  float M = -INFINITY;
-  for (int p = 0; p < a.sdpa_split; ++p) M = fmaxf(M, parts[p * (D + 2) + D]);
-  float lsum = 0.f, acc = 0.f;
-  for (int p = 0; p < a.sdpa_split; ++p) {
-    const float mp = parts[p * (D + 2) + D];
-    if (mp == -INFINITY) continue;
-    const float sc = __expf(mp - M);
-    lsum += parts[p * (D + 2) + D + 1] * sc;
-    acc += parts[p * (D + 2) + d] * sc;
-  }
-  a.out[j * D + d] = (uint16_t)bf16_rne(acc / lsum);
 }
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
     "qprep", "coarse", "thresh", "fine", "fine_select", "pool_count", "pool_emit",
-    "top1600", "union_u1", "score4", "top256", "union_u2", "score8", "top100", "sdpa",
-    "sdpa_merge"};
+    "top1600", "union_u1", "score4", "top256", "union_u2", "score8", "top100_sdpa"};
 
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
@@ -795,7 +856,8 @@ void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_
   mark();
   hipLaunchKernelGGL(k_coarse, dim3(tiles_blocks, G), dim3(256), 0, st, a);
   mark();
-  hipLaunchKernelGGL(k_thresh, dim3(G * H), dim3(SEL_BLOCK), (size_t)a.nc * 2, st, a);
+  hipLaunchKernelGGL(k_thresh, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
+                     (size_t)a.nc * 2, st, a);
   mark();
   hipLaunchKernelGGL(k_fine, dim3(tiles_blocks, G), dim3(256), 0, st, a);
   mark();
@@ -820,10 +882,6 @@ void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_
   hipLaunchKernelGGL(k_score8, dim3(U2_MAX / 64, G), dim3(256), 0, st, a);
   mark();
   hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_sdpa, dim3(a.sdpa_split, G * H), dim3(256), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_sdpa_merge, dim3(G * H), dim3(256), 0, st, a);
   mark();
 }
 

@@ -317,7 +317,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   a.words_u1 = words1;
   a.words_u2 = words2;
   a.pool_blocks = nc / 32;
-  a.sdpa_split = (a.sink + a.local + TOPK + 63) / 64;
+  a.dense_slices = (a.sink + a.local + 127) / 128;
 
   // ---- static arena
   Arena s;
@@ -361,7 +361,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.range_cnt = (int4*)ar.take((size_t)G * a.pool_blocks * 16);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
-    a.attn_part = (float*)ar.take((size_t)G * H * a.sdpa_split * (D + 2) * 4);
+    a.dense_part = (float*)ar.take((size_t)G * H * std::max(a.dense_slices, 1) * (D + 2) * 4);
     // one contiguous range cleared by k_qprep every step
     a.zero_words = (size_t)G * (nc / 32);
     a.zero_base = (uint32_t*)ar.take(a.zero_words * 4);
@@ -506,7 +506,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
            "\"n_centroids\": %d, \"nprobe\": [%d, %d, %d, %d], \"pool_buffer\": %d, "
            "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
            "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
-           "\"kernels_per_step\": 16, \"lds_per_block\": %zu, \"pool_lds_items\": %d}",
+           "\"kernels_per_step\": 14, \"lds_per_block\": %zu, \"pool_lds_items\": %d}",
            json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), T, a.sink, a.local,
            nc, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min, a.pool_capacity, np_max,
            h->static_bytes, h->work_bytes, h->lds_per_block, w.top_u1.lds_items);

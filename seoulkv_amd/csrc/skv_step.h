@@ -15,7 +15,7 @@
 //   k_top256         codegen/refinement_fusion.py:263-266,402-455
 //   k_score8         _kernels/stage16/seoulkv4_union_matrix.py:58-139
 //   k_top100         codegen/refinement_fusion.py:296-300,495-531
-//   k_sdpa           codegen/attention.py:35-201 (+ TTNN sparse_sdpa compute)
+//   k_thresh, k_top100  sparse SDPA: codegen/attention.py:35-201 (+ TTNN sparse_sdpa)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -46,7 +46,7 @@ struct StepArgs {
   int pool_min, pool_capacity, debug;
   int pool_blocks;          // nc / 32: 32-centroid ranges of the pool kernels
   int words_u1, words_u2;   // bitmap words per (group, head)
-  int sdpa_split;           // 64-key slices per query head: ceil((S + L + 100) / 64)
+  int dense_slices;         // 128-key sink/local attention slices per query head
   // static device data
   const uint16_t* q;        // [16][256] bf16 (bound query)
   const float* kscale;      // [G][256]
@@ -76,7 +76,7 @@ struct StepArgs {
   uint16_t* s2;             // [G][H][cap] ordered
   uint64_t* bm_u1;          // [G][H][words_u1] top-1600 members
   uint64_t* bm_u2;          // [G][H][words_u2] top-256 members
-  float* attn_part;         // [16][sdpa_split][D + 2] partial (o, max, sum)
+  float* dense_part;        // [16][dense_slices][D + 2] sink/local partial (o, max, sum)
   // zeroed by k_qprep every step (one contiguous range)
   uint32_t* zero_base;
   size_t zero_words;
@@ -120,7 +120,7 @@ struct StepWork {
   size_t union_u1_lds, union_u2_lds;  // dynamic LDS bytes of the union kernels
 };
 
-constexpr int N_STEP_KERNELS = 16;
+constexpr int N_STEP_KERNELS = 14;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev);
