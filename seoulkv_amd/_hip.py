@@ -119,39 +119,48 @@ def _np(t: torch.Tensor, dtype) -> np.ndarray:
     return np.ascontiguousarray(t.numpy()).view(dtype)
 
 
+def index_desc(index, *, pool_min: int, pool_capacity: int | None, debug: bool):
+    """``skv_index_desc`` of a :class:`SeoulKV4Index`.  Returns ``(desc, keep)``;
+    the numpy arrays in ``keep`` back the descriptor's pointers and must
+    outlive every call that reads it."""
+    cells = index.cells
+    zones = index.zones
+    keep = []
+    desc = IndexDesc()
+    desc.context = zones.context
+    desc.sink = zones.sink
+    desc.local = zones.local
+    desc.n_centroids = len(cells[0]["centroids"])
+    desc.pool_min = int(pool_min)
+    desc.pool_capacity = int(pool_capacity or 0)
+    desc.debug = int(bool(debug))
+    for g, cell in enumerate(cells):
+        arrays = dict(
+            upper=_np(cell["upper"], np.uint8),
+            lower=_np(cell["lower"], np.uint8),
+            scale=_np(cell["scale"].float(), np.float32),
+            resid_f16=_np(cell["coarse_residual_norm"].half(), np.uint16),
+            gfs_f16=_np(cell["group_fine_scale"].half(), np.uint16),
+            offsets=_np(cell["offsets"].int(), np.int32),
+            values=_np(cell["values"].int(), np.int32),
+        )
+        keep.append(arrays)
+        c = desc.cells[g]
+        for name, arr in arrays.items():
+            setattr(c, name, _ptr(arr))
+        c.nprobe = int(cell["p"])
+        c.lam = float(cell["lam"])
+    return desc, keep
+
+
 class Runtime:
     """One device instance of the decode path (the reference's ``state``)."""
 
     def __init__(self, device: int, k: torch.Tensor, v: torch.Tensor, index, *,
                  pool_min: int, pool_capacity: int | None, debug: bool, stream=None):
         self.lib = load_library()
-        cells = index.cells
-        zones = index.zones
-        keep = []  # numpy arrays must outlive skv_create
-        desc = IndexDesc()
-        desc.context = zones.context
-        desc.sink = zones.sink
-        desc.local = zones.local
-        desc.n_centroids = len(cells[0]["centroids"])
-        desc.pool_min = int(pool_min)
-        desc.pool_capacity = int(pool_capacity or 0)
-        desc.debug = int(bool(debug))
-        for g, cell in enumerate(cells):
-            arrays = dict(
-                upper=_np(cell["upper"], np.uint8),
-                lower=_np(cell["lower"], np.uint8),
-                scale=_np(cell["scale"].float(), np.float32),
-                resid_f16=_np(cell["coarse_residual_norm"].half(), np.uint16),
-                gfs_f16=_np(cell["group_fine_scale"].half(), np.uint16),
-                offsets=_np(cell["offsets"].int(), np.int32),
-                values=_np(cell["values"].int(), np.int32),
-            )
-            keep.append(arrays)
-            c = desc.cells[g]
-            for name, arr in arrays.items():
-                setattr(c, name, _ptr(arr))
-            c.nprobe = int(cell["p"])
-            c.lam = float(cell["lam"])
+        desc, keep = index_desc(index, pool_min=pool_min, pool_capacity=pool_capacity,
+                                debug=debug)
         kb = _np(k, np.uint16)
         vb = _np(v, np.uint16)
         handle = ctypes.c_void_p()
