@@ -131,6 +131,36 @@ def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
     }, match, out
 
 
+def calibrate_copy(mib: int) -> int:
+    """Copy ``mib`` MiB between two device buffers 5 times: a dispatch that
+    reads and writes exactly ``mib`` MiB, for scaling the HBM counters."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "dispatches": 5}), flush=True)
+    return 0
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (``profiles/hbm_traffic_cfg2.txt``: lines ``traffic <kernel> <bytes>``),
+    or None when that kernel was not measured."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_cfg2.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -140,6 +170,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--build-device", default="cpu")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 5 times (the known-size "
+                         "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -153,6 +186,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
 
     t0 = time.time()
     p, k, v, qs = make_profile(args.config, n_queries=1)
@@ -264,7 +299,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dominant),
             "kernel_us": round(dom_us, 2),
             "bytes_per_launch": int(nbytes.get(dominant, 0)),
         },

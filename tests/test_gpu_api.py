@@ -1,0 +1,155 @@
+"""The public API on the GPU: lifecycle, borrowed results, the reference's
+error paths (pool below the minimum, pool above capacity: "never truncate"),
+the device-resident query binding, and full-pipeline parity at BASELINE
+configurations 1 and 2 (T = 32K and 128K) through the same entry points a
+caller uses."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+from seoulkv_amd import SeoulKV4, SeoulKV4Config, _hip
+from tests.helpers import bits, case, cosine, oracle_step
+
+pytestmark = pytest.mark.gpu
+
+P0 = dict(context=8192, components=256, nc=512, nprobe=64)
+P1 = dict(context=32768, components=1024, nc=2048, nprobe=384)
+
+
+def _check_output(got, ref):
+    got = got.float().numpy().reshape(16, 256)
+    for j in range(16):
+        assert np.abs(got[j] - ref[j]).max() <= 2e-2, f"head {j} max-abs"
+        assert cosine(got[j], ref[j]) >= 0.999, f"head {j} cosine"
+
+
+def _top100(traces):
+    return torch.tensor(np.stack([t.top100 for t in traces]), dtype=torch.long)
+
+
+def test_lifecycle_and_borrowed_results():
+    index, k, v, qs = case(**P0)
+    print("[gpu] lifecycle cfg0", flush=True)
+    with SeoulKV4(device="cuda:0", k=k, v=v, index=index,
+                  config=SeoulKV4Config(debug=True)) as skv:
+        r0 = skv.run(qs[0])
+        assert skv.initialized
+        out0 = r0.to_torch()
+        assert out0.shape == (1, 1, 16, 256) and out0.dtype == torch.bfloat16
+        traces, ref = oracle_step(P0, qs[0])
+        _check_output(out0, ref)
+        assert torch.equal(skv.debug_snapshot()["selected_ids"], _top100(traces))
+        views = r0.device_tensors
+        assert len(views) == 4 and all(t.shape == (1, 4, 256) for t in views)
+        assert torch.equal(torch.cat([t[0] for t in views]).cpu(), out0.reshape(16, 256))
+        r1 = skv.run(qs[1])
+        with pytest.raises(RuntimeError):
+            r0.to_torch()  # borrowed output: superseded by the next run
+        traces, ref = oracle_step(P0, qs[1])
+        _check_output(r1.to_torch(), ref)
+        assert torch.equal(skv.debug_snapshot()["selected_ids"], _top100(traces))
+        meta = skv.metadata()
+        assert meta["initialized"] and meta["runtime"]["kernels_per_step"] == 14
+    with pytest.raises(RuntimeError):
+        r1.to_torch()  # closed
+    with pytest.raises(RuntimeError):
+        skv.run(qs[0])
+
+
+def test_debug_snapshot_requires_debug_config():
+    index, k, v, qs = case(**P0)
+    skv = SeoulKV4(device=0, k=k, v=v, index=index)
+    skv.run(qs[0]).to_torch()
+    with pytest.raises(RuntimeError):
+        skv.debug_snapshot()
+    skv.close()
+
+
+def test_pool_below_minimum_raises():
+    p = dict(context=8192, components=256, nc=1024, nprobe=16)  # pools of ~700 keys
+    index, k, v, qs = case(**p)
+    print("[gpu] pool underflow", flush=True)
+    skv = SeoulKV4(device=0, k=k, v=v, index=index)
+    with pytest.raises(ValueError, match="never truncate"):
+        skv.run(qs[0])
+    assert not skv.initialized
+    skv.close()
+
+
+def test_capacity_error_then_hbm_sized_pool_at_config1():
+    index, k, v, qs = case(**P1)
+    print("[gpu] capacity cfg1", flush=True)
+    skv = SeoulKV4(device=0, k=k, v=v, index=index)  # reference capacity 13056
+    with pytest.raises(ValueError, match="never truncate"):
+        skv.run(qs[0])
+    skv.close()
+    print("[gpu] parity cfg1 (HBM-sized pool)", flush=True)
+    skv = SeoulKV4(device=0, k=k, v=v, index=index,
+                   config=SeoulKV4Config(stage15_capacity=None, debug=True))
+    for q in qs:
+        out = skv.run(q).to_torch()
+        traces, ref = oracle_step(P1, q)
+        assert torch.equal(skv.debug_snapshot()["selected_ids"], _top100(traces))
+        _check_output(out, ref)
+    skv.close()
+
+
+def test_device_query_binding_matches_host_binding():
+    index, k, v, qs = case(**P0)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    try:
+        rt.bind_query(qs[0])
+        rt.enqueue()
+        rt.synchronize()
+        host_out, host_ids = rt.read_output(), rt.debug_ids()
+        rt.bind_query(qs[1])  # overwrite, then bind the device copy of q0
+        rt.enqueue()
+        rt.synchronize()
+        qd = qs[0].reshape(16, 256).to("cuda:0")
+        rt.bind_query_device(qd)
+        rt.enqueue()
+        rt.synchronize()
+        assert torch.equal(rt.read_output(), host_out)
+        assert torch.equal(rt.debug_ids(), host_ids)
+    finally:
+        rt.close()
+
+
+@pytest.mark.slow
+def test_full_size_parity_config2():
+    """BASELINE configuration 2 (T = 131072, nc = 8192, P = 384), every stage
+    bit-exact against the oracle on the same seeded inputs."""
+    from seoulkv_amd.index import SeoulKV4Index
+    from seoulkv_amd.synthetic import make_profile
+
+    print("[gpu] cfg2 inputs", flush=True)
+    prof, k, v, qs = make_profile("cfg2")
+    index = SeoulKV4Index.build(k, v, sink=prof.sink, local=prof.local, nprobe=prof.nprobe,
+                                n_centroids=prof.n_centroids)
+    print("[gpu] cfg2 oracle", flush=True)
+    kb, vb = bits(k), bits(v)
+    code8, scales = od.key_codec(kb)
+    k8, v8 = od.fp8_records(kb, vb)
+    cells = [od.GroupCell.from_cell(c) for c in index.cells]
+    traces, ref = od.decode_step(cells, code8, scales, k8, v8, bits(qs[0]).reshape(16, 256),
+                                 sink=prof.sink, local=prof.local)
+    print("[gpu] cfg2 device step", flush=True)
+    rt = _hip.Runtime(0, k, v, index, pool_min=2048, pool_capacity=None, debug=True)
+    try:
+        rt.bind_query(qs[0])
+        rt.enqueue()
+        status = rt.synchronize()
+        assert status["err"] == [0, 0, 0, 0]
+        for g, tr in enumerate(traces):
+            np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected)
+            np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool)
+            np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1)
+            np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2)
+            np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
+        _check_output(rt.read_output(), ref)
+    finally:
+        rt.close()
