@@ -40,7 +40,7 @@ def log(msg: str) -> None:
 def kernel_bytes(status: dict, p, nc: int) -> dict:
     """Algorithmic HBM bytes of each kernel for one step (all 4 KV groups),
     from the live stage sizes.  Reads of each input once plus the outputs the
-    next stage needs; see DESIGN.md for the per-unit figures."""
+    next stage needs."""
     G, H = 4, 4
     surv = sum(status["survivors"])
     sel = sum(status["selected"])
@@ -55,8 +55,10 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         "qprep": 16 * 256 * 2 + G * 256 * 4 + bimg,
         # 2-bit upper plane, group scale, residual norm in; lower+upper out
         "coarse": G * nc * (64 + 4 + H * 4) + G * (nc // 32) * 4 + G * 4096,
-        # lower bounds in
-        "thresh": G * H * nc * 2,
+        # lower bounds in; the extra blocks' sink/local FP8 [V||K] records
+        # (once per group) in and their slice partials out
+        "thresh": G * H * nc * 2 + G * (p.sink + p.local) * 512
+        + 16 * ((p.sink + p.local + 127) // 128) * 258 * 4,
         # both planes + upper bounds in; fine scores + masks out
         "fine": G * nc * (128 + H * 2 + H * 2 + 1) + G * 4096,
         # fine scores (+ masks once) in; selected bitmap out
@@ -66,19 +68,18 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         # CSR, mates, tokens, 64 B prefix rows in; pool tokens + scores out
         "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4 + 64) + pool * (4 + H * 2),
         # pool scores in; member bitmaps out
-        "top1600": pool * H * 2 + G * H * 4096 * 4 + G * H * pool // 8,
-        "union_u1": G * H * pool // 8 + u1 * 8,
-        # U1 tokens + 128 B (prefix | residual-2) rows in; scores out
-        "score4": u1 * (4 + 128 + H * 2),
+        "top1600": pool * H * 2 + G * H * pool // 8,
+        # member bitmaps + pool tokens in; U1 tokens, their 128 B (prefix |
+        # residual-2) key rows in; U1 tokens and 4-bit scores out
+        "union_score4": G * H * pool // 8 + u1 * (4 + 4 + 128 + H * 2),
         "top256": u1 * (4 + H * 2) + G * H * u1 // 8,
-        "union_u2": G * H * u1 // 8 + u2 * 8,
-        # U2 tokens + full 256 B key records in; scores out
-        "score8": u2 * (4 + 256 + H * 2),
-        "top100": u2 * (4 + H * 2) + 16 * 100 * 4,
-        # unique FP8 [V||K] records: shared sink/local per group + 100 per head
-        "sdpa": G * (p.sink + p.local) * 512 + 16 * 100 * 512 + 16 * 256 * 4,
-        # slice partials in, BF16 output out
-        "sdpa_merge": 16 * ((p.sink + p.local + 100 + 63) // 64) * 258 * 4 + 16 * 256 * 2,
+        # member bitmaps + U1 tokens in; full 256 B key records in; U2 tokens
+        # and 8-bit scores out
+        "union_score8": G * H * u1 // 8 + u2 * (4 + 4 + 256 + H * 2),
+        # U2 scores + tokens in, top-100 IDs out; the 100 FP8 [V||K] records of
+        # each head, the sink/local slice partials in; BF16 output out
+        "top100_sdpa": u2 * (4 + H * 2) + 16 * 100 * 4 + 16 * 100 * 512
+        + 16 * ((p.sink + p.local + 127) // 128) * 258 * 4 + 16 * 256 * 2,
     }
 
 
@@ -179,7 +180,8 @@ def main() -> int:
         print(
             "bench.py measures one MI355X: this build runs one GPU per process and the "
             "4 KV groups of a layer on that GPU; multi-GPU (--gpus > 1) is not part of "
-            "this build (see DESIGN.md for how the path would shard).",
+            "this build: the 4 KV groups would shard one per GPU with a single 8 KiB "
+            "all-gather of the outputs.",
             file=sys.stderr,
         )
         return 2

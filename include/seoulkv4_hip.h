@@ -86,8 +86,10 @@ int skv_bind_query_device(void *handle, const void *q_dev);
 int skv_enqueue(void *handle);
 
 /* Reference synchronize (api.py:112-115).  Waits for the stream and, if
- * status is non-NULL, stores the per-group device status words
- * [4][8] (see skv_status fields in DESIGN.md: pool size, error code, counts). */
+ * status is non-NULL, stores the per-group device status words [4][8]:
+ * 0 pool size, 1 error code (0, 4 pool above capacity, 5 pool below the
+ * minimum), 2 selected clusters, 3 coarse survivors, 4 |U1|, 5 |U2|,
+ * 6 postings scanned, 7 full-selection bits (see skv_select_mode). */
 int skv_sync(void *handle, int32_t *status);
 
 /* Device pointer of the output [16][256] BF16 (valid until skv_destroy;
@@ -132,6 +134,16 @@ int skv_read_stage(void *handle, int stage, int group, void *host_out,
  * (re)starts the accumulation; skv_profile_read syncs and returns the mean
  * milliseconds of each kernel over the profiled steps (n >= skv_kernel_count()). */
 int skv_profile(void *handle, int enable);
+
+/* Selection path (diagnostic; no counterpart in the reference, whose
+ * TopK-XL trees always rank every item).  Each top-k of the step first tries
+ * a cut estimated from a 4096-item sample and falls back to the full
+ * selection when the sample misses; both give identical results.  exact = 1
+ * always runs the full selection; exact = 2 (tests) makes every sampled cut
+ * miss so the fallback runs; 0 restores the default.  Status word 7 of each group (see skv_sync)
+ * records, one bit per stage (1 thresh, 2 fine select, 4 top-1600, 8 top-256,
+ * 16 top-100), which selections of the last step took the full path. */
+int skv_select_mode(void *handle, int exact);
 int skv_profile_read(void *handle, float *mean_ms, int n, int32_t *steps);
 int skv_kernel_count(void);
 const char *skv_kernel_name(int i);

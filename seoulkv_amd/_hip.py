@@ -26,7 +26,7 @@ STAGES = {
     "pool": 7, "s2": 8, "u1": 9, "s4": 10, "u2": 11, "s8": 12, "top": 13,
     "qprep": 14, "keyrec": 15, "kv8": 16, "kscale": 17,
 }
-STATUS_FIELDS = ("pool", "err", "selected", "survivors", "u1", "u2", "scanned", "reserved")
+STATUS_FIELDS = ("pool", "err", "selected", "survivors", "u1", "u2", "scanned", "full_select")
 ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "out of device memory",
           4: "pool above capacity", 5: "pool below minimum", 6: "invalid state"}
 
@@ -84,6 +84,7 @@ def load_library() -> ctypes.CDLL:
         "skv_debug_ids": (i32, [vp, vp]),
         "skv_read_stage": (i32, [vp, i32, i32, vp, i64, ctypes.POINTER(i64)]),
         "skv_profile": (i32, [vp, i32]),
+        "skv_select_mode": (i32, [vp, i32]),
         "skv_profile_read": (i32, [vp, vp, i32, vp]),
         "skv_kernel_count": (i32, []),
         "skv_kernel_name": (ctypes.c_char_p, [i32]),
@@ -196,6 +197,11 @@ class Runtime:
             raise ValueError("expected a device BF16 Q with 16 x 256 elements")
         q_dev = q_dev.contiguous()
         self._check(self.lib.skv_bind_query_device(self.handle, q_dev.data_ptr()), "bind_query")
+
+    def select_mode(self, mode: int) -> None:
+        """0: sampled cut with full fallback (default); 1: full selection
+        only; 2: every sampled cut forced to miss (exercises the fallback)."""
+        self._check(self.lib.skv_select_mode(self.handle, int(mode)), "select_mode")
 
     def enqueue(self) -> None:
         self._check(self.lib.skv_enqueue(self.handle), "enqueue")

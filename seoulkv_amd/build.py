@@ -41,9 +41,13 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the SeoulKV4 HIP library cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
+def build(verbose: bool = False, trace: bool = False) -> Path:
+    """Compile the library; ``trace`` builds the phase-timestamp variant
+    ``libseoulkv4_hip_trace.so`` (development only) instead."""
+    lib = LIB.with_name("libseoulkv4_hip_trace.so") if trace else LIB
+    tmp = lib.with_suffix(".so.tmp")
+    extra = ["-DSKV_TRACE"] if trace else []
+    cmd = [hipcc(), *FLAGS, *extra, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,9 +59,9 @@ def build(verbose: bool = False) -> Path:
         lines = [l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l]
         if lines:
             print("\n".join(lines))
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, trace="--trace" in sys.argv[1:]))

@@ -15,6 +15,22 @@
 
 namespace skv {
 
+// Phase timestamps for development builds (-DSKV_TRACE): thread 0 of block
+// (0, 0) stores the 100 MHz real-time counter at point i of kernel slot k;
+// skv_trace_read copies the table out.  Compiled out otherwise.
+#ifdef SKV_TRACE
+extern __device__ unsigned long long g_skv_trace[32][16];
+#define SKV_TS(k, i)                                                           \
+  do {                                                                         \
+    if ((k) >= 0 && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)   \
+      g_skv_trace[(k)][(i)] = __builtin_amdgcn_s_memrealtime();                \
+  } while (0)
+#else
+#define SKV_TS(k, i) \
+  do {               \
+  } while (0)
+#endif
+
 constexpr int G = 4;          // KV heads (index cells)
 constexpr int H = 4;          // query heads per KV head
 constexpr int D = 256;        // head dimension

@@ -1,0 +1,298 @@
+// Exact block top-k by (ordered BF16 score desc, ID asc) from a sampled cut.
+//
+// 1. Sample: 4096 items (all of them when n <= 4096, else the items at
+//    floor(j n / 4096)) are histogrammed in LDS (12-bit bins, then the low 4
+//    bits of the chosen bin) to find a score `cut` that about
+//    k + 4 sqrt(k) + 8 items are expected to reach (exactly the k-th best
+//    score when the sample is the whole input).
+// 2. Candidates: one pass over all n scores appends every item scoring
+//    >= cut to an LDS list (one atomic per wave), then loads their IDs.
+// 3. If the list holds fewer than k items (the sample over-estimated the
+//    cut) or overflows, the caller runs the full exact selection instead.
+//    Otherwise the top k of the input are exactly the top k of the list
+//    (every other item scores below cut <= every candidate), found by a
+//    histogram over the candidates' scores and, for ties at the k-th score,
+//    a rank of the tied IDs.
+// The result is therefore identical to a full selection; only the time
+// depends on the sample.
+#pragma once
+
+#include "skv_select.h"
+
+namespace skv {
+
+constexpr int FS_SAMPLE = 4096;
+constexpr int FS_PER = FS_SAMPLE / SEL_BLOCK;  // sample items per thread
+constexpr int CAND_CAP = 4096;
+constexpr int FS_TIE_WAVE = 64;  // ties ranked inside one wave up to this count
+
+struct FastScratch {
+  union {
+    uint32_t hist[4096];
+    KthScratch k;
+  };
+  uint64_t cand[CAND_CAP];  // ord << 40 | (0xfffff - id) << 20 | position
+  uint32_t hist4[16];
+  uint32_t tie[FS_TIE_WAVE];
+  int ncand;
+  int maxo;
+  int ntie;
+  int sel[4];
+  int scan[SEL_WAVES + 1];
+};
+
+struct FastResult {
+  Selection sel;  // members are the candidates with sel.member(ord, id)
+  int ncand;      // candidates in FastScratch::cand
+  bool ok;        // false: use the full selection
+};
+
+__device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40); }
+__device__ __forceinline__ uint32_t cand_id(uint64_t c) {
+  return 0xfffffu - (uint32_t)((c >> 20) & 0xfffffu);
+}
+__device__ __forceinline__ int cand_pos(uint64_t c) { return (int)(c & 0xfffffu); }
+
+// Descending scan of a 4096-bin histogram (each thread owns 8 bins): the bin
+// holding the rank-th largest value and the count in higher bins, in
+// s.sel[0..1]; sel[0] = -1 if the histogram holds fewer than rank values.
+// s.sel[2] = total count.
+__device__ __forceinline__ void fs_rank_bin(FastScratch& s, int rank) {
+  constexpr int PER = 4096 / SEL_BLOCK;
+  const int top = 4095 - PER * (int)threadIdx.x;
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) c += s.hist[top - j];
+  int total;
+  const int exc = block_excl_scan(c, s.scan, &total);
+  if (exc < rank && rank <= exc + c) {
+    int acc = exc, bin = top;
+    for (int j = 0; j < PER; ++j) {
+      const int cnt = s.hist[top - j];
+      if (acc + cnt >= rank) { bin = top - j; break; }
+      acc += cnt;
+    }
+    s.sel[0] = bin;
+    s.sel[1] = acc;
+  }
+  if (threadIdx.x == 0) {
+    s.sel[2] = total;
+    if (total < rank) s.sel[0] = -1;
+  }
+}
+
+// Digit (0..15) of the rank-th largest value in s.hist4: s.sel[0] = digit,
+// s.sel[1] += count in higher digits, s.sel[3] = count at the digit.
+__device__ __forceinline__ void fs_rank_digit(FastScratch& s, int rank, int acc) {
+  if (threadIdx.x == 0) {
+    int a = acc, d = 0, cnt = 0;
+    for (int j = 15; j >= 0; --j) {
+      cnt = s.hist4[j];
+      if (a + cnt >= rank) { d = j; break; }
+      a += cnt;
+    }
+    s.sel[0] = d;
+    s.sel[1] = a;
+    s.sel[3] = cnt;
+  }
+}
+
+// score(i): ordered score of item i < n (0 = excluded), a single load.
+// load8(o, out): ordered scores of items 8o .. 8o+7 (0 beyond n).
+// id(i): the item's ID (< 2^20), read only for candidates.
+// force_miss places the cut at the best sampled score (a test of the
+// fallback: fewer than k candidates unless k ties share that score).
+template <typename ScoreFn, typename Load8Fn, typename IdFn>
+__device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, IdFn id,
+                                  FastScratch& s, bool force_miss = false, int ts = -1) {
+  FastResult res;
+  res.ok = true;
+  res.ncand = 0;
+  res.sel.idcut = 0xffffffffu;
+  res.sel.all = false;
+  res.sel.above = 0;
+  const bool full = n <= FS_SAMPLE;
+
+  // ---- 1. sample
+  uint32_t sv[FS_PER];
+#pragma unroll
+  for (int u = 0; u < FS_PER; ++u) {
+    const int j = (int)threadIdx.x + u * SEL_BLOCK;
+    const int i = full ? j : (int)(((uint64_t)j * (uint64_t)n) >> 12);
+    sv[u] = (full && j >= n) ? 0u : score(i);
+  }
+  for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
+  if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    s.ncand = 0;
+    s.maxo = 0;
+    s.ntie = 0;
+    s.sel[0] = -1;
+    s.sel[1] = 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < FS_PER; ++u)
+    if (sv[u]) atomicAdd(&s.hist[sv[u] >> 4], 1u);
+  __syncthreads();
+  SKV_TS(ts, 1);
+  int rank = k;
+  if (!full) {
+    const float e = (float)k * (float)FS_SAMPLE / (float)n;
+    rank = (int)ceilf(e + 4.f * sqrtf(e) + 8.f);
+  }
+  if (force_miss) rank = 1;
+  fs_rank_bin(s, rank);
+  __syncthreads();
+  const int b1 = s.sel[0];
+  uint32_t cut = 1;  // every valid item
+  if (b1 >= 0) {
+    const int acc1 = s.sel[1];
+#pragma unroll
+    for (int u = 0; u < FS_PER; ++u)
+      if (sv[u] && (int)(sv[u] >> 4) == b1) atomicAdd(&s.hist4[sv[u] & 15], 1u);
+    __syncthreads();
+    fs_rank_digit(s, rank, acc1);
+    __syncthreads();
+    cut = ((uint32_t)b1 << 4) | (uint32_t)s.sel[0];
+  }
+  __syncthreads();
+  SKV_TS(ts, 2);
+
+  // ---- 2. candidates (positions and scores), then their IDs
+  {
+    const int lane = threadIdx.x & 63;
+    const int no = (n + 7) >> 3;
+    uint32_t mx = 0;
+    for (int base = threadIdx.x & ~63; base < no; base += 2 * SEL_BLOCK) {
+      uint32_t v[2][8];
+      int cnt = 0;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int o = base + r * SEL_BLOCK + lane;
+        if (o < no) {
+          load8(o, v[r]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[r][e] = 0;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool c = v[r][e] >= cut && v[r][e] != 0;
+          cnt += c;
+          if (c) mx = max(mx, v[r][e]);
+        }
+      }
+      const int inc = wave_incl_scan(cnt);
+      int wbase = 0;
+      if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
+      wbase = __shfl(wbase, 63, WAVE);
+      int slot = wbase + inc - cnt;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int o = base + r * SEL_BLOCK + lane;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (v[r][e] >= cut && v[r][e] != 0) {
+            if (slot < CAND_CAP) s.cand[slot] = ((uint64_t)v[r][e] << 40) | (uint64_t)(8 * o + e);
+            ++slot;
+          }
+        }
+      }
+    }
+    mx = (uint32_t)wave_max((int)mx);
+    if (lane == 0) atomicMax(&s.maxo, (int)mx);
+  }
+  __syncthreads();
+  SKV_TS(ts, 3);
+  const int nc = s.ncand;
+  res.ncand = nc;
+  if (nc > CAND_CAP || (cut > 1 && nc < k)) {
+    res.ok = false;
+    return res;
+  }
+  for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
+    const uint64_t key = s.cand[c];
+    s.cand[c] = key | ((uint64_t)(0xfffffu - id(cand_pos(key))) << 20);
+  }
+  if (cut == 1 && nc <= k) {  // fewer valid items than k: all are members
+    res.sel.all = true;
+    res.sel.v = 0;
+    res.sel.above = nc;
+    __syncthreads();
+    return res;
+  }
+
+  SKV_TS(ts, 4);
+  // ---- 3. exact k-th score among the candidates (nc >= k here)
+  const uint32_t maxo = (uint32_t)s.maxo;
+  int shift = 0;
+  while (((maxo - cut) >> shift) >= 4096u) ++shift;
+  for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
+  if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
+  __syncthreads();
+  for (int c = threadIdx.x; c < nc; c += SEL_BLOCK)
+    atomicAdd(&s.hist[(cand_ord(s.cand[c]) - cut) >> shift], 1u);
+  __syncthreads();
+  fs_rank_bin(s, k);
+  __syncthreads();
+  const int b2 = s.sel[0];
+  int above = s.sel[1];
+  uint32_t v;
+  int ties;
+  if (shift == 0) {
+    v = cut + (uint32_t)b2;
+    ties = (int)s.hist[b2];
+    __syncthreads();
+  } else {
+    __syncthreads();
+    const uint32_t lowmask = (1u << shift) - 1u;
+    for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
+      const uint32_t d = cand_ord(s.cand[c]) - cut;
+      if ((int)(d >> shift) == b2) atomicAdd(&s.hist4[d & lowmask], 1u);
+    }
+    __syncthreads();
+    fs_rank_digit(s, k, above);
+    __syncthreads();
+    v = cut + (((uint32_t)b2 << shift) | (uint32_t)s.sel[0]);
+    above = s.sel[1];
+    ties = s.sel[3];
+    __syncthreads();
+  }
+  res.sel.v = v;
+  res.sel.above = above;
+  SKV_TS(ts, 5);
+  const int need = k - above;
+  if (need >= ties) return res;  // every tie is a member
+
+  // ---- ties at v: the `need` lowest IDs win
+  if (ties <= FS_TIE_WAVE) {
+    for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
+      const uint64_t key = s.cand[c];
+      if (cand_ord(key) == v) s.tie[atomicAdd(&s.ntie, 1)] = cand_id(key);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      const uint32_t x = lane < ties ? s.tie[lane] : 0xffffffffu;
+      int r = 0;
+      for (int j = 0; j < 64; ++j) r += (uint32_t)__shfl((int)x, j, WAVE) < x;
+      if (lane < ties && r == need - 1) s.sel[2] = (int)x;
+    }
+    __syncthreads();
+    res.sel.idcut = (uint32_t)s.sel[2];
+    __syncthreads();
+    return res;
+  }
+  auto val = [&](int c, uint64_t* out) {
+    const uint64_t key = s.cand[c];
+    if (cand_ord(key) != v) return false;
+    *out = 0xfffffu - cand_id(key);
+    return true;
+  };
+  const uint64_t kth = block_kth<24>(nc, need, val, s.k);
+  res.sel.idcut = 0xfffffu - (uint32_t)kth;
+  return res;
+}
+
+}  // namespace skv

@@ -12,10 +12,9 @@
 //   pool_emit   selected list + pool tokens in encounter order, fused with
 //               the 2-bit scores of the owned postings (cluster-block rows)
 //   top1600     per head: top-1600 of the pool -> membership bitmap
-//   union_u1    U1 = union over heads, pool order
-//   score4      4-bit scores of U1
-//   top256      per head: top-256 of U1 -> bitmap;  union_u2 -> U2
-//   score8      8-bit scores of U2
+//   union_score4  U1 = union over heads in pool order + 4-bit scores of U1
+//   top256      per head: top-256 of U1 -> membership bitmap
+//   union_score8  U2 = union over heads in U1 order + 8-bit scores of U2
 //   top100      per head: best-first top-100 token IDs, then FP8 attention over
 //               them merged with the sink/local attention slices (computed
 //               by extra blocks of the thresh launch; they depend only on Q)
@@ -25,20 +24,27 @@
 // are exact integers on the int8 matrix cores (see skv_device.h).
 
 #include "skv_device.h"
+#include "skv_fastsel.h"
 #include "skv_select.h"
 #include "skv_step.h"
 
 namespace skv {
 
+#ifdef SKV_TRACE
+__device__ unsigned long long g_skv_trace[32][16];
+#endif
+
 // ============================================================ query prep
 // Grid (G, QV_COUNT), 256 threads: thread d owns dim d of the 4 heads.
 __global__ __launch_bounds__(256) void k_qprep(StepArgs a) {
+  SKV_TS(0, 0);
   const int g = blockIdx.x, v = blockIdx.y, d = threadIdx.x;
   const int lane = d & 63, wave = d >> 6;
   __shared__ int s_X[H][D];
   __shared__ int s_max[H][4];
   __shared__ long long s_sum[H][4], s_sq[H][4];
 
+  if (v == 0 && d == 0) a.status[g * ST_WORDS + ST_FULLSEL] = 0;
   {  // per-step counters: pool histograms, selected bitmap, SDPA tickets
     const int blk = g * QV_COUNT + v, nblk = G * QV_COUNT;
     for (size_t i = (size_t)blk * 256 + d; i < a.zero_words; i += (size_t)nblk * 256)
@@ -196,6 +202,7 @@ struct AttnScratch {
   float m[SEL_BLOCK / WAVE], l[SEL_BLOCK / WAVE];
   float o[SEL_BLOCK / WAVE][D];
 };
+static_assert(sizeof(AttnScratch) == ATTN_SCRATCH_BYTES, "attention scratch size");
 
 // Publish a wave partial to LDS; after a barrier, merge_waves gives thread
 // d < 256 the block's (max, sum, output[d]).
@@ -256,6 +263,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 // Wave tile: 16 centroids x 4 heads.  lower/upper = bf16(value -/+ margin),
 // value = RNE(sum q (2u - 3)) * scale/4, margin = ||q|| lambda bf16(resid).
 __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
+  SKV_TS(1, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -295,21 +303,51 @@ __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
   }
 }
 
+// Ordered scores of items 8o .. 8o+7 of a 16-byte aligned 16-bit row (0 past
+// n), each raw value mapped by xf.
+template <typename Fn>
+__device__ __forceinline__ void row_load8(const uint16_t* __restrict__ row, int n, int o, Fn xf,
+                                          uint32_t out[8]) {
+  const uint4 w = *reinterpret_cast<const uint4*>(row + 8 * o);
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    out[e] = 8 * o + e < n ? xf((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu) : 0u;
+}
+
+__device__ __forceinline__ uint32_t same16(uint32_t o) { return o; }
+
 // ============================================================ thresholds
 // Per (group, head): the P-th largest lower bound (its value only).  Blocks
 // beyond the 16 (group, head) pairs compute the sink/local attention slices.
 __global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
+  SKV_TS(2, 0);
+  extern __shared__ __align__(16) unsigned char dyn[];
   if (blockIdx.x >= G * H) {  // sink/local attention slices (depend only on Q)
-    __shared__ AttnScratch att;
-    dense_attend(a, blockIdx.x - G * H, att);
+    dense_attend(a, blockIdx.x - G * H, *reinterpret_cast<AttnScratch*>(dyn));
     return;
   }
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
-  extern __shared__ __align__(16) uint16_t so[];  // nc ordered lower bounds
   const uint16_t* lo = a.lower + ((size_t)g * H + h) * a.nc;
   // a non-NaN bound never maps to ordered 0, the "excluded" mark
-  load_lds_scores(so, lo, a.nc, [](uint32_t b) { return ordered16(b); });
+  auto xf = [](uint32_t b) { return ordered16(b); };
+  if (a.exact_select != 1) {
+    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    const FastResult r = fast_select(
+        a.nc, a.P[g], [&](int i) { return ordered16(lo[i]); },
+        [&](int o, uint32_t* out) { row_load8(lo, a.nc, o, xf, out); },
+        [](int i) { return (uint32_t)i; }, fs, a.exact_select == 2, 2);
+    if (r.ok) {
+      SKV_TS(2, 15);
+      if (threadIdx.x == 0) a.thr[g * H + h] = r.sel.all ? 0u : r.sel.v;
+      return;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) atomicOr(&a.status[g * ST_WORDS + ST_FULLSEL], FS_THRESH);
+  }
+  uint16_t* so = reinterpret_cast<uint16_t*>(dyn);  // nc ordered lower bounds
+  load_lds_scores(so, lo, a.nc, xf);
   __syncthreads();
   const Selection sel = block_select(so, a.nc, a.P[g], [](int i) { return (uint32_t)i; }, s);
   if (threadIdx.x == 0) a.thr[g * H + h] = sel.all ? 0u : sel.v;
@@ -320,6 +358,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
 // and the 4-bit score bf16(RNE(sum q (2 code4 - 15)) * group_fine_scale) of
 // each eligible head.  fine_ord[g][h][c] = ordered score, or 0 if ineligible.
 __global__ __launch_bounds__(256) void k_fine(StepArgs a) {
+  SKV_TS(3, 0);
   const int g = blockIdx.y, nc = a.nc;
   const int lane = threadIdx.x & 63;
   const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -369,17 +408,43 @@ __global__ __launch_bounds__(256) void k_fine(StepArgs a) {
 // Per (group, head): the P eligible centroids with the best (fine score,
 // lowest ID); members set their bit in the group's selected-cluster bitmap.
 __global__ __launch_bounds__(SEL_BLOCK) void k_fine_select(StepArgs a) {
+  SKV_TS(4, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H, nc = a.nc;
   __shared__ SelectScratch s;
-  extern __shared__ __align__(16) uint16_t so[];  // nc ordered fine scores
+  extern __shared__ __align__(16) unsigned char dyn[];
   const uint16_t* f = a.fine_ord + ((size_t)g * H + h) * nc;
-  load_lds_scores(so, f, nc, [](uint32_t o) { return o; });
-  __syncthreads();
-  const Selection sel = block_select(so, nc, a.P[g], [](int c) { return (uint32_t)c; }, s);
   uint32_t* selbm = a.selbm + (size_t)g * (nc / 32);
-  for_scores(so, nc, [&](int c, uint32_t o) {
-    if (sel.member(o, (uint32_t)c)) atomicOr(&selbm[c >> 5], 1u << (c & 31));
-  });
+  bool done = false;
+  if (a.exact_select != 1) {
+    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    const FastResult r = fast_select(
+        nc, a.P[g], [&](int i) { return (uint32_t)f[i]; },
+        [&](int o, uint32_t* out) { row_load8(f, nc, o, same16, out); },
+        [](int i) { return (uint32_t)i; }, fs, a.exact_select == 2, 4);
+    if (r.ok) {
+      SKV_TS(4, 6);
+      for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
+        const uint64_t key = fs.cand[c];
+        if (r.sel.member(cand_ord(key), cand_id(key))) {
+          const int cc = cand_pos(key);
+          atomicOr(&selbm[cc >> 5], 1u << (cc & 31));
+        }
+      }
+      done = true;
+    } else {
+      __syncthreads();
+      if (threadIdx.x == 0) atomicOr(&a.status[g * ST_WORDS + ST_FULLSEL], FS_FINE);
+    }
+  }
+  if (!done) {
+    uint16_t* so = reinterpret_cast<uint16_t*>(dyn);  // nc ordered fine scores
+    load_lds_scores(so, f, nc, same16);
+    __syncthreads();
+    const Selection sel = block_select(so, nc, a.P[g], [](int c) { return (uint32_t)c; }, s);
+    for_scores(so, nc, [&](int c, uint32_t o) {
+      if (sel.member(o, (uint32_t)c)) atomicOr(&selbm[c >> 5], 1u << (c & 31));
+    });
+  }
   if (h == 0) {  // survivors: centroids with a nonzero head mask
     __shared__ int s_cnt[SEL_WAVES + 1];
     const uint32_t* m4 = reinterpret_cast<const uint32_t*>(a.masks + (size_t)g * nc);
@@ -392,6 +457,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_fine_select(StepArgs a) {
     block_excl_scan(surv, s_cnt, &total);
     if (threadIdx.x == 0) a.status[g * ST_WORDS + ST_SURV] = total;
   }
+  SKV_TS(4, 15);
 }
 
 // ============================================================ pool
@@ -417,6 +483,7 @@ __device__ __forceinline__ void stage_range(const StepArgs& a, int g, int b, uin
 }
 
 __global__ __launch_bounds__(256) void k_pool_count(StepArgs a) {
+  SKV_TS(5, 0);
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
@@ -457,6 +524,7 @@ __global__ __launch_bounds__(256) void k_pool_count(StepArgs a) {
 // owned posting on the matrix cores from its cluster-block prefix row:
 // s2 = bf16(16 RNE(sum q15 (2 p2 - 3))).
 __global__ __launch_bounds__(256) void k_pool_emit(StepArgs a) {
+  SKV_TS(6, 0);
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
@@ -578,16 +646,50 @@ __global__ __launch_bounds__(256) void k_pool_emit(StepArgs a) {
 // n items; writes the membership bitmap.  LDS-resident when n <= lds_items,
 // otherwise 8-bit radix passes over the full 40-bit keys in memory.
 __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
+  const int ts = t.count_slot == ST_POOL ? 7 : 10;
+  SKV_TS(ts, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
-  extern __shared__ __align__(16) uint16_t so[];
+  extern __shared__ __align__(16) unsigned char dyn[];
   const int n = t.status[g * ST_WORDS + t.count_slot];
   const uint16_t* sc = t.scores + ((size_t)g * H + h) * t.stride;
   const int* tok = t.tokens + (size_t)g * t.stride;
   uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
   auto id = [&](int i) { return (uint32_t)tok[i]; };
+  if (t.exact_select != 1) {
+    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    const FastResult r = fast_select(
+        n, t.k, [&](int i) { return (uint32_t)sc[i]; },
+        [&](int o, uint32_t* out) { row_load8(sc, n, o, same16, out); }, id, fs,
+        t.exact_select == 2, ts);
+    if (r.ok) {
+      SKV_TS(ts, 6);
+      const int words = (n + 63) / 64;
+      // the histogram space is free after the selection: 2048 bitmap words
+      const bool local = words <= 2048;
+      uint64_t* mb = local ? reinterpret_cast<uint64_t*>(fs.hist) : bm;
+      for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
+      __syncthreads();
+      for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
+        const uint64_t key = fs.cand[c];
+        if (r.sel.member(cand_ord(key), cand_id(key))) {
+          const int p = cand_pos(key);
+          atomicOr(reinterpret_cast<unsigned long long*>(&mb[p >> 6]), 1ull << (p & 63));
+        }
+      }
+      if (local) {
+        __syncthreads();
+        for (int w = threadIdx.x; w < words; w += SEL_BLOCK) bm[w] = mb[w];
+      }
+      SKV_TS(ts, 15);
+      return;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) atomicOr(&t.status[g * ST_WORDS + ST_FULLSEL], t.fullsel_bit);
+  }
+  uint16_t* so = reinterpret_cast<uint16_t*>(dyn);
   if (n <= t.lds_items) {
-    load_lds_scores(so, sc, n, [](uint32_t o) { return o; });
+    load_lds_scores(so, sc, n, same16);
     __syncthreads();
     const Selection sel = block_select(so, n, t.k, id, s);
     write_members(so, n, sel, id, bm);
@@ -608,58 +710,6 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   }
 }
 
-// ============================================================ unions
-// Union of the four heads' member bitmaps in item order -> compact tokens.
-// Word popcounts are scanned in LDS; then thread t handles items t + 1024 j.
-__global__ __launch_bounds__(1024) void k_union(UnionArgs u) {
-  const int g = blockIdx.x;
-  extern __shared__ uint32_t s_dyn[];
-  __shared__ int s_scan[17];
-  const int n = u.status[g * ST_WORDS + u.slot_in];
-  const int words = (n + 63) / 64;
-  const bool in_lds = words <= u.lds_words;
-  uint64_t* s_word = reinterpret_cast<uint64_t*>(s_dyn);
-  int* s_base = reinterpret_cast<int*>(s_dyn + 2 * (in_lds ? words : 0));
-  const uint64_t* __restrict__ bm = u.bitmap + (size_t)g * H * u.words;
-  auto word = [&](int w) {
-    return bm[w] | bm[u.words + w] | bm[2 * u.words + w] | bm[3 * u.words + w];
-  };
-  const int per = (words + blockDim.x - 1) / blockDim.x;
-  const int w0 = threadIdx.x * per, w1 = min(words, w0 + per);
-  int cnt = 0;
-  for (int w = w0; w < w1; ++w) {
-    const uint64_t m = word(w);
-    if (in_lds) s_word[w] = m;
-    s_base[w] = cnt;
-    cnt += __popcll(m);
-  }
-  int total;
-  const int pre = block_excl_scan(cnt, s_scan, &total);
-  for (int w = w0; w < w1; ++w) s_base[w] += pre;
-  __syncthreads();
-  const int* __restrict__ in = u.tokens_in + (size_t)g * u.stride_in;
-  int* __restrict__ out = u.tokens_out + (size_t)g * u.stride_out;
-  constexpr int U = 16;  // independent loads in flight per thread
-  for (int base = threadIdx.x; base < n; base += U * blockDim.x) {
-    int val[U], pos[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int i = base + k * blockDim.x;
-      pos[k] = -1;
-      val[k] = i < n ? in[i] : 0;  // unconditional: all loads issue together
-      if (i < n) {
-        const int w = i >> 6, bit = i & 63;
-        const uint64_t m = in_lds ? s_word[w] : word(w);
-        if ((m >> bit) & 1ull) pos[k] = s_base[w] + __popcll(m & ((1ull << bit) - 1));
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k)
-      if (pos[k] >= 0 && pos[k] < u.stride_out) out[pos[k]] = val[k];
-  }
-  if (threadIdx.x == 0) u.status[g * ST_WORDS + u.slot_out] = min(total, u.stride_out);
-}
-
 // ============================================================ key scores
 // Code4 (p2 << 2 | r2) A-operand words of one key record for all 4 chunks.
 __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t out[4][4]) {
@@ -676,85 +726,167 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
   }
 }
 
-// 4-bit U1 scores: bf16(16 RNE(sum qs (2 code4 - 15))).
-__global__ __launch_bounds__(256) void k_score4(StepArgs a) {
-  const int g = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int n = a.status[g * ST_WORDS + ST_U1];
-  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile * 16 >= n) return;
-  const QOperand* q = &a.qop[g * QV_COUNT + QV_QS];
-  uint32_t b[4][4];
-  load_b(q, b);
-  const int row = lane & 15, kb = lane >> 4;
-  const int i_in = tile * 16 + row;
-  uint32_t av[4][4] = {};
-  if (i_in < n) {
-    const int t = a.u1_tok[(size_t)g * U1_MAX + i_in];
-    load_code4(a.keyrec + ((size_t)g * a.T + t) * 256, kb, av);
-  }
-  v4i acc = {0, 0, 0, 0};
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(av[kc], b[kc], acc);
-  int64_t dot[4];
-  combine_limbs(acc, dot);
-  if ((lane & 3) == 0) {
-    const int h = (lane & 15) >> 2;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = tile * 16 + 4 * kb + r;
-      if (i >= n) continue;
-      a.s4[((size_t)g * H + h) * U1_MAX + i] = (uint16_t)ordered16(
-          bf16_rne(scaled_f32(2 * dot[r] - 15 * q->sum[h], q->fx[h] + 4)));
-    }
-  }
-}
+// ============================================================ unions + scores
+// U1 (STAGE 4) / U2 (STAGE 8): the union of the four heads' member bitmaps
+// over the input items (pool positions / U1 positions), compacted in input
+// order, and the union members' 4-bit / 8-bit scores.  Block b of a group
+// owns a contiguous span of bitmap words: it counts the members in all
+// earlier words (its output base), lists its own members in LDS, copies
+// their tokens to the output list and scores them 16 keys per MFMA tile.
+constexpr int US_BLOCK = 256;
+constexpr int US_CHUNK = 16;  // bitmap words listed per pass (1024 items)
+constexpr int US_GRID_U1 = 48;  // blocks per group (spans of >= 16 pool words)
+constexpr int US_GRID_U2 = 16;  // blocks per group over U1 (<= 100 words)
 
-// 8-bit U2 scores: bf16(RNE(sum qs (2 code8 - 255))), code8 = 16 code4 + r4.
-__global__ __launch_bounds__(256) void k_score8(StepArgs a) {
+template <int STAGE>
+__global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
+  constexpr bool U1 = STAGE == 4;
+  const int ts = U1 ? 8 : 11;
+  SKV_TS(ts, 0);
   const int g = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int n = a.status[g * ST_WORDS + ST_U2];
-  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile * 16 >= n) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_in = a.status[g * ST_WORDS + (U1 ? ST_POOL : ST_U1)];
+  const int words_in = (n_in + 63) / 64;
+  const int W = U1 ? a.words_u1 : a.words_u2;
+  const uint64_t* __restrict__ bm = (U1 ? a.bm_u1 : a.bm_u2) + (size_t)g * H * W;
+  const int* __restrict__ tok_in = U1 ? a.pool_tok + (size_t)g * a.cap : a.u1_tok + (size_t)g * U1_MAX;
+  const int cap_out = U1 ? U1_MAX : U2_MAX;
+  int* __restrict__ tok_out = (U1 ? a.u1_tok : a.u2_tok) + (size_t)g * cap_out;
+  uint16_t* __restrict__ s_out = U1 ? a.s4 : a.s8;
+  const int slot_out = U1 ? ST_U1 : ST_U2;
+  if (n_in == 0) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = 0;
+    return;
+  }
+  const int span = max(US_CHUNK, (words_in + (int)gridDim.x - 1) / (int)gridDim.x);
+  const int w_lo = blockIdx.x * span;
+  if (w_lo >= words_in) return;
+  const int w_hi = min(words_in, w_lo + span);
+
+  __shared__ int s_red[US_BLOCK / WAVE + 1];
+  __shared__ uint64_t s_word[US_CHUNK];
+  __shared__ int s_wbase[US_CHUNK + 1];
+  __shared__ int s_tok[US_CHUNK * 64];
+  auto word = [&](int w) { return bm[w] | bm[W + w] | bm[2 * W + w] | bm[3 * W + w]; };
+
+  // members in words [0, w_lo): 4 words (16 loads) in flight per thread
+  int cnt = 0;
+  for (int w = threadIdx.x; w < w_lo; w += 4 * US_BLOCK) {
+    uint64_t m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ww = w + u * US_BLOCK;
+      m[u] = ww < w_lo ? word(ww) : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cnt += __popcll(m[u]);
+  }
+  cnt = wave_sum(cnt);
+  if (lane == 0) s_red[wave] = cnt;
+  __syncthreads();
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < US_BLOCK / WAVE; ++i) base += s_red[i];
+  SKV_TS(ts, 1);
+
   const QOperand* q = &a.qop[g * QV_COUNT + QV_QS];
   uint32_t b[4][4];
   load_b(q, b);
   const int row = lane & 15, kb = lane >> 4;
-  const int i_in = tile * 16 + row;
-  uint32_t hi[4][4] = {}, lo[4][4] = {};
-  if (i_in < n) {
-    const int t = a.u2_tok[(size_t)g * U2_MAX + i_in];
-    const uint8_t* rec = a.keyrec + ((size_t)g * a.T + t) * 256;
-    load_code4(rec, kb, hi);
-    const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
-    const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
-    const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      expand4(rw[2 * kc], &lo[kc][0]);
-      expand4(rw[2 * kc + 1], &lo[kc][2]);
+  for (int c0 = w_lo; c0 < w_hi; c0 += US_CHUNK) {
+    const int nw = min(US_CHUNK, w_hi - c0);
+    if (threadIdx.x < 64) {  // wave 0: the chunk's words and their member bases
+      const uint64_t m = lane < nw ? word(c0 + lane) : 0ull;
+      const int pc = __popcll(m);
+      const int inc = wave_incl_scan(pc);
+      if (lane < US_CHUNK) {
+        s_word[lane] = m;
+        s_wbase[lane] = inc - pc;
+      }
+      if (lane == US_CHUNK - 1) s_wbase[US_CHUNK] = inc;
     }
-  }
-  v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+    __syncthreads();
+    const int nloc = s_wbase[US_CHUNK];
+    // list the chunk's members: thread t tests 4 bits of word t / 16
+    {
+      const int j = threadIdx.x >> 4, b0 = (threadIdx.x & 15) * 4;
+      const uint64_t m = s_word[j];
+      int r = s_wbase[j] + __popcll(m & ((1ull << b0) - 1));
 #pragma unroll
-  for (int kc = 0; kc < 4; ++kc) {
-    acc_hi = mfma_i8(hi[kc], b[kc], acc_hi);
-    acc_lo = mfma_i8(lo[kc], b[kc], acc_lo);
-  }
-  int64_t dh[4], dl[4];
-  combine_limbs(acc_hi, dh);
-  combine_limbs(acc_lo, dl);
-  if ((lane & 3) == 0) {
-    const int h = (lane & 15) >> 2;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = tile * 16 + 4 * kb + r;
-      if (i >= n) continue;
-      a.s8[((size_t)g * H + h) * U2_MAX + i] = (uint16_t)ordered16(
-          bf16_rne(scaled_f32(2 * (16 * dh[r] + dl[r]) - 255 * q->sum[h], q->fx[h])));
+      for (int e = 0; e < 4; ++e) {
+        if ((m >> (b0 + e)) & 1ull) {
+          const int o = base + r;
+          const int t = tok_in[64 * (c0 + j) + b0 + e];
+          s_tok[r] = t;
+          if (o < cap_out) tok_out[o] = t;
+          ++r;
+        }
+      }
     }
+    __syncthreads();
+    // scores of the listed members, one 16-key tile per wave at a time
+    for (int tile = wave; tile * 16 < nloc; tile += US_BLOCK / WAVE) {
+      const int i_in = tile * 16 + row;
+      v4i acc = {0, 0, 0, 0};
+      if (U1) {
+        uint32_t av[4][4] = {};
+        if (i_in < nloc) load_code4(a.keyrec + ((size_t)g * a.T + s_tok[i_in]) * 256, kb, av);
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(av[kc], b[kc], acc);
+      } else {
+        uint32_t hi[4][4] = {}, lo[4][4] = {};
+        if (i_in < nloc) {
+          const uint8_t* rec = a.keyrec + ((size_t)g * a.T + s_tok[i_in]) * 256;
+          load_code4(rec, kb, hi);
+          const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
+          const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
+          const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+          for (int kc = 0; kc < 4; ++kc) {
+            expand4(rw[2 * kc], &lo[kc][0]);
+            expand4(rw[2 * kc + 1], &lo[kc][2]);
+          }
+        }
+        v4i acc_lo = {0, 0, 0, 0};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          acc = mfma_i8(hi[kc], b[kc], acc);
+          acc_lo = mfma_i8(lo[kc], b[kc], acc_lo);
+        }
+        // 8-bit dot = 16 x (code4 dot) + (residual-4 dot)
+        int64_t dh[4], dl[4];
+        combine_limbs(acc, dh);
+        combine_limbs(acc_lo, dl);
+        if ((lane & 3) == 0) {
+          const int h = (lane & 15) >> 2;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = tile * 16 + 4 * kb + r, o = base + i;
+            if (i >= nloc || o >= cap_out) continue;
+            s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
+                bf16_rne(scaled_f32(2 * (16 * dh[r] + dl[r]) - 255 * q->sum[h], q->fx[h])));
+          }
+        }
+        continue;
+      }
+      int64_t dot[4];
+      combine_limbs(acc, dot);
+      if ((lane & 3) == 0) {
+        const int h = (lane & 15) >> 2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = tile * 16 + 4 * kb + r, o = base + i;
+          if (i >= nloc || o >= cap_out) continue;
+          s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
+              bf16_rne(scaled_f32(2 * dot[r] - 15 * q->sum[h], q->fx[h] + 4)));
+        }
+      }
+    }
+    base += nloc;
+    __syncthreads();
   }
+  if (w_hi == words_in && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = min(base, cap_out);
+  SKV_TS(ts, 15);
 }
 
 // ============================================================ final top-100
@@ -762,6 +894,7 @@ __global__ __launch_bounds__(256) void k_score8(StepArgs a) {
 // member is the number of members with a larger (score, -token) key), then
 // the head's attention over them merged with its sink/local slices.
 __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
+  SKV_TS(13, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
   __shared__ uint64_t s_key[TOPK];
@@ -772,20 +905,47 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   const uint16_t* sc = a.s8 + ((size_t)g * H + h) * U2_MAX;
   const int* tok = a.u2_tok + (size_t)g * U2_MAX;
   auto id = [&](int i) { return (uint32_t)tok[i]; };
-  __shared__ __align__(16) uint16_t so[U2_MAX];
-  load_lds_scores(so, sc, n, [](uint32_t o) { return o; });
+  extern __shared__ __align__(16) unsigned char dyn[];
   if (threadIdx.x == 0) s_cnt = 0;
-  __syncthreads();
-  const Selection sel = block_select(so, n, TOPK, id, s);
-  for_scores(so, n, [&](int i, uint32_t o) {
-    if (!o || !(sel.all || o >= sel.v)) return;
-    const uint32_t t = tok[i];
-    if (sel.member(o, t)) {
-      const int slot = atomicAdd(&s_cnt, 1);
-      if (slot < TOPK) s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
+  bool done = false;
+  if (a.exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
+    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    const FastResult r = fast_select(
+        n, TOPK, [&](int i) { return (uint32_t)sc[i]; },
+        [&](int o, uint32_t* out) { row_load8(sc, n, o, same16, out); }, id, fs,
+        a.exact_select == 2, 13);
+    if (r.ok) {
+      SKV_TS(13, 6);
+      for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
+        const uint64_t key = fs.cand[c];
+        const uint32_t o = cand_ord(key), t = cand_id(key);
+        if (r.sel.member(o, t)) {
+          const int slot = atomicAdd(&s_cnt, 1);
+          if (slot < TOPK) s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
+        }
+      }
+      done = true;
+    } else {
+      __syncthreads();
+      if (threadIdx.x == 0) atomicOr(&a.status[g * ST_WORDS + ST_FULLSEL], FS_TOP100);
     }
-  });
+  }
+  if (!done) {
+    __shared__ __align__(16) uint16_t so[U2_MAX];
+    load_lds_scores(so, sc, n, same16);
+    __syncthreads();
+    const Selection sel = block_select(so, n, TOPK, id, s);
+    for_scores(so, n, [&](int i, uint32_t o) {
+      if (!o || !(sel.all || o >= sel.v)) return;
+      const uint32_t t = tok[i];
+      if (sel.member(o, t)) {
+        const int slot = atomicAdd(&s_cnt, 1);
+        if (slot < TOPK) s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
+      }
+    });
+  }
   __syncthreads();
+  SKV_TS(13, 7);
   const int m = min(s_cnt, TOPK);
   int* out = a.top + (g * H + h) * TOPK;
   if ((int)threadIdx.x < m) {
@@ -808,9 +968,11 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   const int i = wave * SDPA_WAVE_KEYS + lane;
   const int tk = (lane < SDPA_WAVE_KEYS && i < TOPK) ? s_tok[i] : -1;
   float mw, lw, ow[4];
+  SKV_TS(13, 8);
   wave_attend(a.kv8 + (size_t)g * a.T * 512, q, tk, mw, lw, ow);
   stash_wave(att, mw, lw, ow);
   __syncthreads();
+  SKV_TS(13, 9);
   if (threadIdx.x < D) {
     const int d = threadIdx.x;
     float M, L, O;
@@ -833,12 +995,13 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
     }
     a.out[j * D + d] = (uint16_t)bf16_rne(Ot / Lt);
   }
+  SKV_TS(13, 15);
 }
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
     "qprep", "coarse", "thresh", "fine", "fine_select", "pool_count", "pool_emit",
-    "top1600", "union_u1", "score4", "top256", "union_u2", "score8", "top100_sdpa"};
+    "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
 
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
@@ -857,32 +1020,32 @@ void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_
   hipLaunchKernelGGL(k_coarse, dim3(tiles_blocks, G), dim3(256), 0, st, a);
   mark();
   hipLaunchKernelGGL(k_thresh, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
-                     (size_t)a.nc * 2, st, a);
+                     w.thresh_lds, st, a);
   mark();
   hipLaunchKernelGGL(k_fine, dim3(tiles_blocks, G), dim3(256), 0, st, a);
   mark();
-  hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), (size_t)a.nc * 2, st, a);
+  hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), w.fine_select_lds, st, a);
   mark();
   hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(256), bm_lds, st, a);
   mark();
   hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(256), bm_lds, st, a);
   mark();
-  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), (size_t)w.top_u1.lds_items * 2, st,
-                     w.top_u1);
+  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
   mark();
-  hipLaunchKernelGGL(k_union, dim3(G), dim3(1024), w.union_u1_lds, st, w.union_u1);
+  hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(US_BLOCK), 0, st, a);
   mark();
-  hipLaunchKernelGGL(k_score4, dim3(U1_MAX / 64, G), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
   mark();
-  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), (size_t)w.top_u2.lds_items * 2, st,
-                     w.top_u2);
+  hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(US_BLOCK), 0, st, a);
   mark();
-  hipLaunchKernelGGL(k_union, dim3(G), dim3(1024), w.union_u2_lds, st, w.union_u2);
-  mark();
-  hipLaunchKernelGGL(k_score8, dim3(U2_MAX / 64, G), dim3(256), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), 0, st, a);
+  hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
   mark();
 }
 
 }  // namespace skv
+
+#ifdef SKV_TRACE
+extern "C" int skv_trace_read(unsigned long long* out) {
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(skv::g_skv_trace), sizeof(skv::g_skv_trace));
+}
+#endif

@@ -25,6 +25,7 @@
 
 #include "../../include/seoulkv4_hip.h"
 #include "skv_device.h"
+#include "skv_fastsel.h"
 #include "skv_select.h"
 #include "skv_step.h"
 
@@ -479,18 +480,17 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     return bail(SKV_EINVAL);
   }
   w.top_u1 = TopkArgs{a.s2, a.pool_tok, a.cap, M15, a.bm_u1, words1, a.status, ST_POOL,
-                      std::min(lds_items, a.cap)};
-  w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, a.bm_u2, words2, a.status, ST_U1, U1_MAX};
-  // OR-ed bitmap words stay in LDS while words * 12 B fits 96 KiB; the word
-  // bases (4 B each) always do (<= 64 KiB at 2^20 tokens).
-  const int lds1 = words1 * 12 <= 96 * 1024 ? words1 : 0;
-  const int lds2 = words2 * 12 <= 96 * 1024 ? words2 : 0;
-  w.union_u1 = UnionArgs{a.bm_u1, words1, lds1, a.pool_tok, a.cap, a.u1_tok, U1_MAX,
-                         a.status, ST_POOL, ST_U1};
-  w.union_u2 = UnionArgs{a.bm_u2, words2, lds2, a.u1_tok, U1_MAX, a.u2_tok, U2_MAX,
-                         a.status, ST_U1, ST_U2};
-  w.union_u1_lds = (size_t)words1 * (lds1 ? 12 : 4);
-  w.union_u2_lds = (size_t)words2 * (lds2 ? 12 : 4);
+                      std::min(lds_items, a.cap), 0, FS_TOP1600};
+  w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, a.bm_u2, words2, a.status, ST_U1, U1_MAX,
+                      0, FS_TOP256};
+  // Dynamic LDS of the selection kernels: the sampled-cut scratch, or the
+  // LDS-resident scores of the full selection, or the attention scratch of
+  // the sink/local blocks, whichever is largest (they are never live together).
+  const size_t fs_bytes = sizeof(FastScratch);
+  w.thresh_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES});
+  w.fine_select_lds = std::max(fs_bytes, (size_t)nc * 2);
+  w.top_u1_lds = std::max(fs_bytes, (size_t)w.top_u1.lds_items * 2);
+  w.top_u2_lds = std::max(fs_bytes, (size_t)w.top_u2.lds_items * 2);
 
   if (hipHostMalloc((void**)&h->q_host, 16 * D * 2, hipHostMallocDefault) != hipSuccess ||
       hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess) {
@@ -506,10 +506,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
            "\"n_centroids\": %d, \"nprobe\": [%d, %d, %d, %d], \"pool_buffer\": %d, "
            "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
            "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
-           "\"kernels_per_step\": 14, \"lds_per_block\": %zu, \"pool_lds_items\": %d}",
+           "\"kernels_per_step\": %d, \"lds_per_block\": %zu, \"pool_lds_items\": %d}",
            json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), T, a.sink, a.local,
            nc, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min, a.pool_capacity, np_max,
-           h->static_bytes, h->work_bytes, h->lds_per_block, w.top_u1.lds_items);
+           h->static_bytes, h->work_bytes, N_STEP_KERNELS, h->lds_per_block, w.top_u1.lds_items);
   h->meta = buf;
   *handle_out = h;
   return SKV_OK;
@@ -571,6 +571,18 @@ int skv_profile(void* handle, int enable) {
   h->prof_pending = false;
   h->prof_steps = 0;
   for (double& v : h->prof_ms) v = 0.0;
+  return SKV_OK;
+}
+
+int skv_select_mode(void* handle, int exact) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  if (exact < 0 || exact > 2) return fail(h, SKV_EINVAL, "select mode %d not in 0..2", exact);
+  const int e = exact;
+  h->a.exact_select = e;
+  h->w.top_u1.exact_select = e;
+  h->w.top_u2.exact_select = e;
   return SKV_OK;
 }
 

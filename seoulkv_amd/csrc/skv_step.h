@@ -10,10 +10,11 @@
 //   k_pool_count     codegen/stage15.py:275-345 (mate-ownership dedup)
 //   k_pool_emit      codegen/stage15.py:275-345 + 886-995 (2-bit scores)
 //   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
-//   k_union          codegen/stage15.py:1519-1597; codegen/refinement_fusion.py:142-186
-//   k_score4         _kernels/stage16/seoulkv4_stage16_matrix.py:21-60
+//   k_union_score<4> codegen/stage15.py:1519-1597 (U1) +
+//                    _kernels/stage16/seoulkv4_stage16_matrix.py:21-60 (4-bit scores)
 //   k_top256         codegen/refinement_fusion.py:263-266,402-455
-//   k_score8         _kernels/stage16/seoulkv4_union_matrix.py:58-139
+//   k_union_score<8> codegen/refinement_fusion.py:142-186 (U2) +
+//                    _kernels/stage16/seoulkv4_union_matrix.py:58-139 (8-bit scores)
 //   k_top100         codegen/refinement_fusion.py:296-300,495-531
 //   k_thresh, k_top100  sparse SDPA: codegen/attention.py:35-201 (+ TTNN sparse_sdpa)
 #pragma once
@@ -34,7 +35,17 @@ enum {
   ST_U1 = 4,       // |U1|
   ST_U2 = 5,       // |U2|
   ST_SCANNED = 6,  // postings scanned by the pool builder
+  ST_FULLSEL = 7,  // selections that ran the full pass (bit per stage, FS_*)
   ST_WORDS = 8
+};
+
+// ST_FULLSEL bits: the sampled cut missed and the full selection ran
+enum {
+  FS_THRESH = 1,
+  FS_FINE = 2,
+  FS_TOP1600 = 4,
+  FS_TOP256 = 8,
+  FS_TOP100 = 16
 };
 
 
@@ -44,6 +55,7 @@ struct StepArgs {
   int P[G];
   float lam[G];
   int pool_min, pool_capacity, debug;
+  int exact_select;         // 1: always run the full selections (no sampled cut)
   int pool_blocks;          // nc / 32: 32-centroid ranges of the pool kernels
   int words_u1, words_u2;   // bitmap words per (group, head)
   int dense_slices;         // 128-key sink/local attention slices per query head
@@ -100,27 +112,21 @@ struct TopkArgs {
   int* status;
   int count_slot;           // status word holding the item count
   int lds_items;            // scores held in LDS when count <= lds_items
+  int exact_select;         // 1: skip the sampled cut
+  int fullsel_bit;          // FS_* bit recorded when the full selection runs
 };
 
-struct UnionArgs {
-  const uint64_t* bitmap;   // [G][H][words]
-  int words;
-  int lds_words;            // keep OR-ed words in LDS when words <= lds_words
-  const int* tokens_in;
-  int stride_in;
-  int* tokens_out;
-  int stride_out;
-  int* status;
-  int slot_in, slot_out;
-};
 
 struct StepWork {
   TopkArgs top_u1, top_u2;
-  UnionArgs union_u1, union_u2;
-  size_t union_u1_lds, union_u2_lds;  // dynamic LDS bytes of the union kernels
+  size_t thresh_lds, fine_select_lds, top_u1_lds, top_u2_lds;  // selection kernels
 };
 
-constexpr int N_STEP_KERNELS = 14;
+// LDS bytes of the attention scratch of a 512-thread block (8 waves x
+// (max, sum, o[256]) in FP32)
+constexpr size_t ATTN_SCRATCH_BYTES = (size_t)8 * (2 + D) * 4;
+
+constexpr int N_STEP_KERNELS = 12;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev);

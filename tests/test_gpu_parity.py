@@ -115,3 +115,37 @@ def test_step_parity(runtimes, name, qi):
     for j in range(16):
         assert np.abs(got[j] - out[j]).max() <= 2e-2, f"head {j} max-abs"
         assert cosine(got[j], out[j]) >= 0.999, f"head {j} cosine"
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("name", ["t8192_clustered", "t16384_nc1024_p256"])
+def test_selection_paths_agree(runtimes, name, mode):
+    """Every selection through the full path (mode 1) and through a sampled
+    cut forced to miss, i.e. the fallback (mode 2), equals the oracle; the
+    status bits record which selections fell back."""
+    p = CASES[name]
+    rt = runtime_for(runtimes, name)
+    _, _, _, qs = case(**p)
+    print(f"[gpu] select mode {mode} {name}", flush=True)
+    rt.select_mode(mode)
+    try:
+        rt.bind_query(qs[0])
+        rt.enqueue()
+        status = rt.synchronize()
+    finally:
+        rt.select_mode(0)
+    traces, _ = oracle_step(p, qs[0])
+    for g, tr in enumerate(traces):
+        np.testing.assert_array_equal(rt.read_stage("thresh", g), tr.thr)
+        np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected)
+        np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1)
+        np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2)
+        np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
+    bits = status["full_select"]
+    if mode == 1:
+        assert bits == [0, 0, 0, 0]  # the full path ran directly: nothing missed
+    else:
+        assert all(b == 31 for b in bits), bits  # every stage missed and fell back
+    rt.bind_query(qs[0])
+    rt.enqueue()
+    assert rt.synchronize()["full_select"] == [0, 0, 0, 0]  # default: sampled cuts hit
