@@ -5,8 +5,9 @@
 //    bits of the chosen bin) to find a score `cut` that about
 //    k + 4 sqrt(k) + 8 items are expected to reach (exactly the k-th best
 //    score when the sample is the whole input).
-// 2. Candidates: one pass over all n scores appends every item scoring
-//    >= cut to an LDS list (one atomic per wave), then loads their IDs.
+// 2. Candidates: one pass over all n scores appends the position of every
+//    item scoring >= cut to an LDS list (one atomic per wave), then loads
+//    the candidates' scores and IDs.
 // 3. If the list holds fewer than k items (the sample over-estimated the
 //    cut) or overflows, the caller runs the full exact selection instead.
 //    Otherwise the top k of the input are exactly the top k of the list
@@ -24,7 +25,9 @@ namespace skv {
 constexpr int FS_SAMPLE = 4096;
 constexpr int FS_PER = FS_SAMPLE / SEL_BLOCK;  // sample items per thread
 constexpr int CAND_CAP = 4096;
-constexpr int FS_TIE_WAVE = 64;  // ties ranked inside one wave up to this count
+constexpr int FS_TIE_RANK = SEL_BLOCK;  // ties ranked by direct comparison up to this count
+constexpr int FS_OCT = 4;  // score octets per lane per pass (a 32-bit candidate mask)
+constexpr int FS_IDS = CAND_CAP / SEL_BLOCK;  // candidate IDs loaded per thread
 
 struct FastScratch {
   union {
@@ -33,7 +36,7 @@ struct FastScratch {
   };
   uint64_t cand[CAND_CAP];  // ord << 40 | (0xfffff - id) << 20 | position
   uint32_t hist4[16];
-  uint32_t tie[FS_TIE_WAVE];
+  uint32_t tie[FS_TIE_RANK];
   int ncand;
   int maxo;
   int ntie;
@@ -58,19 +61,21 @@ __device__ __forceinline__ int cand_pos(uint64_t c) { return (int)(c & 0xfffffu)
 // s.sel[0..1]; sel[0] = -1 if the histogram holds fewer than rank values.
 // s.sel[2] = total count.
 __device__ __forceinline__ void fs_rank_bin(FastScratch& s, int rank) {
-  constexpr int PER = 4096 / SEL_BLOCK;
-  const int top = 4095 - PER * (int)threadIdx.x;
+  const int lo = 4088 - 8 * (int)threadIdx.x;  // bins lo .. lo + 7, scanned downwards
+  const uint4 a = *reinterpret_cast<const uint4*>(&s.hist[lo]);
+  const uint4 b = *reinterpret_cast<const uint4*>(&s.hist[lo + 4]);
+  const int cv[8] = {(int)b.w, (int)b.z, (int)b.y, (int)b.x, (int)a.w, (int)a.z, (int)a.y, (int)a.x};
   int c = 0;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) c += s.hist[top - j];
+  for (int j = 0; j < 8; ++j) c += cv[j];
   int total;
   const int exc = block_excl_scan(c, s.scan, &total);
   if (exc < rank && rank <= exc + c) {
-    int acc = exc, bin = top;
-    for (int j = 0; j < PER; ++j) {
-      const int cnt = s.hist[top - j];
-      if (acc + cnt >= rank) { bin = top - j; break; }
-      acc += cnt;
+    int acc = exc, bin = lo + 7;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (acc + cv[j] >= rank) { bin = lo + 7 - j; break; }
+      acc += cv[j];
     }
     s.sel[0] = bin;
     s.sel[1] = acc;
@@ -84,26 +89,24 @@ __device__ __forceinline__ void fs_rank_bin(FastScratch& s, int rank) {
 // Digit (0..15) of the rank-th largest value in s.hist4: s.sel[0] = digit,
 // s.sel[1] += count in higher digits, s.sel[3] = count at the digit.
 __device__ __forceinline__ void fs_rank_digit(FastScratch& s, int rank, int acc) {
-  if (threadIdx.x == 0) {
-    int a = acc, d = 0, cnt = 0;
-    for (int j = 15; j >= 0; --j) {
-      cnt = s.hist4[j];
-      if (a + cnt >= rank) { d = j; break; }
-      a += cnt;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int cnt = lane < 16 ? (int)s.hist4[15 - lane] : 0;
+    const int inc = acc + wave_incl_scan(cnt);
+    if (lane < 16 && inc - cnt < rank && rank <= inc) {
+      s.sel[0] = 15 - lane;
+      s.sel[1] = inc - cnt;
+      s.sel[3] = cnt;
     }
-    s.sel[0] = d;
-    s.sel[1] = a;
-    s.sel[3] = cnt;
   }
 }
 
-// score(i): ordered score of item i < n (0 = excluded), a single load.
-// load8(o, out): ordered scores of items 8o .. 8o+7 (0 beyond n).
-// id(i): the item's ID (< 2^20), read only for candidates.
-// force_miss places the cut at the best sampled score (a test of the
-// fallback: fewer than k candidates unless k ties share that score).
-template <typename ScoreFn, typename Load8Fn, typename IdFn>
-__device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, IdFn id,
+// row: the n ordered scores (0 = excluded), 16-byte aligned and readable up
+// to the next multiple of 8 items.  id(i): the item's ID (< 2^20), read only
+// for candidates.  force_miss places the cut at the best sampled score (a
+// test of the fallback: fewer than k candidates unless k ties share it).
+template <typename IdFn>
+__device__ FastResult fast_select(const uint16_t* __restrict__ row, int n, int k, IdFn id,
                                   FastScratch& s, bool force_miss = false, int ts = -1) {
   FastResult res;
   res.ok = true;
@@ -119,7 +122,7 @@ __device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, Id
   for (int u = 0; u < FS_PER; ++u) {
     const int j = (int)threadIdx.x + u * SEL_BLOCK;
     const int i = full ? j : (int)(((uint64_t)j * (uint64_t)n) >> 12);
-    sv[u] = (full && j >= n) ? 0u : score(i);
+    sv[u] = (full && j >= n) ? 0u : (uint32_t)row[i];
   }
   for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
   if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
@@ -159,49 +162,47 @@ __device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, Id
   __syncthreads();
   SKV_TS(ts, 2);
 
-  // ---- 2. candidates (positions and scores), then their IDs
+  // ---- 2. candidate positions: packed compares into a per-lane bit mask
+  // (cut >= 1, so excluded items never pass), then one LDS append per set bit
   {
     const int lane = threadIdx.x & 63;
     const int no = (n + 7) >> 3;
-    uint32_t mx = 0;
-    for (int base = threadIdx.x & ~63; base < no; base += 2 * SEL_BLOCK) {
-      uint32_t v[2][8];
-      int cnt = 0;
+    const uint32_t cut16 = cut << 16;
+    const uint4* __restrict__ r4 = reinterpret_cast<const uint4*>(row);
+    for (int base = threadIdx.x & ~63; base < no; base += FS_OCT * SEL_BLOCK) {
+      uint4 w[FS_OCT];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < FS_OCT; ++r) {
         const int o = base + r * SEL_BLOCK + lane;
-        if (o < no) {
-          load8(o, v[r]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[r][e] = 0;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const bool c = v[r][e] >= cut && v[r][e] != 0;
-          cnt += c;
-          if (c) mx = max(mx, v[r][e]);
-        }
+        w[r] = o < no ? r4[o] : make_uint4(0, 0, 0, 0);
       }
+      uint32_t mask = 0;
+#pragma unroll
+      for (int r = 0; r < FS_OCT; ++r) {
+        const uint32_t ww[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+        uint32_t m8 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          m8 |= (uint32_t)((ww[e] << 16) >= cut16) << (2 * e);  // item 2e (low half)
+          m8 |= (uint32_t)(ww[e] >= cut16) << (2 * e + 1);      // item 2e + 1
+        }
+        const int valid = n - 8 * (base + r * SEL_BLOCK + lane);
+        if (valid < 8) m8 &= valid > 0 ? (1u << valid) - 1u : 0u;
+        mask |= m8 << (8 * r);
+      }
+      const int cnt = __popc(mask);
       const int inc = wave_incl_scan(cnt);
       int wbase = 0;
       if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
       wbase = __shfl(wbase, 63, WAVE);
       int slot = wbase + inc - cnt;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int o = base + r * SEL_BLOCK + lane;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (v[r][e] >= cut && v[r][e] != 0) {
-            if (slot < CAND_CAP) s.cand[slot] = ((uint64_t)v[r][e] << 40) | (uint64_t)(8 * o + e);
-            ++slot;
-          }
-        }
+      while (mask) {
+        const int b = __ffs(mask) - 1;
+        mask &= mask - 1;
+        if (slot < CAND_CAP) s.cand[slot] = (uint64_t)(8 * (base + (b >> 3) * SEL_BLOCK + lane) + (b & 7));
+        ++slot;
       }
     }
-    mx = (uint32_t)wave_max((int)mx);
-    if (lane == 0) atomicMax(&s.maxo, (int)mx);
   }
   __syncthreads();
   SKV_TS(ts, 3);
@@ -211,18 +212,36 @@ __device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, Id
     res.ok = false;
     return res;
   }
-  for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
-    const uint64_t key = s.cand[c];
-    s.cand[c] = key | ((uint64_t)(0xfffffu - id(cand_pos(key))) << 20);
+  // scores and IDs of the candidates (all loads in flight together)
+  {
+    uint32_t idr[FS_IDS], scr[FS_IDS];
+    int posr[FS_IDS];
+#pragma unroll
+    for (int u = 0; u < FS_IDS; ++u) {
+      const int c = (int)threadIdx.x + u * SEL_BLOCK;
+      posr[u] = c < nc ? (int)s.cand[c] : 0;
+      idr[u] = c < nc ? id(posr[u]) : 0u;
+      scr[u] = c < nc ? (uint32_t)row[posr[u]] : 0u;
+    }
+    uint32_t mx = 0;
+#pragma unroll
+    for (int u = 0; u < FS_IDS; ++u) {
+      const int c = (int)threadIdx.x + u * SEL_BLOCK;
+      if (c < nc) {
+        s.cand[c] = ((uint64_t)scr[u] << 40) | ((uint64_t)(0xfffffu - idr[u]) << 20) | (uint64_t)posr[u];
+        mx = max(mx, scr[u]);
+      }
+    }
+    mx = (uint32_t)wave_max((int)mx);
+    if ((threadIdx.x & 63) == 0) atomicMax(&s.maxo, (int)mx);
   }
+  __syncthreads();
   if (cut == 1 && nc <= k) {  // fewer valid items than k: all are members
     res.sel.all = true;
     res.sel.v = 0;
     res.sel.above = nc;
-    __syncthreads();
     return res;
   }
-
   SKV_TS(ts, 4);
   // ---- 3. exact k-th score among the candidates (nc >= k here)
   const uint32_t maxo = (uint32_t)s.maxo;
@@ -243,9 +262,7 @@ __device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, Id
   if (shift == 0) {
     v = cut + (uint32_t)b2;
     ties = (int)s.hist[b2];
-    __syncthreads();
   } else {
-    __syncthreads();
     const uint32_t lowmask = (1u << shift) - 1u;
     for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
       const uint32_t d = cand_ord(s.cand[c]) - cut;
@@ -257,8 +274,8 @@ __device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, Id
     v = cut + (((uint32_t)b2 << shift) | (uint32_t)s.sel[0]);
     above = s.sel[1];
     ties = s.sel[3];
-    __syncthreads();
   }
+  __syncthreads();
   res.sel.v = v;
   res.sel.above = above;
   SKV_TS(ts, 5);
@@ -266,18 +283,17 @@ __device__ FastResult fast_select(int n, int k, ScoreFn score, Load8Fn load8, Id
   if (need >= ties) return res;  // every tie is a member
 
   // ---- ties at v: the `need` lowest IDs win
-  if (ties <= FS_TIE_WAVE) {
+  if (ties <= FS_TIE_RANK) {
     for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
       const uint64_t key = s.cand[c];
       if (cand_ord(key) == v) s.tie[atomicAdd(&s.ntie, 1)] = cand_id(key);
     }
     __syncthreads();
-    if (threadIdx.x < 64) {
-      const int lane = threadIdx.x;
-      const uint32_t x = lane < ties ? s.tie[lane] : 0xffffffffu;
+    if ((int)threadIdx.x < ties) {  // rank = number of smaller tied IDs
+      const uint32_t x = s.tie[threadIdx.x];
       int r = 0;
-      for (int j = 0; j < 64; ++j) r += (uint32_t)__shfl((int)x, j, WAVE) < x;
-      if (lane < ties && r == need - 1) s.sel[2] = (int)x;
+      for (int j = 0; j < ties; ++j) r += s.tie[j] < x;
+      if (r == need - 1) s.sel[2] = (int)x;
     }
     __syncthreads();
     res.sel.idcut = (uint32_t)s.sel[2];

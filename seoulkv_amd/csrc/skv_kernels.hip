@@ -297,22 +297,10 @@ __global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
       const float value = __fmul_rn(val, a.scale4[(size_t)g * (nc / 32) + c / 32]);
       const float margin = __fmul_rn(norm, a.resid[(size_t)g * nc + c]);
       const size_t o = ((size_t)g * H + h) * nc + c;
-      a.lower[o] = (uint16_t)bf16_rne(__fsub_rn(value, margin));
-      a.upper[o] = (uint16_t)bf16_rne(__fadd_rn(value, margin));
+      a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
+      a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
     }
   }
-}
-
-// Ordered scores of items 8o .. 8o+7 of a 16-byte aligned 16-bit row (0 past
-// n), each raw value mapped by xf.
-template <typename Fn>
-__device__ __forceinline__ void row_load8(const uint16_t* __restrict__ row, int n, int o, Fn xf,
-                                          uint32_t out[8]) {
-  const uint4 w = *reinterpret_cast<const uint4*>(row + 8 * o);
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    out[e] = 8 * o + e < n ? xf((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu) : 0u;
 }
 
 __device__ __forceinline__ uint32_t same16(uint32_t o) { return o; }
@@ -329,15 +317,12 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
   }
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
+  // ordered bounds; a non-NaN bound never maps to ordered 0, the "excluded" mark
   const uint16_t* lo = a.lower + ((size_t)g * H + h) * a.nc;
-  // a non-NaN bound never maps to ordered 0, the "excluded" mark
-  auto xf = [](uint32_t b) { return ordered16(b); };
   if (a.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(
-        a.nc, a.P[g], [&](int i) { return ordered16(lo[i]); },
-        [&](int o, uint32_t* out) { row_load8(lo, a.nc, o, xf, out); },
-        [](int i) { return (uint32_t)i; }, fs, a.exact_select == 2, 2);
+    const FastResult r = fast_select(lo, a.nc, a.P[g], [](int i) { return (uint32_t)i; }, fs,
+                                     a.exact_select == 2, 2);
     if (r.ok) {
       SKV_TS(2, 15);
       if (threadIdx.x == 0) a.thr[g * H + h] = r.sel.all ? 0u : r.sel.v;
@@ -347,7 +332,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
     if (threadIdx.x == 0) atomicOr(&a.status[g * ST_WORDS + ST_FULLSEL], FS_THRESH);
   }
   uint16_t* so = reinterpret_cast<uint16_t*>(dyn);  // nc ordered lower bounds
-  load_lds_scores(so, lo, a.nc, xf);
+  load_lds_scores(so, lo, a.nc, same16);
   __syncthreads();
   const Selection sel = block_select(so, a.nc, a.P[g], [](int i) { return (uint32_t)i; }, s);
   if (threadIdx.x == 0) a.thr[g * H + h] = sel.all ? 0u : sel.v;
@@ -389,7 +374,7 @@ __global__ __launch_bounds__(256) void k_fine(StepArgs a) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int c = tile * 16 + 4 * kb + r;
-    const bool ok = ordered16(a.upper[((size_t)g * H + h) * nc + c]) >= thr;
+    const bool ok = a.upper[((size_t)g * H + h) * nc + c] >= thr;
     uint32_t m = (uint32_t)ok << h;  // gather the 4 heads' bits (lanes ^4, ^8)
     m |= __shfl_xor(m, 4, WAVE);
     m |= __shfl_xor(m, 8, WAVE);
@@ -417,10 +402,8 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_fine_select(StepArgs a) {
   bool done = false;
   if (a.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(
-        nc, a.P[g], [&](int i) { return (uint32_t)f[i]; },
-        [&](int o, uint32_t* out) { row_load8(f, nc, o, same16, out); },
-        [](int i) { return (uint32_t)i; }, fs, a.exact_select == 2, 4);
+    const FastResult r = fast_select(f, nc, a.P[g], [](int i) { return (uint32_t)i; }, fs,
+                                     a.exact_select == 2, 4);
     if (r.ok) {
       SKV_TS(4, 6);
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
@@ -658,10 +641,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   auto id = [&](int i) { return (uint32_t)tok[i]; };
   if (t.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(
-        n, t.k, [&](int i) { return (uint32_t)sc[i]; },
-        [&](int o, uint32_t* out) { row_load8(sc, n, o, same16, out); }, id, fs,
-        t.exact_select == 2, ts);
+    const FastResult r = fast_select(sc, n, t.k, id, fs, t.exact_select == 2, ts);
     if (r.ok) {
       SKV_TS(ts, 6);
       const int words = (n + 63) / 64;
@@ -733,9 +713,9 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
 // owns a contiguous span of bitmap words: it counts the members in all
 // earlier words (its output base), lists its own members in LDS, copies
 // their tokens to the output list and scores them 16 keys per MFMA tile.
-constexpr int US_BLOCK = 256;
-constexpr int US_CHUNK = 16;  // bitmap words listed per pass (1024 items)
-constexpr int US_GRID_U1 = 48;  // blocks per group (spans of >= 16 pool words)
+constexpr int US_BLOCK = 512;
+constexpr int US_CHUNK = US_BLOCK / 64;  // bitmap words listed per pass (1 item per thread)
+constexpr int US_GRID_U1 = 96;  // blocks per group over the pool
 constexpr int US_GRID_U2 = 16;  // blocks per group over U1 (<= 100 words)
 
 template <int STAGE>
@@ -807,20 +787,15 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
     }
     __syncthreads();
     const int nloc = s_wbase[US_CHUNK];
-    // list the chunk's members: thread t tests 4 bits of word t / 16
+    // list the chunk's members: thread t tests bit t % 64 of word t / 64
     {
-      const int j = threadIdx.x >> 4, b0 = (threadIdx.x & 15) * 4;
+      const int j = threadIdx.x >> 6, bit = threadIdx.x & 63;
       const uint64_t m = s_word[j];
-      int r = s_wbase[j] + __popcll(m & ((1ull << b0) - 1));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if ((m >> (b0 + e)) & 1ull) {
-          const int o = base + r;
-          const int t = tok_in[64 * (c0 + j) + b0 + e];
-          s_tok[r] = t;
-          if (o < cap_out) tok_out[o] = t;
-          ++r;
-        }
+      if ((m >> bit) & 1ull) {
+        const int r = s_wbase[j] + __popcll(m & ((1ull << bit) - 1));
+        const int t = tok_in[64 * (c0 + j) + bit];
+        s_tok[r] = t;
+        if (base + r < cap_out) tok_out[base + r] = t;
       }
     }
     __syncthreads();
@@ -910,10 +885,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   bool done = false;
   if (a.exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(
-        n, TOPK, [&](int i) { return (uint32_t)sc[i]; },
-        [&](int o, uint32_t* out) { row_load8(sc, n, o, same16, out); }, id, fs,
-        a.exact_select == 2, 13);
+    const FastResult r = fast_select(sc, n, TOPK, id, fs, a.exact_select == 2, 13);
     if (r.ok) {
       SKV_TS(13, 6);
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {

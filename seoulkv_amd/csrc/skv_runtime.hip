@@ -666,9 +666,15 @@ int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t c
   };
   switch (stage) {
     case SKV_STAGE_LOWER:
-      return copy_rows(a.lower + (size_t)group * H * nc, nc, 2, nc, H);
-    case SKV_STAGE_UPPER:
-      return copy_rows(a.upper + (size_t)group * H * nc, nc, 2, nc, H);
+    case SKV_STAGE_UPPER: {  // held as ordered BF16 on the device
+      const int rc = copy_rows((stage == SKV_STAGE_LOWER ? a.lower : a.upper) +
+                                   (size_t)group * H * nc, nc, 2, nc, H);
+      if (rc != SKV_OK) return rc;
+      uint16_t* o = static_cast<uint16_t*>(host_out);
+      for (int64_t i = 0; i < (int64_t)H * nc; ++i)
+        o[i] = (o[i] & 0x8000u) ? (uint16_t)(o[i] ^ 0x8000u) : (uint16_t)(~o[i] & 0xffffu);
+      return SKV_OK;
+    }
     case SKV_STAGE_THRESH:
       return copy_rows(a.thr + group * H, 0, 4, H, 1);
     case SKV_STAGE_MASKS:

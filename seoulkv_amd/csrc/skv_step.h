@@ -75,8 +75,8 @@ struct StepArgs {
   const uint8_t* kv8;       // [G][T][512]: fp8 V | fp8 K
   // per-step workspace
   QOperand* qop;            // [G][QV_COUNT]
-  uint16_t* lower;          // [G][H][nc]
-  uint16_t* upper;          // [G][H][nc]
+  uint16_t* lower;          // [G][H][nc] ordered BF16
+  uint16_t* upper;          // [G][H][nc] ordered BF16
   uint32_t* thr;            // [G][H]
   uint8_t* masks;           // [G][nc] survivor head masks
   uint16_t* fine_ord;       // [G][H][nc] ordered fine score, 0 = ineligible
