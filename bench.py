@@ -65,8 +65,10 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         "fine_select": G * H * nc * 2 + G * nc + G * nc // 8,
         # CSR bounds + mates of the selected clusters' postings
         "pool_count": sel * (8 + 4) + scanned * 4,
-        # CSR, mates, tokens, 64 B prefix rows in; pool tokens + scores out
-        "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4 + 64) + pool * (4 + H * 2),
+        # CSR, mates, tokens of the selected clusters in; pool tokens out
+        "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4) + pool * 4,
+        # pool tokens and their 64 B prefix rows in; 2-bit scores out
+        "score2": pool * (4 + 64 + H * 2),
         # pool scores in; member bitmaps out
         "top1600": pool * H * 2 + G * H * pool // 8,
         # member bitmaps + pool tokens in; U1 tokens, their 128 B (prefix |

@@ -25,9 +25,21 @@ extern __device__ unsigned long long g_skv_trace[32][16];
     if ((k) >= 0 && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)   \
       g_skv_trace[(k)][(i)] = __builtin_amdgcn_s_memrealtime();                \
   } while (0)
+// SKV_TSB(k, i): every block's thread 0 records point i of kernel slot k
+// (first 4096 blocks, x-major over (blockIdx.x, blockIdx.y)).
+extern __device__ unsigned long long g_skv_trace_blk[4][4096][4];
+#define SKV_TSB(k, i)                                                          \
+  do {                                                                         \
+    const unsigned _b = blockIdx.x + blockIdx.y * gridDim.x;                   \
+    if (threadIdx.x == 0 && _b < 4096)                                         \
+      g_skv_trace_blk[(k)][_b][(i)] = __builtin_amdgcn_s_memrealtime();        \
+  } while (0)
 #else
 #define SKV_TS(k, i) \
   do {               \
+  } while (0)
+#define SKV_TSB(k, i) \
+  do {                \
   } while (0)
 #endif
 

@@ -9,8 +9,8 @@
 //               4-bit fine score of every eligible (centroid, head)
 //   fine_select per head: top-P eligible centroids -> selected bitmap (union)
 //   pool_count  per selected cluster: postings owned under spill-2 mate rule
-//   pool_emit   selected list + pool tokens in encounter order, fused with
-//               the 2-bit scores of the owned postings (cluster-block rows)
+//   pool_emit   selected list + pool tokens in encounter order
+//   score2      2-bit scores of the pool
 //   top1600     per head: top-1600 of the pool -> membership bitmap
 //   union_score4  U1 = union over heads in pool order + 4-bit scores of U1
 //   top256      per head: top-256 of U1 -> membership bitmap
@@ -32,6 +32,7 @@ namespace skv {
 
 #ifdef SKV_TRACE
 __device__ unsigned long long g_skv_trace[32][16];
+__device__ unsigned long long g_skv_trace_blk[4][4096][4];
 #endif
 
 // ============================================================ query prep
@@ -457,69 +458,105 @@ __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint
   return mate > c || !((selbm[mate >> 5] >> (mate & 31)) & 1u);
 }
 
-// Stage the group's selected bitmap and the range's 33 CSR offsets in LDS.
+// Stage the group's selected bitmap and the range's 33 CSR offsets and
+// chunk bases in LDS.
 __device__ __forceinline__ void stage_range(const StepArgs& a, int g, int b, uint32_t* s_bm,
-                                            int* s_off) {
+                                            int* s_off, int* s_cb) {
   const uint32_t* bm = a.selbm + (size_t)g * (a.nc / 32);
   for (int i = threadIdx.x; i < a.nc / 32; i += blockDim.x) s_bm[i] = bm[i];
-  if (threadIdx.x <= 32) s_off[threadIdx.x] = a.csr_off[(size_t)g * (a.nc + 1) + b * 32 + threadIdx.x];
+  if (threadIdx.x <= 32) {
+    const size_t o = (size_t)g * (a.nc + 1) + b * 32 + threadIdx.x;
+    s_off[threadIdx.x] = a.csr_off[o];
+    s_cb[threadIdx.x] = a.chunk_base[o];
+  }
 }
 
-__global__ __launch_bounds__(256) void k_pool_count(StepArgs a) {
+constexpr int PC_BLOCK = 512;   // pool_count: one wave per selected cluster
+constexpr int PC_WAVES = PC_BLOCK / WAVE;
+constexpr int PE_BLOCK = 512;   // pool_emit: one wave per 64-posting chunk
+constexpr int PE_WAVES = PE_BLOCK / WAVE;
+constexpr int S2_GRID = 512;    // score2 blocks per group (4 waves; about one 16-item tile per wave)
+
+// Work items of a selected cluster: its 64-posting chunks (one item for an
+// empty list, so that every selected cluster is listed).
+__device__ __forceinline__ int cluster_items(int postings) {
+  return max(1, (postings + 63) / 64);
+}
+
+// Owned postings of every selected cluster of the range (one wave per
+// cluster), per 64-posting chunk and in total, and the range's counts
+// {selected, owned, scanned, work items}.
+__global__ __launch_bounds__(PC_BLOCK) void k_pool_count(StepArgs a) {
   SKV_TS(5, 0);
+  SKV_TSB(0, 0);
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
-  __shared__ int s_off[33];
-  __shared__ int s_own[4], s_scan[4];
-  stage_range(a, g, b, s_bm, s_off);
+  __shared__ int s_off[33], s_cb[33];
+  __shared__ int s_own[PC_WAVES], s_scan[PC_WAVES], s_items[PC_WAVES];
+  stage_range(a, g, b, s_bm, s_off, s_cb);
   __syncthreads();
   const uint32_t M = s_bm[b];
   const int nsel = __popc(M);
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
-  int own_w = 0, scan_w = 0;
-  for (int rk = wave; rk < nsel; rk += 4) {
+  int* own_chunk = a.own_chunk + (size_t)g * a.chunks_max;
+  int own_w = 0, scan_w = 0, items_w = 0;
+  for (int rk = wave; rk < nsel; rk += PC_WAVES) {
     const int cl = nth_set_bit(M, rk);
     const uint32_t c = b * 32 + cl;
     const int j0 = s_off[cl], j1 = s_off[cl + 1];
     int own = 0;
-    for (int jc = j0; jc < j1; jc += 64) {
+    for (int jc = j0, kk = 0; jc < j1; jc += 64, ++kk) {
       const int j = jc + lane;
       const bool o = j < j1 && owned(s_bm, (uint32_t)mate[j], c);
-      own += __popcll(__ballot(o));
+      const int oc = __popcll(__ballot(o));
+      if (lane == 0) own_chunk[s_cb[cl] + kk] = oc;
+      own += oc;
     }
     if (lane == 0) a.own_cnt[(size_t)g * a.nc + c] = own;
     own_w += own;
     scan_w += j1 - j0;
+    items_w += cluster_items(j1 - j0);
   }
   if (lane == 0) {
     s_own[wave] = own_w;
     s_scan[wave] = scan_w;
+    s_items[wave] = items_w;
   }
   __syncthreads();
-  if (threadIdx.x == 0)
-    a.range_cnt[(size_t)g * a.pool_blocks + b] =
-        make_int4(nsel, s_own[0] + s_own[1] + s_own[2] + s_own[3],
-                  s_scan[0] + s_scan[1] + s_scan[2] + s_scan[3], 0);
+  if (threadIdx.x == 0) {
+    int o = 0, sc = 0, it = 0;
+    for (int w = 0; w < PC_WAVES; ++w) {
+      o += s_own[w];
+      sc += s_scan[w];
+      it += s_items[w];
+    }
+    a.range_cnt[(size_t)g * a.pool_blocks + b] = make_int4(nsel, o, sc, it);
+  }
+  SKV_TSB(0, 3);
 }
 
-// Emit the selected list and the pool in encounter order, and score every
-// owned posting on the matrix cores from its cluster-block prefix row:
-// s2 = bf16(16 RNE(sum q15 (2 p2 - 3))).
-__global__ __launch_bounds__(256) void k_pool_emit(StepArgs a) {
+// Emit the selected list and the pool tokens in encounter order.  Block b
+// owns the 32-centroid range b; its work items are the 64-posting chunks of
+// the range's selected clusters, one per wave at a time.  A chunk's first
+// pool position is its cluster's (owned counts of the earlier ranges and of
+// the range's earlier selected clusters) plus the owned counts of the
+// cluster's earlier chunks.
+__global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
   SKV_TS(6, 0);
+  SKV_TSB(1, 0);
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
-  __shared__ int s_off[33];
-  __shared__ int s_cl[32];
-  stage_range(a, g, b, s_bm, s_off);
+  __shared__ int s_off[33], s_cb[33];
+  __shared__ int s_pos[32], s_cl[32], s_chb[33];
+  stage_range(a, g, b, s_bm, s_off, s_cb);
+  __syncthreads();
   const int4* rc = a.range_cnt + (size_t)g * a.pool_blocks;
   if (wave == 0) {
-    // prefix over the preceding ranges (the last range also writes totals),
-    // and the owned counts of this range's selected clusters
+    // prefix over the preceding ranges (the last range also writes totals)
     const bool last = b == a.pool_blocks - 1;
-    const uint32_t M = a.selbm[(size_t)g * (a.nc / 32) + b];
+    const uint32_t M = s_bm[b];
     const int own_raw = lane < 32 ? a.own_cnt[(size_t)g * a.nc + b * 32 + lane] : 0;
     int ps = 0, po = 0, ts = 0, to = 0, tn = 0;
     for (int i0 = lane; i0 <= b; i0 += 256) {
@@ -548,80 +585,97 @@ __global__ __launch_bounds__(256) void k_pool_emit(StepArgs a) {
         a.status[g * ST_WORDS + ST_SCANNED] = tn;
       }
     }
-    // rank of this lane's centroid among the range's selected clusters
+    // per selected cluster (centroid order = selection order): pool base,
+    // range offset and first work item
     const bool is_sel = lane < 32 && ((M >> lane) & 1u);
     const int rank = __popc(M & ((1u << (lane & 31)) - 1u));
     const int own = is_sel ? own_raw : 0;
-    const int inc = wave_incl_scan(own);  // lanes in centroid order = selection order
+    const int nch = is_sel ? cluster_items(s_off[lane + 1] - s_off[lane]) : 0;
+    const int inc = wave_incl_scan(own);
+    const int incc = wave_incl_scan(nch);
     if (is_sel) {
-      s_cl[rank] = po + inc - own;
+      s_pos[rank] = po + inc - own;
+      s_cl[rank] = lane;
+      s_chb[rank] = incc - nch;
       a.sel[(size_t)g * a.nc + ps + rank] = b * 32 + lane;
     }
+    if (lane == 63) s_chb[__popc(M)] = incc;
   }
   __syncthreads();
+  SKV_TSB(1, 1);
   const uint32_t M = s_bm[b];
   const int nsel = __popc(M);
-  if (nsel <= wave) return;
+  const int nitems = s_chb[nsel];
+  const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
+  const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
+  const int* __restrict__ own_chunk = a.own_chunk + (size_t)g * a.chunks_max;
+  int* pool = a.pool_tok + (size_t)g * a.cap;
+  for (int it = wave; it < nitems; it += PE_WAVES) {
+    // the item's cluster: the last selected rank whose first item is <= it
+    const uint64_t bal = __ballot(lane < nsel && s_chb[lane] <= it);
+    const int r = 63 - __clzll(bal);
+    const int k = it - s_chb[r];
+    const int cl = s_cl[r];
+    const uint32_t c = b * 32 + cl;
+    const int j = s_off[cl] + 64 * k + lane, j1 = s_off[cl + 1];
+    const int mj = j < j1 ? mate[j] : -1;
+    const int tj = j < j1 ? ptok[j] : 0;
+    int pre = 0;
+    for (int t = lane; t < k; t += 64) pre += own_chunk[s_cb[cl] + t];
+    const int pos = s_pos[r] + (k > 0 ? wave_sum(pre) : 0);
+    const bool o = j < j1 && owned(s_bm, (uint32_t)mj, c);
+    const uint64_t om = __ballot(o);
+    const int p = pos + __popcll(om & ((1ull << lane) - 1));
+    if (o && p < a.cap) pool[p] = tj;
+  }
+  if (wave == 0) SKV_TSB(1, 3);
+}
+
+// 2-bit pool scores s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) from each token's
+// prefix plane, 16 pool items per matrix-core tile, tiles spread over the
+// grid (grid-stride).
+__global__ __launch_bounds__(256) void k_score2(StepArgs a) {
+  SKV_TS(14, 0);
+  const int g = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int n = a.status[g * ST_WORDS + ST_POOL];
+  const int ntiles = (n + 15) / 16;
+  const int w0 = blockIdx.x * 4 + (threadIdx.x >> 6), wstride = gridDim.x * 4;
+  if (w0 >= ntiles) return;
   const QOperand* q = &a.qop[g * QV_COUNT + QV_Q15];
   uint32_t bq[4][4];
   load_b(q, bq);
-  const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
-  const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
-  const uint8_t* __restrict__ p2 = a.post_p2 + (size_t)g * a.np_max * 64;
-  int* pool = a.pool_tok + (size_t)g * a.cap;
-  uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
   const int row = lane & 15, kb = lane >> 4, h = (lane & 15) >> 2;
   const int64_t S = q->sum[h];
   const int fx = q->fx[h] + 4;
-  for (int rk = wave; rk < nsel; rk += 4) {
-    const int cl = nth_set_bit(M, rk);
-    const uint32_t c = b * 32 + cl;
-    const int j0 = s_off[cl], j1 = s_off[cl + 1];
-    int pos = s_cl[rk];
-    for (int jc = j0; jc < j1; jc += 64) {
-      const int j = jc + lane;
-      // all global reads of this chunk are issued before any is consumed
-      const int mj = j < j1 ? mate[j] : -1;
-      const int tj = j < j1 ? ptok[j] : 0;
-      uint4 w[4];
+  const int* __restrict__ pool = a.pool_tok + (size_t)g * a.cap;
+  const uint8_t* __restrict__ rec = a.keyrec + (size_t)g * a.T * 256;
+  uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
+  for (int tile = w0; tile < ntiles; tile += wstride) {
+    const int i = tile * 16 + row;
+    uint4 wv = make_uint4(0, 0, 0, 0);
+    if (i < n) wv = *reinterpret_cast<const uint4*>(rec + (size_t)pool[i] * 256 + kb * 16);
+    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+    v4i acc = {0, 0, 0, 0};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int jr = jc + 16 * t + row;
-        w[t] = jr < j1 ? *reinterpret_cast<const uint4*>(p2 + (size_t)jr * 64 + kb * 16)
-                       : make_uint4(0, 0, 0, 0);
+    for (int kc = 0; kc < 4; ++kc) {
+      uint32_t av[4];
+      expand2(words[kc], av);
+      acc = mfma_i8(av, bq[kc], acc);
+    }
+    int64_t dot[4];
+    combine_limbs(acc, dot);
+    if ((lane & 3) == 0) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int ii = tile * 16 + 4 * kb + rr;
+        if (ii < n)
+          s2[(size_t)h * a.cap + ii] =
+              (uint16_t)ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
       }
-      const bool o = j < j1 && owned(s_bm, (uint32_t)mj, c);
-      const uint64_t om = __ballot(o);
-      const int prank = __popcll(om & ((1ull << lane) - 1));
-      if (o && pos + prank < a.cap) pool[pos + prank] = tj;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (jc + 16 * t >= j1) break;  // wave-uniform
-        const uint32_t words[4] = {w[t].x, w[t].y, w[t].z, w[t].w};
-        v4i acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-          uint32_t av[4];
-          expand2(words[kc], av);
-          acc = mfma_i8(av, bq[kc], acc);
-        }
-        int64_t dot[4];
-        combine_limbs(acc, dot);
-        if ((lane & 3) == 0) {
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int idx = 16 * t + 4 * kb + rr;  // posting index within chunk
-            if (!((om >> idx) & 1ull)) continue;
-            const int p = pos + __popcll(om & ((1ull << idx) - 1));
-            if (p >= a.cap) continue;
-            s2[(size_t)h * a.cap + p] =
-                (uint16_t)ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
-          }
-        }
-      }
-      pos += __popcll(om);
     }
   }
+  SKV_TS(14, 15);
 }
 
 // ============================================================ token top-k
@@ -972,7 +1026,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
-    "qprep", "coarse", "thresh", "fine", "fine_select", "pool_count", "pool_emit",
+    "qprep", "coarse", "thresh", "fine", "fine_select", "pool_count", "pool_emit", "score2",
     "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
 
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
@@ -998,9 +1052,11 @@ void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_
   mark();
   hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), w.fine_select_lds, st, a);
   mark();
-  hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(256), bm_lds, st, a);
+  hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(PC_BLOCK), bm_lds, st, a);
   mark();
-  hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(256), bm_lds, st, a);
+  hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(PE_BLOCK), bm_lds, st, a);
+  mark();
+  hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);
   mark();
   hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
   mark();
@@ -1019,5 +1075,9 @@ void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_
 #ifdef SKV_TRACE
 extern "C" int skv_trace_read(unsigned long long* out) {
   return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(skv::g_skv_trace), sizeof(skv::g_skv_trace));
+}
+extern "C" int skv_trace_blocks(unsigned long long* out) {
+  return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(skv::g_skv_trace_blk),
+                                  sizeof(skv::g_skv_trace_blk));
 }
 #endif

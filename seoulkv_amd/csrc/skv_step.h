@@ -8,7 +8,8 @@
 //                    codegen/fine_postscale_codegen.py:6-71, codegen/fine.py:1848-1861
 //   k_fine_select    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73
 //   k_pool_count     codegen/stage15.py:275-345 (mate-ownership dedup)
-//   k_pool_emit      codegen/stage15.py:275-345 + 886-995 (2-bit scores)
+//   k_pool_emit      codegen/stage15.py:275-345 (encounter-order pool)
+//   k_score2         codegen/stage15.py:886-995 (2-bit scores)
 //   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
 //   k_union_score<4> codegen/stage15.py:1519-1597 (U1) +
 //                    _kernels/stage16/seoulkv4_stage16_matrix.py:21-60 (4-bit scores)
@@ -68,6 +69,8 @@ struct StepArgs {
   const float* resid;       // [G][nc]
   const float* gfs;         // [G][nc/32]
   const int* csr_off;       // [G][nc+1]
+  const int* chunk_base;    // [G][nc+1] first 64-posting chunk of each cluster
+  int chunks_max;           // chunks per group (row stride of own_chunk)
   const int* post_tok;      // [G][np_max]
   const int* post_mate;     // [G][np_max] (-1: no mate)
   const uint8_t* post_p2;   // [G][np_max][64]
@@ -83,6 +86,7 @@ struct StepArgs {
   uint16_t* fine_bits;      // [G][H][nc] BF16 fine score (debug)
   int* sel;                 // [G][nc] selected clusters, ascending
   int* own_cnt;             // [G][nc] owned postings per selected cluster
+  int* own_chunk;           // [G][chunks_max] owned postings per chunk of a selected cluster
   int4* range_cnt;          // [G][pool_blocks] {selected, owned, scanned, 0}
   int* pool_tok;            // [G][cap]
   uint16_t* s2;             // [G][H][cap] ordered
@@ -126,7 +130,7 @@ struct StepWork {
 // (max, sum, o[256]) in FP32)
 constexpr size_t ATTN_SCRATCH_BYTES = (size_t)8 * (2 + D) * 4;
 
-constexpr int N_STEP_KERNELS = 12;
+constexpr int N_STEP_KERNELS = 13;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev);
