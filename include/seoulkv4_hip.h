@@ -145,6 +145,13 @@ int skv_profile(void *handle, int enable);
  * 16 top-100), which selections of the last step took the full path. */
 int skv_select_mode(void *handle, int exact);
 int skv_profile_read(void *handle, float *mean_ms, int n, int32_t *steps);
+
+/* Duration of step kernel `kernel` alone (diagnostic; the reference's
+ * per-kernel device markers serve the same purpose): after at least one
+ * step, launches that kernel `reps` times back to back on the handle's stream
+ * between two HIP events and stores the mean milliseconds per launch, then
+ * runs one full step so every buffer holds a consistent step again. */
+int skv_time_kernel(void *handle, int kernel, int reps, float *mean_ms);
 int skv_kernel_count(void);
 const char *skv_kernel_name(int i);
 

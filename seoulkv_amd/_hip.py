@@ -85,6 +85,7 @@ def load_library() -> ctypes.CDLL:
         "skv_read_stage": (i32, [vp, i32, i32, vp, i64, ctypes.POINTER(i64)]),
         "skv_profile": (i32, [vp, i32]),
         "skv_select_mode": (i32, [vp, i32]),
+        "skv_time_kernel": (i32, [vp, i32, i32, vp]),
         "skv_profile_read": (i32, [vp, vp, i32, vp]),
         "skv_kernel_count": (i32, []),
         "skv_kernel_name": (ctypes.c_char_p, [i32]),
@@ -197,6 +198,14 @@ class Runtime:
             raise ValueError("expected a device BF16 Q with 16 x 256 elements")
         q_dev = q_dev.contiguous()
         self._check(self.lib.skv_bind_query_device(self.handle, q_dev.data_ptr()), "bind_query")
+
+    def time_kernel(self, kernel: int, reps: int = 50) -> float:
+        """Mean milliseconds of step kernel ``kernel`` launched ``reps`` times
+        back to back (inputs of the last step)."""
+        ms = np.zeros(1, dtype=np.float32)
+        self._check(self.lib.skv_time_kernel(self.handle, int(kernel), int(reps), _ptr(ms)),
+                    "time_kernel")
+        return float(ms[0])
 
     def select_mode(self, mode: int) -> None:
         """0: sampled cut with full fallback (default); 1: full selection

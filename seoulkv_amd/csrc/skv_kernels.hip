@@ -1032,42 +1032,61 @@ const char* const kKernelNames[N_STEP_KERNELS] = {
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
 // ev[N_STEP_KERNELS] after the last one.
-void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev) {
+void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) {
   const int tiles_blocks = (a.nc + 63) / 64;
   const size_t bm_lds = (size_t)(a.nc / 32) * 4;
-  int k = 0;
-  auto mark = [&]() {
+  switch (k) {
+    case 0:
+      hipLaunchKernelGGL(k_qprep, dim3(G, QV_COUNT), dim3(256), 0, st, a);
+      break;
+    case 1:
+      hipLaunchKernelGGL(k_coarse, dim3(tiles_blocks, G), dim3(256), 0, st, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_thresh, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
+                         w.thresh_lds, st, a);
+      break;
+    case 3:
+      hipLaunchKernelGGL(k_fine, dim3(tiles_blocks, G), dim3(256), 0, st, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), w.fine_select_lds, st, a);
+      break;
+    case 5:
+      hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(PC_BLOCK), bm_lds, st, a);
+      break;
+    case 6:
+      hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(PE_BLOCK), bm_lds, st, a);
+      break;
+    case 7:
+      hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);
+      break;
+    case 8:
+      hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
+      break;
+    case 9:
+      hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(US_BLOCK), 0, st, a);
+      break;
+    case 10:
+      hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
+      break;
+    case 11:
+      hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(US_BLOCK), 0, st, a);
+      break;
+    case 12:
+      hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
+      break;
+    default:
+      break;
+  }
+}
+
+void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev) {
+  for (int k = 0; k < N_STEP_KERNELS; ++k) {
     if (ev) (void)hipEventRecord(ev[k], st);
-    ++k;
-  };
-  mark();
-  hipLaunchKernelGGL(k_qprep, dim3(G, QV_COUNT), dim3(256), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_coarse, dim3(tiles_blocks, G), dim3(256), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_thresh, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
-                     w.thresh_lds, st, a);
-  mark();
-  hipLaunchKernelGGL(k_fine, dim3(tiles_blocks, G), dim3(256), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), w.fine_select_lds, st, a);
-  mark();
-  hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(PC_BLOCK), bm_lds, st, a);
-  mark();
-  hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(PE_BLOCK), bm_lds, st, a);
-  mark();
-  hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
-  mark();
-  hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(US_BLOCK), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
-  mark();
-  hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(US_BLOCK), 0, st, a);
-  mark();
-  hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
-  mark();
+    launch_kernel(a, w, st, k);
+  }
+  if (ev) (void)hipEventRecord(ev[N_STEP_KERNELS], st);
 }
 
 }  // namespace skv

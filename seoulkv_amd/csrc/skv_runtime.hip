@@ -589,6 +589,32 @@ int skv_profile(void* handle, int enable) {
   return SKV_OK;
 }
 
+int skv_time_kernel(void* handle, int kernel, int reps, float* mean_ms) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  if (kernel < 0 || kernel >= N_STEP_KERNELS || reps < 1 || !mean_ms)
+    return fail(h, SKV_EINVAL, "kernel %d / reps %d out of range", kernel, reps);
+  if (!h->ran) return fail(h, SKV_ESTATE, "no decode step has run");
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  HIPCHK(h, hipEventCreate(&e0));
+  HIPCHK(h, hipEventCreate(&e1));
+  // the kernel's inputs are those of the last step; every step kernel is a
+  // function of its inputs, so repeated launches recompute the same outputs
+  HIPCHK(h, hipEventRecord(e0, h->stream));
+  for (int r = 0; r < reps; ++r) launch_kernel(h->a, h->w, h->stream, kernel);
+  HIPCHK(h, hipEventRecord(e1, h->stream));
+  HIPCHK(h, hipEventSynchronize(e1));
+  float ms = 0.f;
+  HIPCHK(h, hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *mean_ms = ms / (float)reps;
+  // a full step restores every downstream buffer (query prep clears state)
+  launch_step(h->a, h->w, h->stream, nullptr);
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  return SKV_OK;
+}
+
 int skv_select_mode(void* handle, int exact) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;

@@ -133,6 +133,8 @@ constexpr size_t ATTN_SCRATCH_BYTES = (size_t)8 * (2 + D) * 4;
 constexpr int N_STEP_KERNELS = 13;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
+// Kernel k (0 .. N_STEP_KERNELS - 1, in step order) of one decode step.
+void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k);
 void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev);
 
 }  // namespace skv

@@ -56,6 +56,8 @@ def ivf_keys(n: int, seed: int) -> torch.Tensor:
 
 
 def main(reference_src: str) -> None:
+    # the reference checkout is read-only input: no bytecode caches there
+    sys.dont_write_bytecode = True
     sys.path.insert(0, reference_src)
     from seoulkv4._clustering import _refined_hierarchical_ivf  # reference IVF
     from seoulkv4._index_build import build_stage1_cell  # the reference builder

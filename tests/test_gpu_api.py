@@ -153,3 +153,24 @@ def test_full_size_parity_config2():
         _check_output(rt.read_output(), ref)
     finally:
         rt.close()
+
+
+def test_time_kernel_keeps_the_step_consistent():
+    """Timing a kernel alone re-runs it on the last step's inputs and then a
+    full step: the selection and output stay those of the bound query."""
+    index, k, v, qs = case(**P0)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    try:
+        rt.bind_query(qs[0])
+        rt.enqueue()
+        rt.synchronize()
+        out, ids = rt.read_output(), rt.debug_ids()
+        n = rt.lib.skv_kernel_count()
+        times = [rt.time_kernel(i, reps=3) for i in range(n)]
+        assert all(t > 0 for t in times)
+        assert torch.equal(rt.read_output(), out)
+        assert torch.equal(rt.debug_ids(), ids)
+        with pytest.raises(RuntimeError):
+            rt.time_kernel(n, reps=1)
+    finally:
+        rt.close()
