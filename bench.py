@@ -42,29 +42,25 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
     from the live stage sizes.  Reads of each input once plus the outputs the
     next stage needs."""
     G, H = 4, 4
-    surv = sum(status["survivors"])
     sel = sum(status["selected"])
     scanned = sum(status["scanned"])
     pool = sum(status["pool"])
     u1 = sum(status["u1"])
     u2 = sum(status["u2"])
-    bimg = 3 * G * 4096
-    del surv
     return {
-        # Q, key scales in; fixed-point limb images out
-        "qprep": 16 * 256 * 2 + G * 256 * 4 + bimg,
-        # 2-bit upper plane, group scale, residual norm in; lower+upper out
-        "coarse": G * nc * (64 + 4 + H * 4) + G * (nc // 32) * 4 + G * 4096,
-        # lower bounds in; the extra blocks' sink/local FP8 [V||K] records
-        # (once per group) in and their slice partials out
-        "thresh": G * H * nc * 2 + G * (p.sink + p.local) * 512
+        # Q + key scales in (per block, from L2); both centroid planes, scale,
+        # residual norm in; lower/upper bounds and fine scores out; three
+        # query operand blocks out
+        "front": G * nc * (128 + 4 + H * 6) + G * (nc // 32) * 8 + 16 * 256 * 2
+        + 3 * G * 8400,
+        # lower, upper and fine scores in (per head); selected bitmap out; the
+        # extra blocks' sink/local FP8 [V||K] records (once per group) in and
+        # their slice partials out
+        "select": G * H * nc * 6 + G * nc // 8 + G * (p.sink + p.local) * 512
         + 16 * ((p.sink + p.local + 127) // 128) * 258 * 4,
-        # both planes + upper bounds in; fine scores + masks out
-        "fine": G * nc * (128 + H * 2 + H * 2 + 1) + G * 4096,
-        # fine scores (+ masks once) in; selected bitmap out
-        "fine_select": G * H * nc * 2 + G * nc + G * nc // 8,
-        # CSR bounds + mates of the selected clusters' postings
-        "pool_count": sel * (8 + 4) + scanned * 4,
+        # CSR bounds + mates of the selected clusters' postings; upper bounds
+        # in and survivor masks out
+        "pool_count": sel * (8 + 4) + scanned * 4 + G * nc * (H * 2 + 1),
         # CSR, mates, tokens of the selected clusters in; pool tokens out
         "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4) + pool * 4,
         # pool tokens and their 64 B prefix rows in; 2-bit scores out

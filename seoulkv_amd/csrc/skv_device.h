@@ -144,36 +144,35 @@ __host__ __device__ inline uint32_t f32_to_fp8_e4m3(float f) {
 }
 
 // ---------------------------------------------------------------- wave ops
+// Cross-lane scans and reductions on the DPP data paths (row shifts within
+// 16-lane rows, then row broadcasts 15 and 31 across rows), the wave64 scan
+// pattern of AMD's GCN cross-lane operations guide.  Every lane of the wave
+// must be active.  update_dpp(old, v, ctrl, row_mask, bank_mask, zero_fill)
+// returns v moved by ctrl; lanes without a source take old (or 0).
 __device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & (WAVE - 1);
-#pragma unroll
-  for (int off = 1; off < WAVE; off <<= 1) {
-    int t = __shfl_up(v, off, WAVE);
-    if (lane >= off) v += t;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
 
+// Wave total, uniform across lanes.
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int off = WAVE / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
-  return v;
-}
-
-__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
-#pragma unroll
-  for (int off = WAVE / 2; off > 0; off >>= 1) {
-    int lo = __shfl_xor((int)(uint32_t)v, off, WAVE);
-    int hi = __shfl_xor((int)(uint32_t)((uint64_t)v >> 32), off, WAVE);
-    v += (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-  }
-  return v;
+  return __builtin_amdgcn_readlane(wave_incl_scan(v), 63);
 }
 
 __device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-  for (int off = WAVE / 2; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, WAVE));
-  return v;
+  constexpr int LO = (int)0x80000000;
+  v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x111, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x112, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x114, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x118, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x142, 0xa, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x143, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Exclusive block scan of one int per thread; returns the exclusive prefix

@@ -50,6 +50,30 @@ struct FastResult {
   bool ok;        // false: use the full selection
 };
 
+// Score sources: at(i) = ordered score of item i; oct(o) = the 8 ordered
+// scores of items 8o .. 8o+7 as packed 16-bit pairs.
+struct RowScores {  // a 16-byte aligned row, readable to a multiple of 8 items
+  const uint16_t* __restrict__ row;
+  __device__ uint32_t at(int i) const { return row[i]; }
+  __device__ uint4 oct(int o) const { return reinterpret_cast<const uint4*>(row)[o]; }
+};
+
+struct MaskedScores {  // score[i] where gate[i] >= thr, else 0 (excluded)
+  const uint16_t* __restrict__ score;
+  const uint16_t* __restrict__ gate;
+  uint32_t thr;
+  __device__ uint32_t at(int i) const { return gate[i] >= thr ? score[i] : 0u; }
+  __device__ uint4 oct(int o) const {
+    const uint4 s4 = reinterpret_cast<const uint4*>(score)[o];
+    const uint4 g4 = reinterpret_cast<const uint4*>(gate)[o];
+    const uint32_t t16 = thr << 16;
+    auto pick = [&](uint32_t sw, uint32_t gw) {
+      return ((gw << 16) >= t16 ? (sw & 0xffffu) : 0u) | (gw >= t16 ? (sw & 0xffff0000u) : 0u);
+    };
+    return make_uint4(pick(s4.x, g4.x), pick(s4.y, g4.y), pick(s4.z, g4.z), pick(s4.w, g4.w));
+  }
+};
+
 __device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40); }
 __device__ __forceinline__ uint32_t cand_id(uint64_t c) {
   return 0xfffffu - (uint32_t)((c >> 20) & 0xfffffu);
@@ -101,13 +125,14 @@ __device__ __forceinline__ void fs_rank_digit(FastScratch& s, int rank, int acc)
   }
 }
 
-// row: the n ordered scores (0 = excluded), 16-byte aligned and readable up
-// to the next multiple of 8 items.  id(i): the item's ID (< 2^20), read only
-// for candidates.  force_miss places the cut at the best sampled score (a
-// test of the fallback: fewer than k candidates unless k ties share it).
-template <typename IdFn>
-__device__ FastResult fast_select(const uint16_t* __restrict__ row, int n, int k, IdFn id,
-                                  FastScratch& s, bool force_miss = false, int ts = -1) {
+// src: the n ordered scores (0 = excluded; see RowScores / MaskedScores).
+// id(i): the item's ID (< 2^20), read only for candidates.  VALUE_ONLY: only
+// sel.v (the k-th best score) is wanted: no IDs, no tie resolution.
+// force_miss places the cut at the best sampled score (a test of the
+// fallback: fewer than k candidates unless k ties share it).
+template <bool VALUE_ONLY = false, typename Src, typename IdFn>
+__device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScratch& s,
+                                  bool force_miss = false, int ts = -1) {
   FastResult res;
   res.ok = true;
   res.ncand = 0;
@@ -122,7 +147,7 @@ __device__ FastResult fast_select(const uint16_t* __restrict__ row, int n, int k
   for (int u = 0; u < FS_PER; ++u) {
     const int j = (int)threadIdx.x + u * SEL_BLOCK;
     const int i = full ? j : (int)(((uint64_t)j * (uint64_t)n) >> 12);
-    sv[u] = (full && j >= n) ? 0u : (uint32_t)row[i];
+    sv[u] = (full && j >= n) ? 0u : src.at(i);
   }
   for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
   if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
@@ -168,13 +193,12 @@ __device__ FastResult fast_select(const uint16_t* __restrict__ row, int n, int k
     const int lane = threadIdx.x & 63;
     const int no = (n + 7) >> 3;
     const uint32_t cut16 = cut << 16;
-    const uint4* __restrict__ r4 = reinterpret_cast<const uint4*>(row);
     for (int base = threadIdx.x & ~63; base < no; base += FS_OCT * SEL_BLOCK) {
       uint4 w[FS_OCT];
 #pragma unroll
       for (int r = 0; r < FS_OCT; ++r) {
         const int o = base + r * SEL_BLOCK + lane;
-        w[r] = o < no ? r4[o] : make_uint4(0, 0, 0, 0);
+        w[r] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
       }
       uint32_t mask = 0;
 #pragma unroll
@@ -220,8 +244,8 @@ __device__ FastResult fast_select(const uint16_t* __restrict__ row, int n, int k
     for (int u = 0; u < FS_IDS; ++u) {
       const int c = (int)threadIdx.x + u * SEL_BLOCK;
       posr[u] = c < nc ? (int)s.cand[c] : 0;
-      idr[u] = c < nc ? id(posr[u]) : 0u;
-      scr[u] = c < nc ? (uint32_t)row[posr[u]] : 0u;
+      idr[u] = (c < nc && !VALUE_ONLY) ? id(posr[u]) : 0u;
+      scr[u] = c < nc ? src.at(posr[u]) : 0u;
     }
     uint32_t mx = 0;
 #pragma unroll
@@ -280,7 +304,7 @@ __device__ FastResult fast_select(const uint16_t* __restrict__ row, int n, int k
   res.sel.above = above;
   SKV_TS(ts, 5);
   const int need = k - above;
-  if (need >= ties) return res;  // every tie is a member
+  if (VALUE_ONLY || need >= ties) return res;  // every tie is a member
 
   // ---- ties at v: the `need` lowest IDs win
   if (ties <= FS_TIE_RANK) {

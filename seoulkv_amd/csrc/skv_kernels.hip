@@ -1,14 +1,15 @@
 // SeoulKV4 sparse decode step for MI355X (gfx950).
 //
 // One decode step, per KV group g (4 query heads each):
-//   qprep       q, q15 = bf16(q s / 64), qs = bf16(q s / 256) -> fixed-point
-//               int8 limb images (+ ||q|| lambda); clears per-step counters
-//   coarse      2-bit centroid intervals [lower, upper] for every centroid
-//   thresh      per head: the P-th largest lower bound
-//   fine        per centroid: survivor mask (upper >= threshold) and the
-//               4-bit fine score of every eligible (centroid, head)
-//   fine_select per head: top-P eligible centroids -> selected bitmap (union)
-//   pool_count  per selected cluster: postings owned under spill-2 mate rule
+//   front       query operands (q, q15 = bf16(q s / 64), qs = bf16(q s / 256)
+//               -> fixed-point int8 limb images, ||q|| lambda), then for every
+//               centroid the 2-bit interval [lower, upper] and the 4-bit fine
+//               score of each head
+//   select      per head: the P-th largest lower bound, then the top-P fine
+//               scores among centroids whose upper bound reaches it ->
+//               selected bitmap (union); extra blocks: sink/local attention
+//   pool_count  survivor masks; per selected cluster and 64-posting chunk:
+//               postings owned under the spill-2 mate rule
 //   pool_emit   selected list + pool tokens in encounter order
 //   score2      2-bit scores of the pool
 //   top1600     per head: top-1600 of the pool -> membership bitmap
@@ -16,8 +17,7 @@
 //   top256      per head: top-256 of U1 -> membership bitmap
 //   union_score8  U2 = union over heads in U1 order + 8-bit scores of U2
 //   top100      per head: best-first top-100 token IDs, then FP8 attention over
-//               them merged with the sink/local attention slices (computed
-//               by extra blocks of the thresh launch; they depend only on Q)
+//               them merged with the sink/local attention slices
 // Reference stages: see the table in skv_step.h.
 //
 // Selection keys are (ordered BF16 score, lowest ID first); all score dots
@@ -36,80 +36,81 @@ __device__ unsigned long long g_skv_trace_blk[4][4096][4];
 #endif
 
 // ============================================================ query prep
-// Grid (G, QV_COUNT), 256 threads: thread d owns dim d of the 4 heads.
-__global__ __launch_bounds__(256) void k_qprep(StepArgs a) {
-  SKV_TS(0, 0);
-  const int g = blockIdx.x, v = blockIdx.y, d = threadIdx.x;
-  const int lane = d & 63, wave = d >> 6;
-  __shared__ int s_X[H][D];
-  __shared__ int s_max[H][4];
-  __shared__ long long s_sum[H][4], s_sq[H][4];
+// Fixed-point operand of query variant v for KV group g, computed by one
+// 256-thread block: wave h owns head h, lane l dims 4l .. 4l+3.  Writes the
+// integers X, their sum, the scale exponent, ||q|| lambda (raw variant) and
+// the int8 limb B image to *out (LDS or global memory).
+// Sum of squares: X^2 < 2^44 is split into 22-bit halves so that both wave
+// sums stay below 2^30 (exact in int32).
+struct QPrepScratch {
+  int X[H][D];
+};
 
-  if (v == 0 && d == 0) a.status[g * ST_WORDS + ST_FULLSEL] = 0;
-  {  // per-step counters: pool histograms, selected bitmap, SDPA tickets
-    const int blk = g * QV_COUNT + v, nblk = G * QV_COUNT;
-    for (size_t i = (size_t)blk * 256 + d; i < a.zero_words; i += (size_t)nblk * 256)
-      a.zero_base[i] = 0;
-  }
-  QOperand* out = &a.qop[g * QV_COUNT + v];
-  int X[H], ex[H], sig[H];
-  uint32_t bits[H];
+__device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out) {
+  const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+  const uint2 qw = *reinterpret_cast<const uint2*>(a.q + (g * H + h) * D + 4 * lane);
+  const uint32_t qb[4] = {qw.x & 0xffffu, qw.x >> 16, qw.y & 0xffffu, qw.y >> 16};
+  uint32_t bits[4];
+  if (v != QV_RAW) {
+    const float4 ks = *reinterpret_cast<const float4*>(a.kscale + g * D + 4 * lane);
+    const float kv[4] = {ks.x, ks.y, ks.z, ks.w};
+    const float mul = v == QV_Q15 ? 0.015625f : 0.00390625f;
 #pragma unroll
-  for (int h = 0; h < H; ++h) {
-    const uint32_t qb = a.q[(g * H + h) * D + d];
-    uint32_t b = qb;
-    if (v != QV_RAW) {
-      const float prod = __fmul_rn(bf16_f32(qb), a.kscale[g * D + d]);
-      b = bf16_rne(__fmul_rn(prod, v == QV_Q15 ? 0.015625f : 0.00390625f));
-    }
-    bits[h] = b;
-    const int expf = (b >> 7) & 0xff, mant = b & 0x7f;
-    sig[h] = expf ? (mant | 0x80) : mant;
-    ex[h] = expf ? expf - 134 : -133;
-    const int m = wave_max(sig[h] ? ex[h] : -(1 << 20));
-    if (lane == 0) s_max[h][wave] = m;
-  }
-  __syncthreads();
+    for (int i = 0; i < 4; ++i) bits[i] = bf16_rne(__fmul_rn(__fmul_rn(bf16_f32(qb[i]), kv[i]), mul));
+  } else {
 #pragma unroll
-  for (int h = 0; h < H; ++h) {
-    int exmax = max(max(s_max[h][0], s_max[h][1]), max(s_max[h][2], s_max[h][3]));
-    if (exmax == -(1 << 20)) exmax = 0;
-    const int shift = ex[h] - exmax + FX_HEADROOM;
-    const int mag = shift >= 0 ? (sig[h] << shift) : (shift <= -9 ? 0 : (sig[h] >> -shift));
-    X[h] = (bits[h] & 0x8000u) ? -mag : mag;
-    s_X[h][d] = X[h];
-    out->X[h][d] = X[h];
-    const long long sx = wave_sum64((long long)X[h]);
-    const long long sq = wave_sum64((long long)X[h] * X[h]);
-    if (lane == 0) {
-      s_sum[h][wave] = sx;
-      s_sq[h][wave] = sq;
-    }
-    if (d == 0) out->fx[h] = exmax - FX_HEADROOM;
+    for (int i = 0; i < 4; ++i) bits[i] = qb[i];
   }
-  __syncthreads();
-  if (d < H) {
-    const int h = d;
-    out->sum[h] = s_sum[h][0] + s_sum[h][1] + s_sum[h][2] + s_sum[h][3];
+  int sig[4], ex[4], emax = -(1 << 20);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int expf = (bits[i] >> 7) & 0xff, mant = bits[i] & 0x7f;
+    sig[i] = expf ? (mant | 0x80) : mant;
+    ex[i] = expf ? expf - 134 : -133;
+    if (sig[i]) emax = max(emax, ex[i]);
+  }
+  int exmax = wave_max(emax);
+  if (exmax == -(1 << 20)) exmax = 0;
+  int X[4], sx = 0, sq_lo = 0, sq_hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int shift = ex[i] - exmax + FX_HEADROOM;
+    const int mag = shift >= 0 ? (sig[i] << shift) : (shift <= -9 ? 0 : (sig[i] >> -shift));
+    X[i] = (bits[i] & 0x8000u) ? -mag : mag;
+    sx += X[i];
+    const uint64_t x2 = (uint64_t)((int64_t)X[i] * X[i]);
+    sq_lo += (int)(x2 & 0x3fffffu);
+    sq_hi += (int)(x2 >> 22);
+  }
+  *reinterpret_cast<int4*>(&s.X[h][4 * lane]) = make_int4(X[0], X[1], X[2], X[3]);
+  *reinterpret_cast<int4*>(&out->X[h][4 * lane]) = make_int4(X[0], X[1], X[2], X[3]);
+  sx = wave_sum(sx);
+  sq_lo = wave_sum(sq_lo);
+  sq_hi = wave_sum(sq_hi);
+  if (lane == 0) {
+    out->fx[h] = exmax - FX_HEADROOM;
+    out->sum[h] = sx;
     if (v == QV_RAW) {
-      const unsigned long long N =
-          (unsigned long long)(s_sq[h][0] + s_sq[h][1] + s_sq[h][2] + s_sq[h][3]);
-      out->norm[h] = __fmul_rn(sqrt_rne_scaled(N, out->fx[h]), a.lam[g]);
+      const unsigned long long N = ((unsigned long long)sq_hi << 22) + (unsigned long long)sq_lo;
+      out->norm[h] = __fmul_rn(sqrt_rne_scaled(N, exmax - FX_HEADROOM), a.lam[g]);
     } else {
       out->norm[h] = 0.f;
     }
   }
+  __syncthreads();
   // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
   // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int w = d + 256 * i;  // 0..1023
+    const int w = threadIdx.x + 256 * i;  // 0..1023
     const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
     const int col = l & 15, hh = col >> 2, limb = col & 3;
+    const int4 x4 = *reinterpret_cast<const int4*>(&s.X[hh][(l >> 4) * 64 + kc * 16 + 4 * m]);
+    const int xs[4] = {x4.x, x4.y, x4.z, x4.w};
     uint32_t word = 0;
 #pragma unroll
     for (int byte = 0; byte < 4; ++byte) {
-      const int x = s_X[hh][(l >> 4) * 64 + kc * 16 + 4 * m + byte];
+      const int x = xs[byte];
       const int l0 = (int)(int8_t)(x & 0xff);
       const int x1 = (x - l0) >> 8;
       const int l1 = (int)(int8_t)(x1 & 0xff);
@@ -119,6 +120,7 @@ __global__ __launch_bounds__(256) void k_qprep(StepArgs a) {
     }
     out->bimg[kc][l][m] = word;
   }
+  __syncthreads();
 }
 
 // Load the 16-register B operand of a query variant for this lane.
@@ -134,7 +136,7 @@ __device__ __forceinline__ void load_b(const QOperand* q, uint32_t b[4][4]) {
 // ============================================================ sparse SDPA
 // Attention of query head j = 4g + h over its KV group's FP8 [V || K] records
 // for the keys [sink | local | top-100] (softmax over all of them, scale 1/16).
-// The sink/local part depends only on Q: extra blocks of the k_thresh launch
+// The sink/local part depends only on Q: extra blocks of the k_select launch
 // compute it as 128-key slices (partial max, sum, unnormalised output), and
 // k_top100 attends the head's 100 selected keys and merges everything.
 constexpr int SDPA_WAVE_KEYS = 16;
@@ -260,153 +262,159 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
   }
 }
 
-// ============================================================ coarse
-// Wave tile: 16 centroids x 4 heads.  lower/upper = bf16(value -/+ margin),
-// value = RNE(sum q (2u - 3)) * scale/4, margin = ||q|| lambda bf16(resid).
-__global__ __launch_bounds__(256) void k_coarse(StepArgs a) {
-  SKV_TS(1, 0);
-  const int g = blockIdx.y;
+// ============================================================ front
+// One wave tile = 16 centroids x 4 heads.  Every block first forms the raw
+// query operand of its group in LDS (its centroid-plane loads are already in
+// flight), then per centroid and head:
+//   coarse  lower/upper = bf16(value -/+ margin), value = RNE(sum q (2u - 3))
+//           * scale/4, margin = ||q|| lambda bf16(resid)  (ordered, all heads)
+//   fine    bf16(RNE(sum q (2 code4 - 15)) * group_fine_scale)  (ordered;
+//           eligibility is applied by the selection kernel)
+// Block 0 of each group also publishes the raw operand and clears the
+// group's per-step state; two extra blocks per group publish the q15 / qs
+// operands for the later kernels.
+__global__ __launch_bounds__(256) void k_front(StepArgs a) {
+  SKV_TS(0, 0);
+  const int g = blockIdx.y, nc = a.nc;
+  __shared__ __align__(16) QPrepScratch sp;
+  const int tiles_blocks = (nc + 63) / 64;
+  if ((int)blockIdx.x >= tiles_blocks) {
+    const int v = QV_Q15 + (blockIdx.x - tiles_blocks);
+    prep_operand(a, g, v, sp, &a.qop[g * QV_COUNT + v]);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int nc = a.nc;
-  if (tile * 16 >= nc) return;
-  const QOperand* q = &a.qop[g * QV_COUNT + QV_RAW];
-  uint32_t b[4][4];
-  load_b(q, b);
+  const bool has = tile * 16 < nc;
   const int row = lane & 15, kb = lane >> 4;
-  const uint4 w = *reinterpret_cast<const uint4*>(
-      a.cen_up + ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16);
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-  v4i acc = {0, 0, 0, 0};
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc) {
-    uint32_t av[4];
-    expand2(words[kc], av);
-    acc = mfma_i8(av, b[kc], acc);
+  uint4 wu = make_uint4(0, 0, 0, 0), wl = make_uint4(0, 0, 0, 0);
+  if (has) {
+    const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
+    wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
+    wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
   }
-  int64_t dot[4];
-  combine_limbs(acc, dot);
-  if ((lane & 3) == 0) {
-    const int h = (lane & 15) >> 2;
-    const int64_t S = q->sum[h];
-    const int fx = q->fx[h];
-    const float norm = q->norm[h];
+  if (blockIdx.x == 0) {  // per-step state of the group
+    uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
+    for (int i = threadIdx.x; i < nc / 32; i += 256) bm[i] = 0;
+    if (threadIdx.x == 0) a.status[g * ST_WORDS + ST_FULLSEL] = 0;
+  }
+  __shared__ __align__(16) QOperand sq;
+  prep_operand(a, g, QV_RAW, sp, &sq);
+  SKV_TS(0, 1);
+  if (has) {
+    uint32_t b[4][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tile * 16 + 4 * kb + r;
-      const float val = scaled_f32(2 * dot[r] - 3 * S, fx);
-      const float value = __fmul_rn(val, a.scale4[(size_t)g * (nc / 32) + c / 32]);
-      const float margin = __fmul_rn(norm, a.resid[(size_t)g * nc + c]);
-      const size_t o = ((size_t)g * H + h) * nc + c;
-      a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
-      a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
+    for (int kc = 0; kc < 4; ++kc) {
+      const uint4 w = *reinterpret_cast<const uint4*>(&sq.bimg[kc][lane][0]);
+      b[kc][0] = w.x; b[kc][1] = w.y; b[kc][2] = w.z; b[kc][3] = w.w;
     }
+    const uint32_t up[4] = {wu.x, wu.y, wu.z, wu.w};
+    const uint32_t lo[4] = {wl.x, wl.y, wl.z, wl.w};
+    v4i acc_c = {0, 0, 0, 0}, acc_f = {0, 0, 0, 0};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      uint32_t eu[4], el[4], a4[4];
+      expand2(up[kc], eu);
+      expand2(lo[kc], el);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) a4[m] = (eu[m] << 2) | el[m];
+      acc_c = mfma_i8(eu, b[kc], acc_c);
+      acc_f = mfma_i8(a4, b[kc], acc_f);
+    }
+    int64_t dc[4], df[4];
+    combine_limbs(acc_c, dc);
+    combine_limbs(acc_f, df);
+    if ((lane & 3) == 0) {
+      const int h = (lane & 15) >> 2;
+      const int64_t S = sq.sum[h];
+      const int fx = sq.fx[h];
+      const float norm = sq.norm[h];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = tile * 16 + 4 * kb + r;
+        const float val = scaled_f32(2 * dc[r] - 3 * S, fx);
+        const float value = __fmul_rn(val, a.scale4[(size_t)g * (nc / 32) + c / 32]);
+        const float margin = __fmul_rn(norm, a.resid[(size_t)g * nc + c]);
+        const size_t o = ((size_t)g * H + h) * nc + c;
+        a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
+        a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
+        const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
+        const uint32_t fb = bf16_rne(__fmul_rn(fv, a.gfs[(size_t)g * (nc / 32) + c / 32]));
+        a.fine_ord[o] = (uint16_t)ordered16(fb);
+        if (a.debug) a.fine_bits[o] = (uint16_t)fb;
+      }
+    }
+  }
+  SKV_TS(0, 2);
+  if (blockIdx.x == 0) {  // publish the raw operand (a copy of sq)
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&sq);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + QV_RAW]);
+    for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += 256) dst[i] = src[i];
   }
 }
 
 __device__ __forceinline__ uint32_t same16(uint32_t o) { return o; }
 
-// ============================================================ thresholds
-// Per (group, head): the P-th largest lower bound (its value only).  Blocks
+// ============================================================ centroid selection
+// Per (group, head): the P-th largest lower bound thr, then the P centroids
+// with the best (fine score, lowest ID) among those whose upper bound reaches
+// thr; members set their bit in the group's selected-cluster bitmap.  Blocks
 // beyond the 16 (group, head) pairs compute the sink/local attention slices.
-__global__ __launch_bounds__(SEL_BLOCK) void k_thresh(StepArgs a) {
+__device__ __forceinline__ void load_lds_masked(uint16_t* so, const uint16_t* __restrict__ score,
+                                                const uint16_t* __restrict__ gate, uint32_t thr,
+                                                int n) {
+  const MaskedScores src{score, gate, thr};
+  uint4* d4 = reinterpret_cast<uint4*>(so);
+  for (int o = threadIdx.x; o < (n >> 3); o += blockDim.x) d4[o] = src.oct(o);
+}
+
+__global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   SKV_TS(2, 0);
   extern __shared__ __align__(16) unsigned char dyn[];
   if (blockIdx.x >= G * H) {  // sink/local attention slices (depend only on Q)
     dense_attend(a, blockIdx.x - G * H, *reinterpret_cast<AttnScratch*>(dyn));
     return;
   }
-  const int g = blockIdx.x / H, h = blockIdx.x % H;
-  __shared__ SelectScratch s;
-  // ordered bounds; a non-NaN bound never maps to ordered 0, the "excluded" mark
-  const uint16_t* lo = a.lower + ((size_t)g * H + h) * a.nc;
-  if (a.exact_select != 1) {
-    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(lo, a.nc, a.P[g], [](int i) { return (uint32_t)i; }, fs,
-                                     a.exact_select == 2, 2);
-    if (r.ok) {
-      SKV_TS(2, 15);
-      if (threadIdx.x == 0) a.thr[g * H + h] = r.sel.all ? 0u : r.sel.v;
-      return;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) atomicOr(&a.status[g * ST_WORDS + ST_FULLSEL], FS_THRESH);
-  }
-  uint16_t* so = reinterpret_cast<uint16_t*>(dyn);  // nc ordered lower bounds
-  load_lds_scores(so, lo, a.nc, same16);
-  __syncthreads();
-  const Selection sel = block_select(so, a.nc, a.P[g], [](int i) { return (uint32_t)i; }, s);
-  if (threadIdx.x == 0) a.thr[g * H + h] = sel.all ? 0u : sel.v;
-}
-
-// ============================================================ fine
-// Every centroid: survivor mask (bit h iff ordered(upper_h) >= threshold_h)
-// and the 4-bit score bf16(RNE(sum q (2 code4 - 15)) * group_fine_scale) of
-// each eligible head.  fine_ord[g][h][c] = ordered score, or 0 if ineligible.
-__global__ __launch_bounds__(256) void k_fine(StepArgs a) {
-  SKV_TS(3, 0);
-  const int g = blockIdx.y, nc = a.nc;
-  const int lane = threadIdx.x & 63;
-  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile * 16 >= nc) return;
-  const QOperand* q = &a.qop[g * QV_COUNT + QV_RAW];
-  uint32_t b[4][4];
-  load_b(q, b);
-  const int row = lane & 15, kb = lane >> 4;
-  const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
-  const uint4 wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
-  const uint4 wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
-  const uint32_t up[4] = {wu.x, wu.y, wu.z, wu.w};
-  const uint32_t lo[4] = {wl.x, wl.y, wl.z, wl.w};
-  v4i acc = {0, 0, 0, 0};
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc) {
-    uint32_t eu[4], el[4], av[4];
-    expand2(up[kc], eu);
-    expand2(lo[kc], el);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) av[m] = (eu[m] << 2) | el[m];
-    acc = mfma_i8(av, b[kc], acc);
-  }
-  int64_t dot[4];
-  combine_limbs(acc, dot);
-  const int h = (lane & 15) >> 2;
-  const uint32_t thr = a.thr[g * H + h];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = tile * 16 + 4 * kb + r;
-    const bool ok = a.upper[((size_t)g * H + h) * nc + c] >= thr;
-    uint32_t m = (uint32_t)ok << h;  // gather the 4 heads' bits (lanes ^4, ^8)
-    m |= __shfl_xor(m, 4, WAVE);
-    m |= __shfl_xor(m, 8, WAVE);
-    if ((lane & 3) == 0) {
-      const float val = scaled_f32(2 * dot[r] - 15 * q->sum[h], q->fx[h]);
-      const uint32_t bits = bf16_rne(__fmul_rn(val, a.gfs[(size_t)g * (nc / 32) + c / 32]));
-      const size_t o = ((size_t)g * H + h) * nc + c;
-      a.fine_ord[o] = ok ? (uint16_t)ordered16(bits) : 0;
-      if (a.debug) a.fine_bits[o] = ok ? (uint16_t)bits : 0xffff;
-      if (h == 0) a.masks[(size_t)g * nc + c] = (uint8_t)m;
-    }
-  }
-}
-
-// ============================================================ fine select
-// Per (group, head): the P eligible centroids with the best (fine score,
-// lowest ID); members set their bit in the group's selected-cluster bitmap.
-__global__ __launch_bounds__(SEL_BLOCK) void k_fine_select(StepArgs a) {
-  SKV_TS(4, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H, nc = a.nc;
   __shared__ SelectScratch s;
-  extern __shared__ __align__(16) unsigned char dyn[];
-  const uint16_t* f = a.fine_ord + ((size_t)g * H + h) * nc;
-  uint32_t* selbm = a.selbm + (size_t)g * (nc / 32);
+  __shared__ uint32_t s_thr;
+  const size_t row = ((size_t)g * H + h) * nc;
+  const uint16_t* lo = a.lower + row;  // ordered; never 0 (the "excluded" mark)
+  const uint16_t* up = a.upper + row;
+  const uint16_t* fi = a.fine_ord + row;
+  const bool force = a.exact_select == 2;
+  auto cid = [](int i) { return (uint32_t)i; };
+  // ---- threshold: the P-th largest lower bound (its value)
   bool done = false;
   if (a.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(f, nc, a.P[g], [](int i) { return (uint32_t)i; }, fs,
-                                     a.exact_select == 2, 4);
+    const FastResult r = fast_select<true>(RowScores{lo}, nc, a.P[g], cid, fs, force, 2);
     if (r.ok) {
-      SKV_TS(4, 6);
+      if (threadIdx.x == 0) s_thr = r.sel.all ? 0u : r.sel.v;
+      done = true;
+    } else {
+      __syncthreads();
+      if (threadIdx.x == 0) atomicOr(&a.status[g * ST_WORDS + ST_FULLSEL], FS_THRESH);
+    }
+  }
+  if (!done) {
+    uint16_t* so = reinterpret_cast<uint16_t*>(dyn);
+    load_lds_scores(so, lo, nc, same16);
+    __syncthreads();
+    const Selection sel = block_select(so, nc, a.P[g], cid, s);
+    if (threadIdx.x == 0) s_thr = sel.all ? 0u : sel.v;
+  }
+  __syncthreads();
+  const uint32_t thr = s_thr;
+  if (threadIdx.x == 0) a.thr[g * H + h] = thr;
+  SKV_TS(2, 6);
+  // ---- fine select among the eligible centroids
+  uint32_t* selbm = a.selbm + (size_t)g * (nc / 32);
+  done = false;
+  if (a.exact_select != 1) {
+    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    const FastResult r = fast_select(MaskedScores{fi, up, thr}, nc, a.P[g], cid, fs, force, 4);
+    if (r.ok) {
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
         if (r.sel.member(cand_ord(key), cand_id(key))) {
@@ -421,27 +429,15 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_fine_select(StepArgs a) {
     }
   }
   if (!done) {
-    uint16_t* so = reinterpret_cast<uint16_t*>(dyn);  // nc ordered fine scores
-    load_lds_scores(so, f, nc, same16);
+    uint16_t* so = reinterpret_cast<uint16_t*>(dyn);
+    load_lds_masked(so, fi, up, thr, nc);
     __syncthreads();
-    const Selection sel = block_select(so, nc, a.P[g], [](int c) { return (uint32_t)c; }, s);
+    const Selection sel = block_select(so, nc, a.P[g], cid, s);
     for_scores(so, nc, [&](int c, uint32_t o) {
       if (sel.member(o, (uint32_t)c)) atomicOr(&selbm[c >> 5], 1u << (c & 31));
     });
   }
-  if (h == 0) {  // survivors: centroids with a nonzero head mask
-    __shared__ int s_cnt[SEL_WAVES + 1];
-    const uint32_t* m4 = reinterpret_cast<const uint32_t*>(a.masks + (size_t)g * nc);
-    int surv = 0;
-    for (int i = threadIdx.x; i < nc / 4; i += SEL_BLOCK) {
-      const uint32_t w = m4[i];
-      surv += ((w & 0xffu) != 0) + ((w & 0xff00u) != 0) + ((w & 0xff0000u) != 0) + ((w >> 24) != 0);
-    }
-    int total;
-    block_excl_scan(surv, s_cnt, &total);
-    if (threadIdx.x == 0) a.status[g * ST_WORDS + ST_SURV] = total;
-  }
-  SKV_TS(4, 15);
+  SKV_TS(2, 15);
 }
 
 // ============================================================ pool
@@ -495,6 +491,18 @@ __global__ __launch_bounds__(PC_BLOCK) void k_pool_count(StepArgs a) {
   __shared__ int s_off[33], s_cb[33];
   __shared__ int s_own[PC_WAVES], s_scan[PC_WAVES], s_items[PC_WAVES];
   stage_range(a, g, b, s_bm, s_off, s_cb);
+  if (threadIdx.x < 64) {  // survivor head masks of the range: upper_h >= thr_h
+    const int c = b * 32 + (threadIdx.x & 31);
+    uint32_t m = 0;
+    if (threadIdx.x < 32) {
+#pragma unroll
+      for (int h = 0; h < H; ++h)
+        m |= (uint32_t)(a.upper[((size_t)g * H + h) * a.nc + c] >= a.thr[g * H + h]) << h;
+      a.masks[(size_t)g * a.nc + c] = (uint8_t)m;
+    }
+    const uint64_t alive = __ballot(m != 0);
+    if (threadIdx.x == 0) a.surv_cnt[(size_t)g * a.pool_blocks + b] = __popcll(alive);
+  }
   __syncthreads();
   const uint32_t M = s_bm[b];
   const int nsel = __popc(M);
@@ -572,6 +580,9 @@ __global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
     ps = wave_sum(ps);
     po = wave_sum(po);
     if (last) {
+      int sv = 0;
+      for (int i = lane; i < a.pool_blocks; i += 64) sv += a.surv_cnt[(size_t)g * a.pool_blocks + i];
+      sv = wave_sum(sv);
       ts = wave_sum(ts);
       to = wave_sum(to);
       tn = wave_sum(tn);
@@ -582,6 +593,7 @@ __global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
         a.status[g * ST_WORDS + ST_POOL] = min(to, a.cap);
         a.status[g * ST_WORDS + ST_ERR] = err;
         a.status[g * ST_WORDS + ST_SEL] = ts;
+        a.status[g * ST_WORDS + ST_SURV] = sv;
         a.status[g * ST_WORDS + ST_SCANNED] = tn;
       }
     }
@@ -695,7 +707,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   auto id = [&](int i) { return (uint32_t)tok[i]; };
   if (t.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(sc, n, t.k, id, fs, t.exact_select == 2, ts);
+    const FastResult r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
     if (r.ok) {
       SKV_TS(ts, 6);
       const int words = (n + 63) / 64;
@@ -939,7 +951,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   bool done = false;
   if (a.exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(sc, n, TOPK, id, fs, a.exact_select == 2, 13);
+    const FastResult r = fast_select(RowScores{sc}, n, TOPK, id, fs, a.exact_select == 2, 13);
     if (r.ok) {
       SKV_TS(13, 6);
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
@@ -1026,8 +1038,8 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
-    "qprep", "coarse", "thresh", "fine", "fine_select", "pool_count", "pool_emit", "score2",
-    "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
+    "front", "select", "pool_count", "pool_emit", "score2", "top1600", "union_score4",
+    "top256", "union_score8", "top100_sdpa"};
 
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
@@ -1037,43 +1049,34 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
   const size_t bm_lds = (size_t)(a.nc / 32) * 4;
   switch (k) {
     case 0:
-      hipLaunchKernelGGL(k_qprep, dim3(G, QV_COUNT), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(k_front, dim3(tiles_blocks + 2, G), dim3(256), 0, st, a);
       break;
     case 1:
-      hipLaunchKernelGGL(k_coarse, dim3(tiles_blocks, G), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
+                         w.select_lds, st, a);
       break;
     case 2:
-      hipLaunchKernelGGL(k_thresh, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
-                         w.thresh_lds, st, a);
-      break;
-    case 3:
-      hipLaunchKernelGGL(k_fine, dim3(tiles_blocks, G), dim3(256), 0, st, a);
-      break;
-    case 4:
-      hipLaunchKernelGGL(k_fine_select, dim3(G * H), dim3(SEL_BLOCK), w.fine_select_lds, st, a);
-      break;
-    case 5:
       hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(PC_BLOCK), bm_lds, st, a);
       break;
-    case 6:
+    case 3:
       hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(PE_BLOCK), bm_lds, st, a);
       break;
-    case 7:
+    case 4:
       hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);
       break;
-    case 8:
+    case 5:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
       break;
-    case 9:
+    case 6:
       hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(US_BLOCK), 0, st, a);
       break;
-    case 10:
+    case 7:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
       break;
-    case 11:
+    case 8:
       hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(US_BLOCK), 0, st, a);
       break;
-    case 12:
+    case 9:
       hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
       break;
     default:

@@ -374,13 +374,11 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.own_cnt = (int*)ar.take((size_t)G * nc * 4);
     a.own_chunk = (int*)ar.take((size_t)G * a.chunks_max * 4);
     a.range_cnt = (int4*)ar.take((size_t)G * a.pool_blocks * 16);
+    a.surv_cnt = (int*)ar.take((size_t)G * a.pool_blocks * 4);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
     a.dense_part = (float*)ar.take((size_t)G * H * std::max(a.dense_slices, 1) * (D + 2) * 4);
-    // one contiguous range cleared by k_qprep every step
-    a.zero_words = (size_t)G * (nc / 32);
-    a.zero_base = (uint32_t*)ar.take(a.zero_words * 4);
-    a.selbm = a.zero_base;
+    a.selbm = (uint32_t*)ar.take((size_t)G * (nc / 32) * 4);  // cleared by k_front
     a.u1_tok = (int*)ar.take((size_t)G * U1_MAX * 4);
     a.s4 = (uint16_t*)ar.take((size_t)G * H * U1_MAX * 2);
     a.u2_tok = (int*)ar.take((size_t)G * U2_MAX * 4);
@@ -502,8 +500,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   // LDS-resident scores of the full selection, or the attention scratch of
   // the sink/local blocks, whichever is largest (they are never live together).
   const size_t fs_bytes = sizeof(FastScratch);
-  w.thresh_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES});
-  w.fine_select_lds = std::max(fs_bytes, (size_t)nc * 2);
+  w.select_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES});
   w.top_u1_lds = std::max(fs_bytes, (size_t)w.top_u1.lds_items * 2);
   w.top_u2_lds = std::max(fs_bytes, (size_t)w.top_u2.lds_items * 2);
 
@@ -720,9 +717,18 @@ int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t c
       return copy_rows(a.thr + group * H, 0, 4, H, 1);
     case SKV_STAGE_MASKS:
       return copy_rows(a.masks + (size_t)group * nc, 0, 1, nc, 1);
-    case SKV_STAGE_FINE:
+    case SKV_STAGE_FINE: {  // BF16 fine scores; 0xffff where the head is ineligible
       if (!a.debug) return fail(h, SKV_ESTATE, "fine scores need debug=1");
-      return copy_rows(a.fine_bits + (size_t)group * H * nc, nc, 2, nc, H);
+      const int rc = copy_rows(a.fine_bits + (size_t)group * H * nc, nc, 2, nc, H);
+      if (rc != SKV_OK) return rc;
+      std::vector<uint8_t> m(nc);
+      HIPCHK(h, hipMemcpy(m.data(), a.masks + (size_t)group * nc, nc, hipMemcpyDeviceToHost));
+      uint16_t* o = static_cast<uint16_t*>(host_out);
+      for (int hh = 0; hh < H; ++hh)
+        for (int c = 0; c < nc; ++c)
+          if (!((m[c] >> hh) & 1)) o[(size_t)hh * nc + c] = 0xffff;
+      return SKV_OK;
+    }
     case SKV_STAGE_SELECTED:
       return copy_rows(a.sel + (size_t)group * nc, 0, 4, st[ST_SEL], 1);
     case SKV_STAGE_POOL:

@@ -1,13 +1,14 @@
 // Argument blocks of the decode-step kernels and their reference stages.
 //
 //   kernel           reference stage (src/seoulkv4/...)
-//   k_qprep          _kernels/query_prepare/host.py:26-51 (q15, qs, ||q|| lambda)
-//   k_coarse         codegen/coarse_compute.py:61-119 (2-bit interval scores)
-//   k_thresh         _kernels/stage1_coarse/seoulkv4_coarse_select.py:297-310
-//   k_fine           _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379 (masks),
-//                    codegen/fine_postscale_codegen.py:6-71, codegen/fine.py:1848-1861
-//   k_fine_select    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73
-//   k_pool_count     codegen/stage15.py:275-345 (mate-ownership dedup)
+//   k_front          _kernels/query_prepare/host.py:26-51 (q15, qs, ||q|| lambda);
+//                    codegen/coarse_compute.py:61-119 (2-bit interval scores);
+//                    codegen/fine_postscale_codegen.py:6-71 (4-bit fine scores)
+//   k_select         _kernels/stage1_coarse/seoulkv4_coarse_select.py:297-310 (threshold);
+//                    codegen/fine.py:1848-1861 (head masks),
+//                    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73 (top-P union)
+//   k_pool_count     _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379 (survivor
+//                    masks); codegen/stage15.py:275-345 (mate-ownership dedup)
 //   k_pool_emit      codegen/stage15.py:275-345 (encounter-order pool)
 //   k_score2         codegen/stage15.py:886-995 (2-bit scores)
 //   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
@@ -17,7 +18,7 @@
 //   k_union_score<8> codegen/refinement_fusion.py:142-186 (U2) +
 //                    _kernels/stage16/seoulkv4_union_matrix.py:58-139 (8-bit scores)
 //   k_top100         codegen/refinement_fusion.py:296-300,495-531
-//   k_thresh, k_top100  sparse SDPA: codegen/attention.py:35-201 (+ TTNN sparse_sdpa)
+//   k_select, k_top100  sparse SDPA: codegen/attention.py:35-201 (+ TTNN sparse_sdpa)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -82,21 +83,19 @@ struct StepArgs {
   uint16_t* upper;          // [G][H][nc] ordered BF16
   uint32_t* thr;            // [G][H]
   uint8_t* masks;           // [G][nc] survivor head masks
-  uint16_t* fine_ord;       // [G][H][nc] ordered fine score, 0 = ineligible
+  uint16_t* fine_ord;       // [G][H][nc] ordered fine score of every centroid
   uint16_t* fine_bits;      // [G][H][nc] BF16 fine score (debug)
   int* sel;                 // [G][nc] selected clusters, ascending
   int* own_cnt;             // [G][nc] owned postings per selected cluster
   int* own_chunk;           // [G][chunks_max] owned postings per chunk of a selected cluster
-  int4* range_cnt;          // [G][pool_blocks] {selected, owned, scanned, 0}
+  int4* range_cnt;          // [G][pool_blocks] {selected, owned, scanned, work items}
+  int* surv_cnt;            // [G][pool_blocks] coarse survivors per range
   int* pool_tok;            // [G][cap]
   uint16_t* s2;             // [G][H][cap] ordered
   uint64_t* bm_u1;          // [G][H][words_u1] top-1600 members
   uint64_t* bm_u2;          // [G][H][words_u2] top-256 members
   float* dense_part;        // [16][dense_slices][D + 2] sink/local partial (o, max, sum)
-  // zeroed by k_qprep every step (one contiguous range)
-  uint32_t* zero_base;
-  size_t zero_words;
-  uint32_t* selbm;          // [G][nc/32] selected-cluster bitmap
+  uint32_t* selbm;          // [G][nc/32] selected-cluster bitmap (cleared each step)
   int* u1_tok;              // [G][U1_MAX]
   uint16_t* s4;             // [G][H][U1_MAX] ordered
   int* u2_tok;              // [G][U2_MAX]
@@ -123,14 +122,14 @@ struct TopkArgs {
 
 struct StepWork {
   TopkArgs top_u1, top_u2;
-  size_t thresh_lds, fine_select_lds, top_u1_lds, top_u2_lds;  // selection kernels
+  size_t select_lds, top_u1_lds, top_u2_lds;  // dynamic LDS of the selection kernels
 };
 
 // LDS bytes of the attention scratch of a 512-thread block (8 waves x
 // (max, sum, o[256]) in FP32)
 constexpr size_t ATTN_SCRATCH_BYTES = (size_t)8 * (2 + D) * 4;
 
-constexpr int N_STEP_KERNELS = 13;
+constexpr int N_STEP_KERNELS = 10;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 // Kernel k (0 .. N_STEP_KERNELS - 1, in step order) of one decode step.
