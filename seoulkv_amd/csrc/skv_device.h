@@ -164,6 +164,20 @@ __device__ __forceinline__ int wave_sum(int v) {
   return __builtin_amdgcn_readlane(wave_incl_scan(v), 63);
 }
 
+// Float wave total (tree order fixed by the DPP pattern), uniform across lanes.
+#define SKV_DPP_ADDF(v, ctrl, rows, zero) \
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rows, 0xf, zero))
+__device__ __forceinline__ float wave_sum_f(float v) {
+  SKV_DPP_ADDF(v, 0x111, 0xf, true);   // row_shr:1
+  SKV_DPP_ADDF(v, 0x112, 0xf, true);   // row_shr:2
+  SKV_DPP_ADDF(v, 0x114, 0xf, true);   // row_shr:4
+  SKV_DPP_ADDF(v, 0x118, 0xf, true);   // row_shr:8
+  SKV_DPP_ADDF(v, 0x142, 0xa, false);  // row_bcast:15
+  SKV_DPP_ADDF(v, 0x143, 0xc, false);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+#undef SKV_DPP_ADDF
+
 __device__ __forceinline__ int wave_max(int v) {
   constexpr int LO = (int)0x80000000;
   v = max(v, __builtin_amdgcn_update_dpp(LO, v, 0x111, 0xf, 0xf, false));
@@ -233,9 +247,9 @@ __device__ __forceinline__ v4i mfma_i8(const uint32_t a[4], const uint32_t b[4],
 __device__ __forceinline__ void combine_limbs(v4i acc, int64_t out[4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    int v0 = acc[r];
-    int v1 = __shfl_down(v0, 1, WAVE);
-    int v2 = __shfl_down(v0, 2, WAVE);
+    const int v0 = acc[r];
+    const int v1 = __builtin_amdgcn_update_dpp(0, v0, 0x101, 0xf, 0xf, true);  // row_shl:1
+    const int v2 = __builtin_amdgcn_update_dpp(0, v0, 0x102, 0xf, 0xf, true);  // row_shl:2
     out[r] = (int64_t)v0 + ((int64_t)v1 << 8) + ((int64_t)v2 << 16);
   }
 }

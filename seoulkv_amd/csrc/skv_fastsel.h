@@ -62,7 +62,10 @@ struct MaskedScores {  // score[i] where gate[i] >= thr, else 0 (excluded)
   const uint16_t* __restrict__ score;
   const uint16_t* __restrict__ gate;
   uint32_t thr;
-  __device__ uint32_t at(int i) const { return gate[i] >= thr ? score[i] : 0u; }
+  __device__ uint32_t at(int i) const {
+    const uint32_t gv = gate[i], sv = score[i];  // both loads issued together
+    return gv >= thr ? sv : 0u;
+  }
   __device__ uint4 oct(int o) const {
     const uint4 s4 = reinterpret_cast<const uint4*>(score)[o];
     const uint4 g4 = reinterpret_cast<const uint4*>(gate)[o];
@@ -218,7 +221,7 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
       const int inc = wave_incl_scan(cnt);
       int wbase = 0;
       if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
-      wbase = __shfl(wbase, 63, WAVE);
+      wbase = __builtin_amdgcn_readlane(wbase, 63);
       int slot = wbase + inc - cnt;
       while (mask) {
         const int b = __ffs(mask) - 1;

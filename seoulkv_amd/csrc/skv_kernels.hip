@@ -167,7 +167,7 @@ __device__ __forceinline__ void wave_attend(const uint8_t* __restrict__ kv, cons
   uint32_t kw[SDPA_WAVE_KEYS], vw[SDPA_WAVE_KEYS];
 #pragma unroll
   for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
-    t[b] = __shfl(tk, b, WAVE);
+    t[b] = __builtin_amdgcn_readlane(tk, b);
     const uint8_t* rec = kv + (size_t)max(t[b], 0) * 512;
     kw[b] = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
     vw[b] = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
@@ -180,9 +180,7 @@ __device__ __forceinline__ void wave_attend(const uint8_t* __restrict__ kv, cons
     logit[b] = q[0] * kf[0] + q[1] * kf[1] + q[2] * kf[2] + q[3] * kf[3];
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-    for (int b = 0; b < SDPA_WAVE_KEYS; ++b) logit[b] += __shfl_xor(logit[b], off, WAVE);
+  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) logit[b] = wave_sum_f(logit[b]);
   m = -INFINITY;
 #pragma unroll
   for (int b = 0; b < SDPA_WAVE_KEYS; ++b)
