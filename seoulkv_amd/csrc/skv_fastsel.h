@@ -5,9 +5,9 @@
 //    bits of the chosen bin) to find a score `cut` that about
 //    k + 4 sqrt(k) + 8 items are expected to reach (exactly the k-th best
 //    score when the sample is the whole input).
-// 2. Candidates: one pass over all n scores appends the position of every
-//    item scoring >= cut to an LDS list (one atomic per wave), then loads
-//    the candidates' scores and IDs.
+// 2. Candidates: one pass over all n scores appends (score, position) of
+//    every item scoring >= cut to an LDS list (one atomic per wave).  IDs are
+//    read later, only for items tied at the k-th score.
 // 3. If the list holds fewer than k items (the sample over-estimated the
 //    cut) or overflows, the caller runs the full exact selection instead.
 //    Otherwise the top k of the input are exactly the top k of the list
@@ -27,14 +27,15 @@ constexpr int FS_PER = FS_SAMPLE / SEL_BLOCK;  // sample items per thread
 constexpr int CAND_CAP = 4096;
 constexpr int FS_TIE_RANK = SEL_BLOCK;  // ties ranked by direct comparison up to this count
 constexpr int FS_OCT = 4;  // score octets per lane per pass (a 32-bit candidate mask)
-constexpr int FS_IDS = CAND_CAP / SEL_BLOCK;  // candidate IDs loaded per thread
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct FastScratch {
   union {
     uint32_t hist[4096];
     KthScratch k;
   };
-  uint64_t cand[CAND_CAP];  // ord << 40 | (0xfffff - id) << 20 | position
+  uint64_t cand[CAND_CAP];  // ord << 40 | position
   uint32_t hist4[16];
   uint32_t tie[FS_TIE_RANK];
   int ncand;
@@ -44,11 +45,25 @@ struct FastScratch {
   int scan[SEL_WAVES + 1];
 };
 
+__device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40); }
+__device__ __forceinline__ int cand_pos(uint64_t c) { return (int)(c & 0xfffffu); }
+
 struct FastResult {
-  Selection sel;  // members are the candidates with sel.member(ord, id)
+  Selection sel;  // members: the candidates passing fs_member
   int ncand;      // candidates in FastScratch::cand
   bool ok;        // false: use the full selection
 };
+
+// Membership of candidate key c; id(position) is read only for a candidate
+// tied at the cut score when not every tie is a member.
+template <typename IdFn>
+__device__ __forceinline__ bool fs_member(const FastResult& r, uint64_t c, IdFn id) {
+  const uint32_t o = cand_ord(c);
+  if (o == 0) return false;
+  if (r.sel.all || o > r.sel.v) return true;
+  if (o < r.sel.v) return false;
+  return r.sel.idcut == 0xffffffffu || id(cand_pos(c)) <= r.sel.idcut;
+}
 
 // Score sources: at(i) = ordered score of item i; oct(o) = the 8 ordered
 // scores of items 8o .. 8o+7 as packed 16-bit pairs.
@@ -77,11 +92,6 @@ struct MaskedScores {  // score[i] where gate[i] >= thr, else 0 (excluded)
   }
 };
 
-__device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40); }
-__device__ __forceinline__ uint32_t cand_id(uint64_t c) {
-  return 0xfffffu - (uint32_t)((c >> 20) & 0xfffffu);
-}
-__device__ __forceinline__ int cand_pos(uint64_t c) { return (int)(c & 0xfffffu); }
 
 // Descending scan of a 4096-bin histogram (each thread owns 8 bins): the bin
 // holding the rank-th largest value and the count in higher bins, in
@@ -196,6 +206,7 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
     const int lane = threadIdx.x & 63;
     const int no = (n + 7) >> 3;
     const uint32_t cut16 = cut << 16;
+    uint32_t mx = 0;
     for (int base = threadIdx.x & ~63; base < no; base += FS_OCT * SEL_BLOCK) {
       uint4 w[FS_OCT];
 #pragma unroll
@@ -223,13 +234,24 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
       if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
       wbase = __builtin_amdgcn_readlane(wbase, 63);
       int slot = wbase + inc - cnt;
-      while (mask) {
-        const int b = __ffs(mask) - 1;
-        mask &= mask - 1;
-        if (slot < CAND_CAP) s.cand[slot] = (uint64_t)(8 * (base + (b >> 3) * SEL_BLOCK + lane) + (b & 7));
-        ++slot;
+#pragma unroll
+      for (int r = 0; r < FS_OCT; ++r) {  // compile-time octet: no indexed arrays
+        uint32_t m8 = (mask >> (8 * r)) & 0xffu;
+        const u32x4 wv = {w[r].x, w[r].y, w[r].z, w[r].w};
+        const int pos0 = 8 * (base + r * SEL_BLOCK + lane);
+        while (m8) {
+          const int e = __ffs(m8) - 1;
+          m8 &= m8 - 1;
+          const uint32_t word = wv[e >> 1];
+          const uint32_t o = (e & 1) ? word >> 16 : word & 0xffffu;
+          mx = max(mx, o);
+          if (slot < CAND_CAP) s.cand[slot] = ((uint64_t)o << 40) | (uint64_t)(pos0 + e);
+          ++slot;
+        }
       }
     }
+    mx = (uint32_t)wave_max((int)mx);
+    if (lane == 0) atomicMax(&s.maxo, (int)mx);
   }
   __syncthreads();
   SKV_TS(ts, 3);
@@ -239,30 +261,6 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
     res.ok = false;
     return res;
   }
-  // scores and IDs of the candidates (all loads in flight together)
-  {
-    uint32_t idr[FS_IDS], scr[FS_IDS];
-    int posr[FS_IDS];
-#pragma unroll
-    for (int u = 0; u < FS_IDS; ++u) {
-      const int c = (int)threadIdx.x + u * SEL_BLOCK;
-      posr[u] = c < nc ? (int)s.cand[c] : 0;
-      idr[u] = (c < nc && !VALUE_ONLY) ? id(posr[u]) : 0u;
-      scr[u] = c < nc ? src.at(posr[u]) : 0u;
-    }
-    uint32_t mx = 0;
-#pragma unroll
-    for (int u = 0; u < FS_IDS; ++u) {
-      const int c = (int)threadIdx.x + u * SEL_BLOCK;
-      if (c < nc) {
-        s.cand[c] = ((uint64_t)scr[u] << 40) | ((uint64_t)(0xfffffu - idr[u]) << 20) | (uint64_t)posr[u];
-        mx = max(mx, scr[u]);
-      }
-    }
-    mx = (uint32_t)wave_max((int)mx);
-    if ((threadIdx.x & 63) == 0) atomicMax(&s.maxo, (int)mx);
-  }
-  __syncthreads();
   if (cut == 1 && nc <= k) {  // fewer valid items than k: all are members
     res.sel.all = true;
     res.sel.v = 0;
@@ -313,7 +311,7 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
   if (ties <= FS_TIE_RANK) {
     for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
       const uint64_t key = s.cand[c];
-      if (cand_ord(key) == v) s.tie[atomicAdd(&s.ntie, 1)] = cand_id(key);
+      if (cand_ord(key) == v) s.tie[atomicAdd(&s.ntie, 1)] = id(cand_pos(key));
     }
     __syncthreads();
     if ((int)threadIdx.x < ties) {  // rank = number of smaller tied IDs
@@ -330,7 +328,7 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
   auto val = [&](int c, uint64_t* out) {
     const uint64_t key = s.cand[c];
     if (cand_ord(key) != v) return false;
-    *out = 0xfffffu - cand_id(key);
+    *out = 0xfffffu - id(cand_pos(key));
     return true;
   };
   const uint64_t kth = block_kth<24>(nc, need, val, s.k);

@@ -415,7 +415,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
     if (r.ok) {
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
-        if (r.sel.member(cand_ord(key), cand_id(key))) {
+        if (fs_member(r, key, cid)) {
           const int cc = cand_pos(key);
           atomicOr(&selbm[cc >> 5], 1u << (cc & 31));
         }
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
       __syncthreads();
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
-        if (r.sel.member(cand_ord(key), cand_id(key))) {
+        if (fs_member(r, key, id)) {
           const int p = cand_pos(key);
           atomicOr(reinterpret_cast<unsigned long long*>(&mb[p >> 6]), 1ull << (p & 63));
         }
@@ -954,10 +954,10 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
       SKV_TS(13, 6);
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
-        const uint32_t o = cand_ord(key), t = cand_id(key);
-        if (r.sel.member(o, t)) {
+        if (fs_member(r, key, id)) {
+          const uint32_t t = id(cand_pos(key));
           const int slot = atomicAdd(&s_cnt, 1);
-          if (slot < TOPK) s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
+          if (slot < TOPK) s_key[slot] = ((uint64_t)cand_ord(key) << 20) | (0xfffffu - t);
         }
       }
       done = true;
