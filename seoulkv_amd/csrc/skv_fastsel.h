@@ -143,9 +143,16 @@ __device__ __forceinline__ void fs_rank_digit(FastScratch& s, int rank, int acc)
 // sel.v (the k-th best score) is wanted: no IDs, no tie resolution.
 // force_miss places the cut at the best sampled score (a test of the
 // fallback: fewer than k candidates unless k ties share it).
-template <bool VALUE_ONLY = false, typename Src, typename IdFn>
-__device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScratch& s,
-                                  bool force_miss = false, int ts = -1) {
+// sample(u, i): the score of sample u (item i = fs_sample_item(n, u));
+// fast_select without it reads src.at(i).
+__device__ __forceinline__ int fs_sample_item(int n, int u) {
+  const int j = (int)threadIdx.x + u * SEL_BLOCK;
+  return n <= FS_SAMPLE ? j : (int)(((uint64_t)j * (uint64_t)n) >> 12);
+}
+
+template <bool VALUE_ONLY, typename Src, typename IdFn, typename SampleFn>
+__device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastScratch& s,
+                                    bool force_miss, int ts, SampleFn sample) {
   FastResult res;
   res.ok = true;
   res.ncand = 0;
@@ -158,9 +165,8 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
   uint32_t sv[FS_PER];
 #pragma unroll
   for (int u = 0; u < FS_PER; ++u) {
-    const int j = (int)threadIdx.x + u * SEL_BLOCK;
-    const int i = full ? j : (int)(((uint64_t)j * (uint64_t)n) >> 12);
-    sv[u] = (full && j >= n) ? 0u : src.at(i);
+    const int i = fs_sample_item(n, u);
+    sv[u] = i >= n ? 0u : sample(u, i);
   }
   for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
   if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
@@ -334,6 +340,13 @@ __device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScr
   const uint64_t kth = block_kth<24>(nc, need, val, s.k);
   res.sel.idcut = 0xfffffu - (uint32_t)kth;
   return res;
+}
+
+template <bool VALUE_ONLY = false, typename Src, typename IdFn>
+__device__ FastResult fast_select(const Src& src, int n, int k, IdFn id, FastScratch& s,
+                                  bool force_miss = false, int ts = -1) {
+  return fast_select_s<VALUE_ONLY>(src, n, k, id, s, force_miss, ts,
+                                   [&](int, int i) { return src.at(i); });
 }
 
 }  // namespace skv

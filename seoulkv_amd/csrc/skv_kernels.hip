@@ -382,6 +382,14 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   const uint16_t* fi = a.fine_ord + row;
   const bool force = a.exact_select == 2;
   auto cid = [](int i) { return (uint32_t)i; };
+  // the fine selection's sample (gate and score), loaded now, masked later
+  uint32_t pg[FS_PER], pf[FS_PER];
+#pragma unroll
+  for (int u = 0; u < FS_PER; ++u) {
+    const int i = min(fs_sample_item(nc, u), nc - 1);
+    pg[u] = up[i];
+    pf[u] = fi[i];
+  }
   // ---- threshold: the P-th largest lower bound (its value)
   bool done = false;
   if (a.exact_select != 1) {
@@ -411,7 +419,9 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   done = false;
   if (a.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(MaskedScores{fi, up, thr}, nc, a.P[g], cid, fs, force, 4);
+    const FastResult r = fast_select_s<false>(
+        MaskedScores{fi, up, thr}, nc, a.P[g], cid, fs, force, 4,
+        [&](int u, int) { return pg[u] >= thr ? pf[u] : 0u; });
     if (r.ok) {
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
