@@ -287,7 +287,7 @@ def main() -> int:
         "dtype": "int8-mfma scores / fp8-e4m3 attention",
         "data": "synthetic: seeded 4096-component Gaussian-mixture K with RoPE, N(0,1) V",
         "config": {
-            "workload": f"{args.config}: BASELINE config 2 (T={p.context}, 4 KV x 16 Q heads, "
+            "workload": f"{args.config}: BASELINE config {args.config[3:]} (T={p.context}, 4 KV x 16 Q heads, "
                         f"d=256, nc={p.n_centroids}, nprobe={p.nprobe}, top-100, sink "
                         f"{p.sink}, local {p.local}, FP8 K/V records)",
             "context": p.context,

@@ -119,26 +119,25 @@ def test_device_query_binding_matches_host_binding():
         rt.close()
 
 
-@pytest.mark.slow
-def test_full_size_parity_config2():
-    """BASELINE configuration 2 (T = 131072, nc = 8192, P = 384), every stage
-    bit-exact against the oracle on the same seeded inputs."""
+def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048):
+    """Every funnel stage bit-exact against the oracle on a BASELINE-sized
+    cache (seeded synthetic inputs), output within the attention tolerance."""
     from seoulkv_amd.index import SeoulKV4Index
     from seoulkv_amd.synthetic import make_profile
 
-    print("[gpu] cfg2 inputs", flush=True)
-    prof, k, v, qs = make_profile("cfg2")
-    index = SeoulKV4Index.build(k, v, sink=prof.sink, local=prof.local, nprobe=prof.nprobe,
-                                n_centroids=prof.n_centroids)
-    print("[gpu] cfg2 oracle", flush=True)
+    print(f"[gpu] {name} P={nprobe} clustered={clustered}: inputs", flush=True)
+    prof, k, v, qs = make_profile(name, clustered=clustered)
+    index = SeoulKV4Index.build(k, v, sink=prof.sink, local=prof.local,
+                                nprobe=nprobe or prof.nprobe, n_centroids=prof.n_centroids)
+    print(f"[gpu] {name}: oracle", flush=True)
     kb, vb = bits(k), bits(v)
     code8, scales = od.key_codec(kb)
     k8, v8 = od.fp8_records(kb, vb)
     cells = [od.GroupCell.from_cell(c) for c in index.cells]
     traces, ref = od.decode_step(cells, code8, scales, k8, v8, bits(qs[0]).reshape(16, 256),
                                  sink=prof.sink, local=prof.local)
-    print("[gpu] cfg2 device step", flush=True)
-    rt = _hip.Runtime(0, k, v, index, pool_min=2048, pool_capacity=None, debug=True)
+    print(f"[gpu] {name}: device step", flush=True)
+    rt = _hip.Runtime(0, k, v, index, pool_min=pool_min, pool_capacity=None, debug=True)
     try:
         rt.bind_query(qs[0])
         rt.enqueue()
@@ -153,6 +152,27 @@ def test_full_size_parity_config2():
         _check_output(rt.read_output(), ref)
     finally:
         rt.close()
+
+
+@pytest.mark.slow
+def test_full_size_parity_config2():
+    """T = 131072, nc = 8192, P = 384."""
+    _full_size_parity("cfg2")
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("nprobe,clustered", [(16, True), (64, True), (256, True), (512, True),
+                                              (128, False), (384, False)])
+def test_full_size_parity_config3_nprobe_sweep(nprobe, clustered):
+    """config-2 shapes over the nprobe sweep, with
+    clustered and i.i.d. keys (the i.i.d. keys give the largest pools)."""
+    _full_size_parity("cfg2", nprobe=nprobe, clustered=clustered, pool_min=0)
+
+
+@pytest.mark.slow
+def test_full_size_parity_config4():
+    """T = 1048576, nc = 65536, P = 512."""
+    _full_size_parity("cfg4")
 
 
 def test_time_kernel_keeps_the_step_consistent():
