@@ -57,7 +57,7 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         # extra blocks' sink/local FP8 [V||K] records (once per group) in and
         # their slice partials out
         "select": G * H * nc * 6 + G * nc // 8 + G * (p.sink + p.local) * 512
-        + 16 * ((p.sink + p.local + 127) // 128) * 258 * 4,
+        + 16 * ((p.sink + p.local + 255) // 256) * 258 * 4,
         # CSR bounds + mates of the selected clusters' postings; upper bounds
         # in and survivor masks out
         "pool_count": sel * (8 + 4) + scanned * 4 + G * nc * (H * 2 + 1),
@@ -77,7 +77,7 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         # U2 scores + tokens in, top-100 IDs out; the 100 FP8 [V||K] records of
         # each head, the sink/local slice partials in; BF16 output out
         "top100_sdpa": u2 * (4 + H * 2) + 16 * 100 * 4 + 16 * 100 * 512
-        + 16 * ((p.sink + p.local + 127) // 128) * 258 * 4 + 16 * 256 * 2,
+        + 16 * ((p.sink + p.local + 255) // 256) * 258 * 4 + 16 * 256 * 2,
     }
 
 

@@ -144,6 +144,16 @@ int skv_profile(void *handle, int enable);
  * records, one bit per stage (1 thresh, 2 fine select, 4 top-1600, 8 top-256,
  * 16 top-100), which selections of the last step took the full path. */
 int skv_select_mode(void *handle, int exact);
+
+/* Launch mode (no counterpart in the reference, whose programs are enqueued
+ * by TT-Metal): enable = 1 captures the step's kernels into a HIP graph on
+ * the next skv_enqueue and replays it with one host call per step; 0 (the
+ * default) launches the 10 kernels one by one.  The graph saves host time
+ * but, measured on MI355X with ROCm 7.2, consecutive graph launches leave
+ * ~8 us of device idle between them, so back-to-back steps run slower.
+ * Per-kernel profiling (skv_profile) always launches one by one.  Results
+ * are identical in both modes. */
+int skv_graph_mode(void *handle, int enable);
 int skv_profile_read(void *handle, float *mean_ms, int n, int32_t *steps);
 
 /* Duration of step kernel `kernel` alone (diagnostic; the reference's

@@ -85,6 +85,7 @@ def load_library() -> ctypes.CDLL:
         "skv_read_stage": (i32, [vp, i32, i32, vp, i64, ctypes.POINTER(i64)]),
         "skv_profile": (i32, [vp, i32]),
         "skv_select_mode": (i32, [vp, i32]),
+        "skv_graph_mode": (i32, [vp, i32]),
         "skv_time_kernel": (i32, [vp, i32, i32, vp]),
         "skv_profile_read": (i32, [vp, vp, i32, vp]),
         "skv_kernel_count": (i32, []),
@@ -206,6 +207,11 @@ class Runtime:
         self._check(self.lib.skv_time_kernel(self.handle, int(kernel), int(reps), _ptr(ms)),
                     "time_kernel")
         return float(ms[0])
+
+    def graph_mode(self, enable: bool) -> None:
+        """True: replay the step as one captured HIP graph (one host call per
+        step); False (default): launch the step's kernels one by one."""
+        self._check(self.lib.skv_graph_mode(self.handle, int(bool(enable))), "graph_mode")
 
     def select_mode(self, mode: int) -> None:
         """0: sampled cut with full fallback (default); 1: full selection

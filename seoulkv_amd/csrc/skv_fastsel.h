@@ -29,6 +29,15 @@ constexpr int FS_TIE_RANK = SEL_BLOCK;  // ties ranked by direct comparison up t
 constexpr int FS_OCT = 4;  // score octets per lane per pass (a 32-bit candidate mask)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// Packed 16-bit test of both halves of w against cut (cm1 = cut - 1 in each
+// half): bit 0 = (low half >= cut), bit 16 = (high half >= cut).
+__device__ __forceinline__ uint32_t ge_cut2(uint32_t w, u16x2 cm1) {
+  const u16x2 d = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, w), cm1);
+  const u16x2 one = {1, 1};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(d, one));
+}
 
 struct FastScratch {
   union {
@@ -98,20 +107,28 @@ struct MaskedScores {  // score[i] where gate[i] >= thr, else 0 (excluded)
 // s.sel[0..1]; sel[0] = -1 if the histogram holds fewer than rank values.
 // s.sel[2] = total count.
 __device__ __forceinline__ void fs_rank_bin(FastScratch& s, int rank) {
-  const int lo = 4088 - 8 * (int)threadIdx.x;  // bins lo .. lo + 7, scanned downwards
-  const uint4 a = *reinterpret_cast<const uint4*>(&s.hist[lo]);
-  const uint4 b = *reinterpret_cast<const uint4*>(&s.hist[lo + 4]);
-  const int cv[8] = {(int)b.w, (int)b.z, (int)b.y, (int)b.x, (int)a.w, (int)a.z, (int)a.y, (int)a.x};
+  constexpr int BPT = 4096 / SEL_BLOCK;  // bins per thread, scanned downwards
+  static_assert(BPT % 4 == 0, "bins per thread must fill 16-byte reads");
+  const int lo = 4096 - BPT * ((int)threadIdx.x + 1);
+  int cv[BPT];
+#pragma unroll
+  for (int q = 0; q < BPT / 4; ++q) {
+    const uint4 a = *reinterpret_cast<const uint4*>(&s.hist[lo + 4 * q]);
+    cv[BPT - 1 - 4 * q] = (int)a.x;
+    cv[BPT - 2 - 4 * q] = (int)a.y;
+    cv[BPT - 3 - 4 * q] = (int)a.z;
+    cv[BPT - 4 - 4 * q] = (int)a.w;
+  }
   int c = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) c += cv[j];
+  for (int j = 0; j < BPT; ++j) c += cv[j];
   int total;
   const int exc = block_excl_scan(c, s.scan, &total);
   if (exc < rank && rank <= exc + c) {
-    int acc = exc, bin = lo + 7;
+    int acc = exc, bin = lo + BPT - 1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (acc + cv[j] >= rank) { bin = lo + 7 - j; break; }
+    for (int j = 0; j < BPT; ++j) {
+      if (acc + cv[j] >= rank) { bin = lo + BPT - 1 - j; break; }
       acc += cv[j];
     }
     s.sel[0] = bin;
@@ -211,7 +228,7 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   {
     const int lane = threadIdx.x & 63;
     const int no = (n + 7) >> 3;
-    const uint32_t cut16 = cut << 16;
+    const u16x2 cm1 = {(uint16_t)(cut - 1), (uint16_t)(cut - 1)};  // cut >= 1
     uint32_t mx = 0;
     for (int base = threadIdx.x & ~63; base < no; base += FS_OCT * SEL_BLOCK) {
       uint4 w[FS_OCT];
@@ -223,13 +240,10 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
       uint32_t mask = 0;
 #pragma unroll
       for (int r = 0; r < FS_OCT; ++r) {
-        const uint32_t ww[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
-        uint32_t m8 = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          m8 |= (uint32_t)((ww[e] << 16) >= cut16) << (2 * e);  // item 2e (low half)
-          m8 |= (uint32_t)(ww[e] >= cut16) << (2 * e + 1);      // item 2e + 1
-        }
+        // bit 2e: low half of word e >= cut; bit 2e + 1: high half
+        const uint32_t m = ge_cut2(w[r].x, cm1) | (ge_cut2(w[r].y, cm1) << 2) |
+                           (ge_cut2(w[r].z, cm1) << 4) | (ge_cut2(w[r].w, cm1) << 6);
+        uint32_t m8 = (m & 0x55u) | ((m >> 15) & 0xaau);
         const int valid = n - 8 * (base + r * SEL_BLOCK + lane);
         if (valid < 8) m8 &= valid > 0 ? (1u << valid) - 1u : 0u;
         mask |= m8 << (8 * r);

@@ -141,6 +141,8 @@ __device__ __forceinline__ void load_b(const QOperand* q, uint32_t b[4][4]) {
 // k_top100 attends the head's 100 selected keys and merges everything.
 constexpr int SDPA_WAVE_KEYS = 16;
 constexpr int DENSE_BLOCK_KEYS = (SEL_BLOCK / WAVE) * SDPA_WAVE_KEYS;
+static_assert(DENSE_BLOCK_KEYS == DENSE_SLICE_KEYS && SEL_BLOCK / WAVE == ATTN_WAVES,
+              "attention slices follow the selection block size");
 
 // Four FP8 e4m3 values -> FP32 with the gfx950 converter (OCP e4m3fn; exact).
 __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
@@ -479,7 +481,8 @@ constexpr int PC_BLOCK = 512;   // pool_count: one wave per selected cluster
 constexpr int PC_WAVES = PC_BLOCK / WAVE;
 constexpr int PE_BLOCK = 512;   // pool_emit: one wave per 64-posting chunk
 constexpr int PE_WAVES = PE_BLOCK / WAVE;
-constexpr int S2_GRID = 512;    // score2 blocks per group (4 waves; about one 16-item tile per wave)
+constexpr int S2_GRID = 512;    // score2 blocks per group (4 waves each)
+constexpr int S2_TILES = 2;     // 16-item tiles per wave and pass (loads issued together)
 
 // Work items of a selected cluster: its 64-posting chunks (one item for an
 // empty list, so that every selected cluster is listed).
@@ -656,6 +659,7 @@ __global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
 // grid (grid-stride).
 __global__ __launch_bounds__(256) void k_score2(StepArgs a) {
   SKV_TS(14, 0);
+  SKV_TSB(2, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int n = a.status[g * ST_WORDS + ST_POOL];
@@ -671,31 +675,46 @@ __global__ __launch_bounds__(256) void k_score2(StepArgs a) {
   const int* __restrict__ pool = a.pool_tok + (size_t)g * a.cap;
   const uint8_t* __restrict__ rec = a.keyrec + (size_t)g * a.T * 256;
   uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
-  for (int tile = w0; tile < ntiles; tile += wstride) {
-    const int i = tile * 16 + row;
-    uint4 wv = make_uint4(0, 0, 0, 0);
-    if (i < n) wv = *reinterpret_cast<const uint4*>(rec + (size_t)pool[i] * 256 + kb * 16);
-    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-    v4i acc = {0, 0, 0, 0};
+  // S2_TILES tiles per wave and pass, all token and row loads issued first
+  for (int t0 = w0; t0 < ntiles; t0 += wstride * S2_TILES) {
+    int tk[S2_TILES];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      uint32_t av[4];
-      expand2(words[kc], av);
-      acc = mfma_i8(av, bq[kc], acc);
+    for (int u = 0; u < S2_TILES; ++u) {
+      const int i = (t0 + u * wstride) * 16 + row;
+      tk[u] = i < n ? pool[i] : -1;
     }
-    int64_t dot[4];
-    combine_limbs(acc, dot);
-    if ((lane & 3) == 0) {
+    uint4 wv[S2_TILES];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int ii = tile * 16 + 4 * kb + rr;
-        if (ii < n)
-          s2[(size_t)h * a.cap + ii] =
-              (uint16_t)ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
+    for (int u = 0; u < S2_TILES; ++u)
+      wv[u] = tk[u] >= 0 ? *reinterpret_cast<const uint4*>(rec + (size_t)tk[u] * 256 + kb * 16)
+                         : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < S2_TILES; ++u) {
+      const int tile = t0 + u * wstride;
+      if (tile >= ntiles) break;  // wave-uniform
+      const uint32_t words[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      v4i acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        uint32_t av[4];
+        expand2(words[kc], av);
+        acc = mfma_i8(av, bq[kc], acc);
+      }
+      int64_t dot[4];
+      combine_limbs(acc, dot);
+      if ((lane & 3) == 0) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int ii = tile * 16 + 4 * kb + rr;
+          if (ii < n)
+            s2[(size_t)h * a.cap + ii] =
+                (uint16_t)ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
+        }
       }
     }
   }
   SKV_TS(14, 15);
+  SKV_TSB(2, 3);
 }
 
 // ============================================================ token top-k
@@ -797,6 +816,7 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   constexpr bool U1 = STAGE == 4;
   const int ts = U1 ? 8 : 11;
   SKV_TS(ts, 0);
+  if (U1) SKV_TSB(3, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_in = a.status[g * ST_WORDS + (U1 ? ST_POOL : ST_U1)];
@@ -936,6 +956,7 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   }
   if (w_hi == words_in && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = min(base, cap_out);
   SKV_TS(ts, 15);
+  if (U1) SKV_TSB(3, 3);
 }
 
 // ============================================================ final top-100

@@ -63,8 +63,23 @@ struct Handle {
   hipEvent_t prof_ev[N_STEP_KERNELS + 1] = {};
   double prof_ms[N_STEP_KERNELS] = {};
   int prof_steps = 0;
+  // opt-in: the step's kernels captured once into a graph, replayed by
+  // skv_enqueue (consecutive graph launches leave ~8 us idle between them on
+  // ROCm 7.2, more than the launch gaps of the eager path)
+  bool use_graph = false;
+  hipStream_t capture_stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
   std::string error, meta;
 };
+
+// Drop the captured step (launch options changed).
+void drop_graph(Handle* h) {
+  if (h->graph_exec) (void)hipGraphExecDestroy(h->graph_exec);
+  if (h->graph) (void)hipGraphDestroy(h->graph);
+  h->graph_exec = nullptr;
+  h->graph = nullptr;
+}
 
 int fail(Handle* h, int code, const char* fmt, ...) {
   char buf[512];
@@ -213,6 +228,8 @@ void skv_destroy(void* handle) {
   if (h->q_copied) (void)hipEventDestroy(h->q_copied);
   for (hipEvent_t e : h->prof_ev)
     if (e) (void)hipEventDestroy(e);
+  drop_graph(h);
+  if (h->capture_stream) (void)hipStreamDestroy(h->capture_stream);
   if (h->q_host) (void)hipHostFree(h->q_host);
   if (h->static_mem) (void)hipFree(h->static_mem);
   if (h->work_mem) (void)hipFree(h->work_mem);
@@ -330,7 +347,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     chunk_base[(size_t)g * (nc + 1) + nc] = acc;
     a.chunks_max = std::max(a.chunks_max, acc);
   }
-  a.dense_slices = (a.sink + a.local + 127) / 128;
+  a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
 
   // ---- static arena
   Arena s;
@@ -565,11 +582,30 @@ int skv_enqueue(void* handle) {
     }
     launch_step(h->a, h->w, h->stream, h->prof_ev);
     h->prof_pending = true;
+  } else if (h->use_graph) {
+    if (!h->graph_exec) {  // capture the kernels once on a private stream
+      if (!h->capture_stream)
+        HIPCHK(h, hipStreamCreateWithFlags(&h->capture_stream, hipStreamNonBlocking));
+      HIPCHK(h, hipStreamBeginCapture(h->capture_stream, hipStreamCaptureModeThreadLocal));
+      launch_step(h->a, h->w, h->capture_stream, nullptr);
+      HIPCHK(h, hipStreamEndCapture(h->capture_stream, &h->graph));
+      HIPCHK(h, hipGraphInstantiate(&h->graph_exec, h->graph, nullptr, nullptr, 0));
+    }
+    HIPCHK(h, hipGraphLaunch(h->graph_exec, h->stream));
   } else {
     launch_step(h->a, h->w, h->stream, nullptr);
   }
   HIPCHK(h, hipGetLastError());
   h->ran = true;
+  return SKV_OK;
+}
+
+int skv_graph_mode(void* handle, int enable) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  h->use_graph = enable != 0;
+  drop_graph(h);
   return SKV_OK;
 }
 
@@ -621,6 +657,7 @@ int skv_select_mode(void* handle, int exact) {
   h->a.exact_select = e;
   h->w.top_u1.exact_select = e;
   h->w.top_u2.exact_select = e;
+  drop_graph(h);  // the kernels take the options by value
   return SKV_OK;
 }
 

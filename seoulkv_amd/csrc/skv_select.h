@@ -16,7 +16,7 @@
 
 namespace skv {
 
-constexpr int SEL_BLOCK = 512;
+constexpr int SEL_BLOCK = 1024;
 constexpr int SEL_WAVES = SEL_BLOCK / WAVE;
 constexpr int TIE_CAP = 2048;
 

@@ -60,7 +60,7 @@ struct StepArgs {
   int exact_select;         // 1: always run the full selections (no sampled cut)
   int pool_blocks;          // nc / 32: 32-centroid ranges of the pool kernels
   int words_u1, words_u2;   // bitmap words per (group, head)
-  int dense_slices;         // 128-key sink/local attention slices per query head
+  int dense_slices;         // DENSE_SLICE_KEYS-key sink/local attention slices per query head
   // static device data
   const uint16_t* q;        // [16][256] bf16 (bound query)
   const float* kscale;      // [G][256]
@@ -125,9 +125,12 @@ struct StepWork {
   size_t select_lds, top_u1_lds, top_u2_lds;  // dynamic LDS of the selection kernels
 };
 
-// LDS bytes of the attention scratch of a 512-thread block (8 waves x
-// (max, sum, o[256]) in FP32)
-constexpr size_t ATTN_SCRATCH_BYTES = (size_t)8 * (2 + D) * 4;
+// Attention blocks: 1024 threads, 16 keys per wave; LDS bytes of their
+// scratch (16 waves x (max, sum, o[256]) in FP32) and keys per sink/local
+// slice.
+constexpr int ATTN_WAVES = 16;
+constexpr size_t ATTN_SCRATCH_BYTES = (size_t)ATTN_WAVES * (2 + D) * 4;
+constexpr int DENSE_SLICE_KEYS = ATTN_WAVES * 16;
 
 constexpr int N_STEP_KERNELS = 10;
 extern const char* const kKernelNames[N_STEP_KERNELS];

@@ -149,3 +149,47 @@ def test_selection_paths_agree(runtimes, name, mode):
     rt.bind_query(qs[0])
     rt.enqueue()
     assert rt.synchronize()["full_select"] == [0, 0, 0, 0]  # default: sampled cuts hit
+
+
+@pytest.mark.parametrize("name", ["t8192_clustered", "t8192_p16_sink0"])
+def test_graph_replay_matches_eager(runtimes, name):
+    """The captured step replayed several times, with eager steps
+    and host synchronizations between the replays, gives the same top-100
+    IDs, status words and output bits as kernel-by-kernel launches, and
+    both equal the oracle's IDs."""
+    p = CASES[name]
+    rt = runtime_for(runtimes, name)
+    _, _, _, (q0, q1) = case(**p)
+    qs = (q0, q1, (q0.float() - q1.float()).bfloat16(), -q0)
+    print(f"[gpu] graph vs eager {name}", flush=True)
+
+    def step(q, graph):
+        rt.graph_mode(graph)
+        rt.bind_query(q)
+        rt.enqueue()
+        st = rt.synchronize()
+        return st, rt.debug_ids().clone(), rt.read_output().view(torch.int16).clone()
+
+    try:
+        for rep in range(3):
+            for qi, q in enumerate(qs):
+                st_e, ids_e, out_e = step(q, False)
+                st_g, ids_g, out_g = step(q, True)
+                assert st_g == st_e, (rep, qi)
+                assert torch.equal(ids_g, ids_e), (rep, qi)
+                assert torch.equal(out_g, out_e), (rep, qi)
+                if rep == 0:
+                    traces, _ = oracle_step(p, q)
+                    for g, tr in enumerate(traces):
+                        np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
+        # consecutive replays with no eager step between them
+        rt.graph_mode(True)
+        for qi in (3, 0, 2, 1):
+            rt.bind_query(qs[qi])
+            rt.enqueue()
+            rt.synchronize()
+            traces, _ = oracle_step(p, qs[qi])
+            for g, tr in enumerate(traces):
+                np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
+    finally:
+        rt.graph_mode(False)
