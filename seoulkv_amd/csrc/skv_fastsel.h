@@ -91,8 +91,11 @@ struct MaskedScores {  // score[i] where gate[i] >= thr, else 0 (excluded)
     return gv >= thr ? sv : 0u;
   }
   __device__ uint4 oct(int o) const {
-    const uint4 s4 = reinterpret_cast<const uint4*>(score)[o];
-    const uint4 g4 = reinterpret_cast<const uint4*>(gate)[o];
+    return pick4(reinterpret_cast<const uint4*>(score)[o], reinterpret_cast<const uint4*>(gate)[o],
+                 thr);
+  }
+  // the 8 packed scores of s4 whose packed gates in g4 reach thr
+  __device__ static uint4 pick4(uint4 s4, uint4 g4, uint32_t thr) {
     const uint32_t t16 = thr << 16;
     auto pick = [&](uint32_t sw, uint32_t gw) {
       return ((gw << 16) >= t16 ? (sw & 0xffffu) : 0u) | (gw >= t16 ? (sw & 0xffff0000u) : 0u);

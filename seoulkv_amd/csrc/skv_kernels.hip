@@ -25,6 +25,7 @@
 
 #include "skv_device.h"
 #include "skv_fastsel.h"
+#include "skv_octsel.h"
 #include "skv_select.h"
 #include "skv_step.h"
 
@@ -141,6 +142,7 @@ __device__ __forceinline__ void load_b(const QOperand* q, uint32_t b[4][4]) {
 // k_top100 attends the head's 100 selected keys and merges everything.
 constexpr int SDPA_WAVE_KEYS = 16;
 constexpr int DENSE_BLOCK_KEYS = (SEL_BLOCK / WAVE) * SDPA_WAVE_KEYS;
+static_assert(U2_MAX <= OCT_ITEMS && U1_MAX <= OCT_ITEMS, "unions fit the register selection");
 static_assert(DENSE_BLOCK_KEYS == DENSE_SLICE_KEYS && SEL_BLOCK / WAVE == ATTN_WAVES,
               "attention slices follow the selection block size");
 
@@ -368,6 +370,30 @@ __device__ __forceinline__ void load_lds_masked(uint16_t* so, const uint16_t* __
   for (int o = threadIdx.x; o < (n >> 3); o += blockDim.x) d4[o] = src.oct(o);
 }
 
+// Both selections of one (group, head) with its nc <= OCT_ITEMS centroids
+// held in registers, one octet of lower, upper and fine scores per thread.
+__device__ void select_in_registers(const StepArgs& a, int g, int h, FastScratch& fs) {
+  const int nc = a.nc, t = threadIdx.x;
+  const size_t row = ((size_t)g * H + h) * nc;
+  const uint4 wl = load_oct(a.lower + row, nc);
+  const uint4 wu = load_oct(a.upper + row, nc);
+  const uint4 wf = load_oct(a.fine_ord + row, nc);
+  auto cid = [](int i) { return (uint32_t)i; };
+  const OctResult r1 = oct_select<true, true>(wl, a.P[g], cid, fs);
+  const uint32_t thr = r1.sel.all ? 0u : r1.sel.v;
+  if (t == 0) a.thr[g * H + h] = thr;
+  SKV_TS(2, 6);
+  // fine scores of the eligible centroids (upper >= thr), others excluded
+  const uint4 wm = MaskedScores::pick4(wf, wu, thr);
+  const OctResult r2 = oct_select<false, true>(wm, a.P[g], cid, fs);
+  // items 8t .. 8t+7 are byte t & 3 of bitmap word t >> 2: merge 4 lanes
+  uint32_t m = r2.mine << (8 * (t & 3));
+  m |= __shfl_xor(m, 1);
+  m |= __shfl_xor(m, 2);
+  if ((t & 3) == 0 && m) atomicOr(&a.selbm[(size_t)g * (nc / 32) + (t >> 2)], m);
+  SKV_TS(2, 15);
+}
+
 __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   SKV_TS(2, 0);
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -376,6 +402,10 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
     return;
   }
   const int g = blockIdx.x / H, h = blockIdx.x % H, nc = a.nc;
+  if (a.exact_select == 0 && nc <= OCT_ITEMS) {
+    select_in_registers(a, g, h, *reinterpret_cast<FastScratch*>(dyn));
+    return;
+  }
   __shared__ SelectScratch s;
   __shared__ uint32_t s_thr;
   const size_t row = ((size_t)g * H + h) * nc;
@@ -732,6 +762,25 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   const int* tok = t.tokens + (size_t)g * t.stride;
   uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
   auto id = [&](int i) { return (uint32_t)tok[i]; };
+  if (t.exact_select == 0 && n <= OCT_ITEMS) {  // the scores fit in registers
+    const OctResult r =
+        oct_select<false, false>(load_oct(sc, n), t.k, id, *reinterpret_cast<FastScratch*>(dyn));
+    if (r.ok) {
+      // items 8u .. 8u+7 (u = thread) are byte u & 7 of bitmap word u >> 3
+      const int u = threadIdx.x, words = (n + 63) / 64;
+      const uint32_t m = r.mine << (8 * (u & 3));
+      uint32_t lo = (u & 4) ? 0u : m, hi = (u & 4) ? m : 0u;
+      lo |= __shfl_xor(lo, 1);
+      hi |= __shfl_xor(hi, 1);
+      lo |= __shfl_xor(lo, 2);
+      hi |= __shfl_xor(hi, 2);
+      lo |= __shfl_xor(lo, 4);
+      hi |= __shfl_xor(hi, 4);
+      if ((u & 7) == 0 && (u >> 3) < words) bm[u >> 3] = ((uint64_t)hi << 32) | lo;
+      SKV_TS(ts, 15);
+      return;
+    }
+  }
   if (t.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
     const FastResult r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
@@ -978,7 +1027,23 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   extern __shared__ __align__(16) unsigned char dyn[];
   if (threadIdx.x == 0) s_cnt = 0;
   bool done = false;
-  if (a.exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
+  if (a.exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: the scores fit in registers
+    const uint4 w = load_oct(sc, n);
+    const OctResult r = oct_select<false, false>(w, TOPK, id, *reinterpret_cast<FastScratch*>(dyn));
+    if (r.ok) {
+      SKV_TS(13, 6);
+      const u32x4 wv = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (!((r.mine >> e) & 1u)) continue;
+        const uint32_t t = id(8 * (int)threadIdx.x + e);
+        const int slot = atomicAdd(&s_cnt, 1);
+        if (slot < TOPK) s_key[slot] = ((uint64_t)oct_half(wv, e) << 20) | (0xfffffu - t);
+      }
+      done = true;
+    }
+  }
+  if (!done && a.exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
     const FastResult r = fast_select(RowScores{sc}, n, TOPK, id, fs, a.exact_select == 2, 13);
     if (r.ok) {

@@ -1,0 +1,159 @@
+// Exact block top-k by (ordered BF16 score desc, ID asc) of n <= 8 x SEL_BLOCK
+// items held in registers: thread t holds the octet of items 8t .. 8t+7 as
+// packed 16-bit ordered scores (0 = excluded or absent).
+//
+// Two histogram passes over the registers find the k-th best score v and the
+// count of items above it: 4096 bins of the top 12 bits (LDS atomics), then
+// 16 bins of the low 4 bits of the chosen bin.  No candidate list and no
+// second read of memory.  Items tied at v are members in ID order:
+//   POS_IDS (the ID is the item position): a block scan of the per-thread
+//   tie counts ranks every tie directly;
+//   otherwise the tied IDs are gathered into LDS and ranked by comparison
+//   (up to FS_TIE_RANK ties; beyond that ok = false and the caller runs the
+//   full selection).
+#pragma once
+
+#include "skv_fastsel.h"
+
+namespace skv {
+
+constexpr int OCT_ITEMS = 8 * SEL_BLOCK;  // largest n held one octet per thread
+
+// Half e (0..7, a compile-time constant after unrolling) of an octet.
+__device__ __forceinline__ uint32_t oct_half(const u32x4& wv, int e) {
+  return (e & 1) ? wv[e >> 1] >> 16 : wv[e >> 1] & 0xffffu;
+}
+
+// This thread's octet of a 16-byte aligned row of n ordered scores, items
+// beyond n cleared (the row may hold stale values there).
+__device__ __forceinline__ uint4 load_oct(const uint16_t* __restrict__ row, int n) {
+  const int t = threadIdx.x, valid = n - 8 * t;
+  if (valid <= 0) return make_uint4(0, 0, 0, 0);
+  const uint4 w = reinterpret_cast<const uint4*>(row)[t];
+  if (valid >= 8) return w;
+  auto cut = [&](uint32_t x, int q) {  // halves of word q kept: valid - 2q
+    const int keep = valid - 2 * q;
+    return keep >= 2 ? x : keep == 1 ? (x & 0xffffu) : 0u;
+  };
+  return make_uint4(cut(w.x, 0), cut(w.y, 1), cut(w.z, 2), cut(w.w, 3));
+}
+
+struct OctResult {
+  Selection sel;  // v (k-th best score), above (count scoring > v), all
+  uint32_t mine;  // member bits of this thread's 8 items (bit e = item 8t + e)
+  bool ok;        // false: too many ties at v to rank here (use the full path)
+};
+
+template <bool VALUE_ONLY, bool POS_IDS, typename IdFn>
+__device__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s) {
+  OctResult res;
+  res.ok = true;
+  res.mine = 0;
+  res.sel.v = 0;
+  res.sel.idcut = 0xffffffffu;
+  res.sel.above = 0;
+  res.sel.all = false;
+  const u32x4 wv = {w.x, w.y, w.z, w.w};
+  for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
+  if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    s.ntie = 0;
+    s.sel[0] = -1;
+    s.sel[1] = 0;
+  }
+  __syncthreads();
+  uint32_t valid = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t o = oct_half(wv, e);
+    if (o) {
+      atomicAdd(&s.hist[o >> 4], 1u);
+      valid |= 1u << e;
+    }
+  }
+  __syncthreads();
+  fs_rank_bin(s, k);
+  __syncthreads();
+  const int b1 = s.sel[0];
+  const int acc1 = s.sel[1];
+  const int total = s.sel[2];
+  if (b1 < 0) {  // fewer than k valid items: all of them are members
+    __syncthreads();  // the scratch may be reused on return
+    res.sel.all = true;
+    res.sel.above = total;
+    res.mine = valid;
+    return res;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t o = oct_half(wv, e);
+    if (o && (int)(o >> 4) == b1) atomicAdd(&s.hist4[o & 15], 1u);
+  }
+  __syncthreads();
+  fs_rank_digit(s, k, acc1);
+  __syncthreads();
+  const uint32_t v = ((uint32_t)b1 << 4) | (uint32_t)s.sel[0];
+  const int above = s.sel[1];
+  const int ties = s.sel[3];
+  __syncthreads();  // the scratch may be reused on return
+  res.sel.v = v;
+  res.sel.above = above;
+  if (VALUE_ONLY) return res;
+  uint32_t gt = 0, eq = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t o = oct_half(wv, e);
+    gt |= (uint32_t)(o > v) << e;
+    eq |= (uint32_t)(o == v) << e;
+  }
+  const int need = k - above;  // 1 <= need <= ties
+  if (need >= ties) {
+    res.mine = gt | eq;
+    return res;
+  }
+  if (POS_IDS) {  // ties in position order: thread order, then bit order
+    const int c = __popc(eq);
+    int nt;
+    const int exc = block_excl_scan(c, s.scan, &nt);  // ends with a barrier
+    const int take = min(max(need - exc, 0), c);  // this thread's lowest `take` ties
+    uint32_t m = 0, rest = eq;
+    for (int j = 0; j < take; ++j) {
+      m |= rest & (0u - rest);
+      rest &= rest - 1;
+    }
+    res.mine = gt | m;
+    return res;
+  }
+  if (ties > FS_TIE_RANK) {
+    res.ok = false;
+    return res;
+  }
+  // gather the tied IDs, rank them, keep those up to the need-th lowest
+  uint32_t myid[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) myid[e] = 0xffffffffu;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if ((eq >> e) & 1u) {
+      myid[e] = id(8 * (int)threadIdx.x + e);
+      s.tie[atomicAdd(&s.ntie, 1)] = myid[e];
+    }
+  __syncthreads();
+  if ((int)threadIdx.x < ties) {  // rank = number of smaller tied IDs
+    const uint32_t x = s.tie[threadIdx.x];
+    int r = 0;
+    for (int j = 0; j < ties; ++j) r += s.tie[j] < x;
+    if (r == need - 1) s.sel[2] = (int)x;
+  }
+  __syncthreads();
+  const uint32_t idcut = (uint32_t)s.sel[2];
+  res.sel.idcut = idcut;
+  uint32_t m = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m |= (uint32_t)(((eq >> e) & 1u) && myid[e] <= idcut) << e;
+  res.mine = gt | m;
+  __syncthreads();
+  return res;
+}
+
+}  // namespace skv
