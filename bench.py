@@ -61,9 +61,10 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         # CSR bounds + mates of the selected clusters' postings; upper bounds
         # in and survivor masks out
         "pool_count": sel * (8 + 4) + scanned * 4 + G * nc * (H * 2 + 1),
-        # CSR, mates, tokens of the selected clusters in; pool tokens out
-        "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4) + pool * 4,
-        # pool tokens and their 64 B prefix rows in; 2-bit scores out
+        # CSR, mates, tokens of the selected clusters in; pool tokens and
+        # posting indices out
+        "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4) + pool * 8,
+        # posting indices and their 64 B prefix rows in; 2-bit scores out
         "score2": pool * (4 + 64 + H * 2),
         # pool scores in; member bitmaps out
         "top1600": pool * H * 2 + G * H * pool // 8,

@@ -26,13 +26,20 @@ extern __device__ unsigned long long g_skv_trace[32][16];
       g_skv_trace[(k)][(i)] = __builtin_amdgcn_s_memrealtime();                \
   } while (0)
 // SKV_TSB(k, i): every block's thread 0 records point i of kernel slot k
-// (first 4096 blocks, x-major over (blockIdx.x, blockIdx.y)).
-extern __device__ unsigned long long g_skv_trace_blk[4][4096][4];
+// (first 4096 blocks, x-major over (blockIdx.x, blockIdx.y)); SKV_TSE(k):
+// point 3 = the latest time any wave of the block reached it.
+extern __device__ unsigned long long g_skv_trace_blk[12][4096][4];
 #define SKV_TSB(k, i)                                                          \
   do {                                                                         \
     const unsigned _b = blockIdx.x + blockIdx.y * gridDim.x;                   \
     if (threadIdx.x == 0 && _b < 4096)                                         \
       g_skv_trace_blk[(k)][_b][(i)] = __builtin_amdgcn_s_memrealtime();        \
+  } while (0)
+#define SKV_TSE(k)                                                             \
+  do {                                                                         \
+    const unsigned _b = blockIdx.x + blockIdx.y * gridDim.x;                   \
+    if ((threadIdx.x & 63) == 0 && _b < 4096)                                  \
+      atomicMax(&g_skv_trace_blk[(k)][_b][3], __builtin_amdgcn_s_memrealtime()); \
   } while (0)
 #else
 #define SKV_TS(k, i) \
@@ -40,6 +47,9 @@ extern __device__ unsigned long long g_skv_trace_blk[4][4096][4];
   } while (0)
 #define SKV_TSB(k, i) \
   do {                \
+  } while (0)
+#define SKV_TSE(k) \
+  do {             \
   } while (0)
 #endif
 

@@ -33,7 +33,7 @@ namespace skv {
 
 #ifdef SKV_TRACE
 __device__ unsigned long long g_skv_trace[32][16];
-__device__ unsigned long long g_skv_trace_blk[4][4096][4];
+__device__ unsigned long long g_skv_trace_blk[12][4096][4];
 #endif
 
 // ============================================================ query prep
@@ -161,46 +161,63 @@ __device__ __forceinline__ void load_q4(const StepArgs& a, int j, float q[4]) {
   q[2] = bf16_f32(qw.y & 0xffff); q[3] = bf16_f32(qw.y >> 16);
 }
 
-// One wave over up to 16 keys: lane b < 16 holds the token of key b in tk
-// (-1: none); lane l owns dims 4l..4l+3.  All records are loaded before any
-// is used.  Returns the wave's max logit m, softmax sum l and output o.
-__device__ __forceinline__ void wave_attend(const uint8_t* __restrict__ kv, const float q[4],
-                                            int tk, float& m, float& l, float o[4]) {
+// One wave over up to KPW keys: lane b < KPW holds the token of key b in tk
+// (-1: none); lane l owns dims 4l..4l+3.  attend_load issues every record
+// load; attend_math (after any independent work) returns the wave's max
+// logit m, softmax sum l and unnormalised output o.
+template <int KPW>
+struct AttnLoads {
+  int t[KPW];
+  uint32_t kw[KPW], vw[KPW];
+};
+
+template <int KPW>
+__device__ __forceinline__ AttnLoads<KPW> attend_load(const uint8_t* __restrict__ kv, int tk) {
   const int lane = threadIdx.x & 63;
-  int t[SDPA_WAVE_KEYS];
-  uint32_t kw[SDPA_WAVE_KEYS], vw[SDPA_WAVE_KEYS];
+  AttnLoads<KPW> L;
 #pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
-    t[b] = __builtin_amdgcn_readlane(tk, b);
-    const uint8_t* rec = kv + (size_t)max(t[b], 0) * 512;
-    kw[b] = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
-    vw[b] = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
+  for (int b = 0; b < KPW; ++b) {
+    L.t[b] = __builtin_amdgcn_readlane(tk, b);
+    const uint8_t* rec = kv + (size_t)max(L.t[b], 0) * 512;
+    L.kw[b] = *reinterpret_cast<const uint32_t*>(rec + 256 + 4 * lane);
+    L.vw[b] = *reinterpret_cast<const uint32_t*>(rec + 4 * lane);
   }
-  float logit[SDPA_WAVE_KEYS];
+  return L;
+}
+
+template <int KPW>
+__device__ __forceinline__ void attend_math(const AttnLoads<KPW>& L, const float q[4], float& m,
+                                            float& l, float o[4]) {
+  float logit[KPW];
 #pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
+  for (int b = 0; b < KPW; ++b) {
     float kf[4];
-    fp8x4_to_f32(kw[b], kf);
+    fp8x4_to_f32(L.kw[b], kf);
     logit[b] = q[0] * kf[0] + q[1] * kf[1] + q[2] * kf[2] + q[3] * kf[3];
   }
 #pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) logit[b] = wave_sum_f(logit[b]);
+  for (int b = 0; b < KPW; ++b) logit[b] = wave_sum_f(logit[b]);
   m = -INFINITY;
 #pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b)
-    if (t[b] >= 0) m = fmaxf(m, logit[b] * 0.0625f);
+  for (int b = 0; b < KPW; ++b)
+    if (L.t[b] >= 0) m = fmaxf(m, logit[b] * 0.0625f);
   l = 0.f;
   o[0] = o[1] = o[2] = o[3] = 0.f;
 #pragma unroll
-  for (int b = 0; b < SDPA_WAVE_KEYS; ++b) {
-    if (t[b] < 0) continue;
+  for (int b = 0; b < KPW; ++b) {
+    if (L.t[b] < 0) continue;
     const float p = __expf(logit[b] * 0.0625f - m);
     float vf[4];
-    fp8x4_to_f32(vw[b], vf);
+    fp8x4_to_f32(L.vw[b], vf);
     l += p;
 #pragma unroll
     for (int d = 0; d < 4; ++d) o[d] += p * vf[d];
   }
+}
+
+__device__ __forceinline__ void wave_attend(const uint8_t* __restrict__ kv, const float q[4],
+                                            int tk, float& m, float& l, float o[4]) {
+  attend_math<SDPA_WAVE_KEYS>(attend_load<SDPA_WAVE_KEYS>(kv, tk), q, m, l, o);
 }
 
 struct AttnScratch {
@@ -276,6 +293,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 // group's per-step state; two extra blocks per group publish the q15 / qs
 // operands for the later kernels.
 __global__ __launch_bounds__(256) void k_front(StepArgs a) {
+  SKV_TSB(4, 0);
   SKV_TS(0, 0);
   const int g = blockIdx.y, nc = a.nc;
   __shared__ __align__(16) QPrepScratch sp;
@@ -283,6 +301,7 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
   if ((int)blockIdx.x >= tiles_blocks) {
     const int v = QV_Q15 + (blockIdx.x - tiles_blocks);
     prep_operand(a, g, v, sp, &a.qop[g * QV_COUNT + v]);
+    SKV_TSE(4);
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -294,6 +313,16 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
     const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
     wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
     wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
+  }
+  // the per-centroid factors of this lane's output centroids c0 .. c0+3
+  // (one 32-centroid block), loaded with the planes
+  const int c0 = tile * 16 + 4 * kb;
+  float4 rs = make_float4(0.f, 0.f, 0.f, 0.f);
+  float sc4 = 0.f, gf = 0.f;
+  if (has && (lane & 3) == 0) {
+    rs = *reinterpret_cast<const float4*>(a.resid + (size_t)g * nc + c0);
+    sc4 = a.scale4[(size_t)g * (nc / 32) + (c0 >> 5)];
+    gf = a.gfs[(size_t)g * (nc / 32) + (c0 >> 5)];
   }
   if (blockIdx.x == 0) {  // per-step state of the group
     uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
@@ -331,17 +360,18 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
       const int64_t S = sq.sum[h];
       const int fx = sq.fx[h];
       const float norm = sq.norm[h];
+      const float res[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int c = tile * 16 + 4 * kb + r;
+        const int c = c0 + r;
         const float val = scaled_f32(2 * dc[r] - 3 * S, fx);
-        const float value = __fmul_rn(val, a.scale4[(size_t)g * (nc / 32) + c / 32]);
-        const float margin = __fmul_rn(norm, a.resid[(size_t)g * nc + c]);
+        const float value = __fmul_rn(val, sc4);
+        const float margin = __fmul_rn(norm, res[r]);
         const size_t o = ((size_t)g * H + h) * nc + c;
         a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
         a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
         const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
-        const uint32_t fb = bf16_rne(__fmul_rn(fv, a.gfs[(size_t)g * (nc / 32) + c / 32]));
+        const uint32_t fb = bf16_rne(__fmul_rn(fv, gf));
         a.fine_ord[o] = (uint16_t)ordered16(fb);
         if (a.debug) a.fine_bits[o] = (uint16_t)fb;
       }
@@ -353,6 +383,7 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
     uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + QV_RAW]);
     for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += 256) dst[i] = src[i];
   }
+  SKV_TSE(4);
 }
 
 __device__ __forceinline__ uint32_t same16(uint32_t o) { return o; }
@@ -395,15 +426,18 @@ __device__ void select_in_registers(const StepArgs& a, int g, int h, FastScratch
 }
 
 __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
+  SKV_TSB(5, 0);
   SKV_TS(2, 0);
   extern __shared__ __align__(16) unsigned char dyn[];
   if (blockIdx.x >= G * H) {  // sink/local attention slices (depend only on Q)
     dense_attend(a, blockIdx.x - G * H, *reinterpret_cast<AttnScratch*>(dyn));
+    SKV_TSE(5);
     return;
   }
   const int g = blockIdx.x / H, h = blockIdx.x % H, nc = a.nc;
   if (a.exact_select == 0 && nc <= OCT_ITEMS) {
     select_in_registers(a, g, h, *reinterpret_cast<FastScratch*>(dyn));
+    SKV_TSE(5);
     return;
   }
   __shared__ SelectScratch s;
@@ -478,6 +512,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
     });
   }
   SKV_TS(2, 15);
+  SKV_TSE(5);
 }
 
 // ============================================================ pool
@@ -511,7 +546,7 @@ constexpr int PC_BLOCK = 512;   // pool_count: one wave per selected cluster
 constexpr int PC_WAVES = PC_BLOCK / WAVE;
 constexpr int PE_BLOCK = 512;   // pool_emit: one wave per 64-posting chunk
 constexpr int PE_WAVES = PE_BLOCK / WAVE;
-constexpr int S2_GRID = 512;    // score2 blocks per group (4 waves each)
+constexpr int S2_GRID = 320;    // score2 blocks per group (4 waves each)
 constexpr int S2_TILES = 2;     // 16-item tiles per wave and pass (loads issued together)
 
 // Work items of a selected cluster: its 64-posting chunks (one item for an
@@ -524,8 +559,8 @@ __device__ __forceinline__ int cluster_items(int postings) {
 // cluster), per 64-posting chunk and in total, and the range's counts
 // {selected, owned, scanned, work items}.
 __global__ __launch_bounds__(PC_BLOCK) void k_pool_count(StepArgs a) {
-  SKV_TS(5, 0);
   SKV_TSB(0, 0);
+  SKV_TS(5, 0);
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
@@ -582,7 +617,7 @@ __global__ __launch_bounds__(PC_BLOCK) void k_pool_count(StepArgs a) {
     }
     a.range_cnt[(size_t)g * a.pool_blocks + b] = make_int4(nsel, o, sc, it);
   }
-  SKV_TSB(0, 3);
+  SKV_TSE(0);
 }
 
 // Emit the selected list and the pool tokens in encounter order.  Block b
@@ -592,8 +627,8 @@ __global__ __launch_bounds__(PC_BLOCK) void k_pool_count(StepArgs a) {
 // the range's earlier selected clusters) plus the owned counts of the
 // cluster's earlier chunks.
 __global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
-  SKV_TS(6, 0);
   SKV_TSB(1, 0);
+  SKV_TS(6, 0);
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
@@ -663,6 +698,7 @@ __global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
   const int* __restrict__ own_chunk = a.own_chunk + (size_t)g * a.chunks_max;
   int* pool = a.pool_tok + (size_t)g * a.cap;
+  int* pool_post = a.pool_post + (size_t)g * a.cap;
   for (int it = wave; it < nitems; it += PE_WAVES) {
     // the item's cluster: the last selected rank whose first item is <= it
     const uint64_t bal = __ballot(lane < nsel && s_chb[lane] <= it);
@@ -679,44 +715,52 @@ __global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
     const bool o = j < j1 && owned(s_bm, (uint32_t)mj, c);
     const uint64_t om = __ballot(o);
     const int p = pos + __popcll(om & ((1ull << lane) - 1));
-    if (o && p < a.cap) pool[p] = tj;
+    if (o && p < a.cap) {
+      pool[p] = tj;
+      pool_post[p] = j;
+    }
   }
-  if (wave == 0) SKV_TSB(1, 3);
+  SKV_TSE(1);
 }
 
-// 2-bit pool scores s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) from each token's
-// prefix plane, 16 pool items per matrix-core tile, tiles spread over the
-// grid (grid-stride).
+// 2-bit pool scores s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) from each pool
+// key's prefix plane (its row in the posting-ordered copy), 16 pool items per
+// matrix-core tile, tiles spread over the grid (grid-stride).
 __global__ __launch_bounds__(256) void k_score2(StepArgs a) {
-  SKV_TS(14, 0);
   SKV_TSB(2, 0);
+  SKV_TS(14, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int n = a.status[g * ST_WORDS + ST_POOL];
   const int ntiles = (n + 15) / 16;
   const int w0 = blockIdx.x * 4 + (threadIdx.x >> 6), wstride = gridDim.x * 4;
-  if (w0 >= ntiles) return;
+  if (w0 >= ntiles) {
+    SKV_TSE(2);
+    return;
+  }
   const QOperand* q = &a.qop[g * QV_COUNT + QV_Q15];
   uint32_t bq[4][4];
   load_b(q, bq);
   const int row = lane & 15, kb = lane >> 4, h = (lane & 15) >> 2;
   const int64_t S = q->sum[h];
   const int fx = q->fx[h] + 4;
-  const int* __restrict__ pool = a.pool_tok + (size_t)g * a.cap;
-  const uint8_t* __restrict__ rec = a.keyrec + (size_t)g * a.T * 256;
+  // the prefix rows in posting order: pool keys of one cluster list are
+  // consecutive there, so the 64-byte rows are read as whole lines
+  const int* __restrict__ ppost = a.pool_post + (size_t)g * a.cap;
+  const uint8_t* __restrict__ rows = a.post_p2 + (size_t)g * a.np_max * 64;
   uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
-  // S2_TILES tiles per wave and pass, all token and row loads issued first
+  // S2_TILES tiles per wave and pass, all index and row loads issued first
   for (int t0 = w0; t0 < ntiles; t0 += wstride * S2_TILES) {
-    int tk[S2_TILES];
+    int jp[S2_TILES];
 #pragma unroll
     for (int u = 0; u < S2_TILES; ++u) {
       const int i = (t0 + u * wstride) * 16 + row;
-      tk[u] = i < n ? pool[i] : -1;
+      jp[u] = i < n ? ppost[i] : -1;
     }
     uint4 wv[S2_TILES];
 #pragma unroll
     for (int u = 0; u < S2_TILES; ++u)
-      wv[u] = tk[u] >= 0 ? *reinterpret_cast<const uint4*>(rec + (size_t)tk[u] * 256 + kb * 16)
+      wv[u] = jp[u] >= 0 ? *reinterpret_cast<const uint4*>(rows + (size_t)jp[u] * 64 + kb * 16)
                          : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int u = 0; u < S2_TILES; ++u) {
@@ -744,14 +788,31 @@ __global__ __launch_bounds__(256) void k_score2(StepArgs a) {
     }
   }
   SKV_TS(14, 15);
-  SKV_TSB(2, 3);
+  SKV_TSE(2);
 }
 
 // ============================================================ token top-k
+// Member bits of this thread's octet (bit e = item 8t + e) -> 64-bit bitmap
+// words: octet t is byte t & 7 of word t >> 3, merged over 8 lanes.
+__device__ __forceinline__ void write_member_words(uint32_t mine, int n, uint64_t* bm) {
+  const int u = threadIdx.x, words = (n + 63) / 64;
+  const uint32_t m = mine << (8 * (u & 3));
+  uint32_t lo = (u & 4) ? 0u : m, hi = (u & 4) ? m : 0u;
+  lo |= __shfl_xor(lo, 1);
+  hi |= __shfl_xor(hi, 1);
+  lo |= __shfl_xor(lo, 2);
+  hi |= __shfl_xor(hi, 2);
+  lo |= __shfl_xor(lo, 4);
+  hi |= __shfl_xor(hi, 4);
+  if ((u & 7) == 0 && (u >> 3) < words) bm[u >> 3] = ((uint64_t)hi << 32) | lo;
+}
+
+
 // Per (group, head): members = top-k by (ordered score, lowest token) of the
 // n items; writes the membership bitmap.  LDS-resident when n <= lds_items,
 // otherwise 8-bit radix passes over the full 40-bit keys in memory.
 __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
+  SKV_TSB((t.count_slot == ST_POOL ? 6 : 7), 0);
   const int ts = t.count_slot == ST_POOL ? 7 : 10;
   SKV_TS(ts, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H;
@@ -761,23 +822,14 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   const uint16_t* sc = t.scores + ((size_t)g * H + h) * t.stride;
   const int* tok = t.tokens + (size_t)g * t.stride;
   uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
-  auto id = [&](int i) { return (uint32_t)tok[i]; };
+  auto id = [tok](int i) { return (uint32_t)tok[i]; };
   if (t.exact_select == 0 && n <= OCT_ITEMS) {  // the scores fit in registers
     const OctResult r =
         oct_select<false, false>(load_oct(sc, n), t.k, id, *reinterpret_cast<FastScratch*>(dyn));
     if (r.ok) {
-      // items 8u .. 8u+7 (u = thread) are byte u & 7 of bitmap word u >> 3
-      const int u = threadIdx.x, words = (n + 63) / 64;
-      const uint32_t m = r.mine << (8 * (u & 3));
-      uint32_t lo = (u & 4) ? 0u : m, hi = (u & 4) ? m : 0u;
-      lo |= __shfl_xor(lo, 1);
-      hi |= __shfl_xor(hi, 1);
-      lo |= __shfl_xor(lo, 2);
-      hi |= __shfl_xor(hi, 2);
-      lo |= __shfl_xor(lo, 4);
-      hi |= __shfl_xor(hi, 4);
-      if ((u & 7) == 0 && (u >> 3) < words) bm[u >> 3] = ((uint64_t)hi << 32) | lo;
+      write_member_words(r.mine, n, bm);
       SKV_TS(ts, 15);
+      SKV_TSE((t.count_slot == ST_POOL ? 6 : 7));
       return;
     }
   }
@@ -804,6 +856,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
         for (int w = threadIdx.x; w < words; w += SEL_BLOCK) bm[w] = mb[w];
       }
       SKV_TS(ts, 15);
+      SKV_TSE((t.count_slot == ST_POOL ? 6 : 7));
       return;
     }
     __syncthreads();
@@ -815,9 +868,10 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
     __syncthreads();
     const Selection sel = block_select(so, n, t.k, id, s);
     write_members(so, n, sel, id, bm);
+    SKV_TSE((t.count_slot == ST_POOL ? 6 : 7));
     return;
   }
-  auto val = [&](int i, uint64_t* v) {
+  auto val = [sc, tok](int i, uint64_t* v) {
     *v = ((uint64_t)sc[i] << 20) | (0xfffffu - (uint32_t)tok[i]);
     return true;
   };
@@ -830,6 +884,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
     const uint64_t ball = __ballot(m);
     if (lane == 0) bm[base >> 6] = ball;
   }
+  SKV_TSE((t.count_slot == ST_POOL ? 6 : 7));
 }
 
 // ============================================================ key scores
@@ -863,9 +918,9 @@ constexpr int US_GRID_U2 = 16;  // blocks per group over U1 (<= 100 words)
 template <int STAGE>
 __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   constexpr bool U1 = STAGE == 4;
+  SKV_TSB((U1 ? 3 : 8), 0);
   const int ts = U1 ? 8 : 11;
   SKV_TS(ts, 0);
-  if (U1) SKV_TSB(3, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_in = a.status[g * ST_WORDS + (U1 ? ST_POOL : ST_U1)];
@@ -879,11 +934,15 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   const int slot_out = U1 ? ST_U1 : ST_U2;
   if (n_in == 0) {
     if (blockIdx.x == 0 && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = 0;
+    SKV_TSE((U1 ? 3 : 8));
     return;
   }
   const int span = max(US_CHUNK, (words_in + (int)gridDim.x - 1) / (int)gridDim.x);
   const int w_lo = blockIdx.x * span;
-  if (w_lo >= words_in) return;
+  if (w_lo >= words_in) {
+    SKV_TSE((U1 ? 3 : 8));
+    return;
+  }
   const int w_hi = min(words_in, w_lo + span);
 
   __shared__ int s_red[US_BLOCK / WAVE + 1];
@@ -1005,41 +1064,70 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   }
   if (w_hi == words_in && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = min(base, cap_out);
   SKV_TS(ts, 15);
-  if (U1) SKV_TSB(3, 3);
+  SKV_TSE((U1 ? 3 : 8));
 }
 
 // ============================================================ final top-100
 // Per (group, head): the 100 best of U2, written best first (the rank of a
 // member is the number of members with a larger (score, -token) key), then
 // the head's attention over them merged with its sink/local slices.
+constexpr int TOP_KPW = (TOPK + ATTN_WAVES - 1) / ATTN_WAVES;  // selected keys per wave
+constexpr int DENSE_PREF = 2;  // sink/local partials prefetched per merge thread
+
 __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
+  SKV_TSB(9, 0);
   SKV_TS(13, 0);
-  const int g = blockIdx.x / H, h = blockIdx.x % H;
+  const int g = blockIdx.x / H, h = blockIdx.x % H, j = g * H + h;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ SelectScratch s;
   __shared__ uint64_t s_key[TOPK];
-  __shared__ int s_tok[TOPK];
   __shared__ int s_cnt;
   __shared__ AttnScratch att;
   const int n = a.status[g * ST_WORDS + ST_U2];
-  const uint16_t* sc = a.s8 + ((size_t)g * H + h) * U2_MAX;
+  const uint16_t* sc = a.s8 + (size_t)j * U2_MAX;
   const int* tok = a.u2_tok + (size_t)g * U2_MAX;
-  auto id = [&](int i) { return (uint32_t)tok[i]; };
+  auto id = [tok](int i) { return (uint32_t)tok[i]; };
   extern __shared__ __align__(16) unsigned char dyn[];
+  // loads independent of the selection, issued first: the query and the
+  // sink/local partials (consumed only by the final merge)
+  float q[4];
+  load_q4(a, j, q);
+  const int d = threadIdx.x & (D - 1);
+  const float* parts = a.dense_part + (size_t)j * a.dense_slices * (D + 2);
+  float pm[DENSE_PREF], pl[DENSE_PREF], po[DENSE_PREF];
+#pragma unroll
+  for (int r = 0; r < DENSE_PREF; ++r) {
+    const bool has = r < a.dense_slices && (int)threadIdx.x < D;
+    pm[r] = has ? parts[r * (D + 2) + D] : -INFINITY;
+    pl[r] = has ? parts[r * (D + 2) + D + 1] : 0.f;
+    po[r] = has ? parts[r * (D + 2) + d] : 0.f;
+  }
   if (threadIdx.x == 0) s_cnt = 0;
   bool done = false;
-  if (a.exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: the scores fit in registers
+  if (a.exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: scores and IDs in registers
     const uint4 w = load_oct(sc, n);
+    uint4 t0 = make_uint4(0, 0, 0, 0), t1 = t0;
+    if (8 * (int)threadIdx.x < n) {  // rows hold U2_MAX (a multiple of 8) entries
+      t0 = reinterpret_cast<const uint4*>(tok)[2 * threadIdx.x];
+      t1 = reinterpret_cast<const uint4*>(tok)[2 * threadIdx.x + 1];
+    }
     const OctResult r = oct_select<false, false>(w, TOPK, id, *reinterpret_cast<FastScratch*>(dyn));
     if (r.ok) {
       SKV_TS(13, 6);
+      // members in list order (deterministic, so the attention sums are too)
+      int nm;
+      const int base = block_excl_scan(__popc(r.mine), s.scan, &nm);
       const u32x4 wv = {w.x, w.y, w.z, w.w};
+      const u32x4 ta = {t0.x, t0.y, t0.z, t0.w}, tb = {t1.x, t1.y, t1.z, t1.w};
+      int slot = base;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if (!((r.mine >> e) & 1u)) continue;
-        const uint32_t t = id(8 * (int)threadIdx.x + e);
-        const int slot = atomicAdd(&s_cnt, 1);
+        const uint32_t t = e < 4 ? ta[e & 3] : tb[e & 3];
         if (slot < TOPK) s_key[slot] = ((uint64_t)oct_half(wv, e) << 20) | (0xfffffu - t);
+        ++slot;
       }
+      if (threadIdx.x == 0) s_cnt = nm;
       done = true;
     }
   }
@@ -1079,55 +1167,62 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   __syncthreads();
   SKV_TS(13, 7);
   const int m = min(s_cnt, TOPK);
-  int* out = a.top + (g * H + h) * TOPK;
+  // attention over the members: wave w takes list entries w + 16 b; the
+  // record loads are issued before the output list is ranked
+  int tk = -1;
+  if (lane < TOP_KPW) {
+    const int i = wave + ATTN_WAVES * lane;
+    if (i < m) tk = (int)(0xfffffu - (uint32_t)(s_key[i] & 0xfffffu));
+  }
+  const AttnLoads<TOP_KPW> L = attend_load<TOP_KPW>(a.kv8 + (size_t)g * a.T * 512, tk);
+  // the output list, best first (member keys are distinct)
+  int* out = a.top + j * TOPK;
   if ((int)threadIdx.x < m) {
     const uint64_t key = s_key[threadIdx.x];
     int rank = 0;
     for (int jj = 0; jj < m; ++jj) rank += s_key[jj] > key;
-    const int t = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
-    out[rank] = t;
-    s_tok[rank] = t;
-  } else if (threadIdx.x < TOPK) {
+    out[rank] = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
+  } else if ((int)threadIdx.x < TOPK) {
     out[threadIdx.x] = -1;
-    s_tok[threadIdx.x] = -1;
   }
-  __syncthreads();
-  // attention over the selected keys, merged with the sink/local slices
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int j = g * H + h;
-  float q[4];
-  load_q4(a, j, q);
-  const int i = wave * SDPA_WAVE_KEYS + lane;
-  const int tk = (lane < SDPA_WAVE_KEYS && i < TOPK) ? s_tok[i] : -1;
-  float mw, lw, ow[4];
   SKV_TS(13, 8);
-  wave_attend(a.kv8 + (size_t)g * a.T * 512, q, tk, mw, lw, ow);
+  float mw, lw, ow[4];
+  attend_math<TOP_KPW>(L, q, mw, lw, ow);
   stash_wave(att, mw, lw, ow);
   __syncthreads();
   SKV_TS(13, 9);
+  // merge with the sink/local slices
   if (threadIdx.x < D) {
-    const int d = threadIdx.x;
-    float M, L, O;
-    merge_waves(att, d, M, L, O);
-    const float* parts = a.dense_part + (size_t)j * a.dense_slices * (D + 2);
+    float M, Ls, O;
+    merge_waves(att, d, M, Ls, O);
     float Mt = M;
-    for (int r = 0; r < a.dense_slices; ++r) Mt = fmaxf(Mt, parts[r * (D + 2) + D]);
+#pragma unroll
+    for (int r = 0; r < DENSE_PREF; ++r) Mt = fmaxf(Mt, pm[r]);
+    for (int r = DENSE_PREF; r < a.dense_slices; ++r) Mt = fmaxf(Mt, parts[r * (D + 2) + D]);
     float Lt = 0.f, Ot = 0.f;
     if (M != -INFINITY) {
-      const float sc = __expf(M - Mt);
-      Lt = L * sc;
-      Ot = O * sc;
+      const float sc0 = __expf(M - Mt);
+      Lt = Ls * sc0;
+      Ot = O * sc0;
     }
-    for (int r = 0; r < a.dense_slices; ++r) {
+#pragma unroll
+    for (int r = 0; r < DENSE_PREF; ++r) {
+      if (pm[r] == -INFINITY) continue;
+      const float f = __expf(pm[r] - Mt);
+      Lt += pl[r] * f;
+      Ot += po[r] * f;
+    }
+    for (int r = DENSE_PREF; r < a.dense_slices; ++r) {
       const float mr = parts[r * (D + 2) + D];
       if (mr == -INFINITY) continue;
-      const float sc = __expf(mr - Mt);
-      Lt += parts[r * (D + 2) + D + 1] * sc;
-      Ot += parts[r * (D + 2) + d] * sc;
+      const float f = __expf(mr - Mt);
+      Lt += parts[r * (D + 2) + D + 1] * f;
+      Ot += parts[r * (D + 2) + d] * f;
     }
     a.out[j * D + d] = (uint16_t)bf16_rne(Ot / Lt);
   }
   SKV_TS(13, 15);
+  SKV_TSE(9);
 }
 
 // ============================================================ launcher

@@ -38,6 +38,46 @@ __device__ __forceinline__ uint4 load_oct(const uint16_t* __restrict__ row, int 
   return make_uint4(cut(w.x, 0), cut(w.y, 1), cut(w.z, 2), cut(w.w, 3));
 }
 
+// Items tied at the k-th score where only `need` of the `ties` (<= FS_TIE_RANK)
+// are members: the need lowest IDs win.  eq: this thread's tied items as
+// member bits; pos(b): the position of bit b; s.ntie must be 0.  The tie
+// positions are compacted into LDS, their IDs read with one load per tie and
+// ranked by comparison.  Returns this thread's winning bits.
+template <typename PosFn, typename IdFn>
+__device__ __forceinline__ uint64_t rank_ties(uint64_t eq, int ties, int need, PosFn pos,
+                                              IdFn id, FastScratch& s) {
+  const int t = threadIdx.x;
+  uint32_t* tpos = reinterpret_cast<uint32_t*>(s.cand);  // [FS_TIE_RANK] positions
+  uint8_t* win = reinterpret_cast<uint8_t*>(tpos + FS_TIE_RANK);  // [FS_TIE_RANK]
+  const int c = __popcll(eq);
+  const int exc = c ? atomicAdd(&s.ntie, c) : 0;  // s.ntie is 0 on entry
+  {
+    uint64_t rest = eq;
+    for (int j = exc; rest; ++j) {
+      tpos[j] = (uint32_t)pos(__ffsll((long long)rest) - 1);
+      rest &= rest - 1;
+    }
+  }
+  __syncthreads();
+  if (t < ties) s.tie[t] = id((int)tpos[t]);
+  __syncthreads();
+  if (t < ties) {  // rank = number of smaller tied IDs (IDs are distinct)
+    const uint32_t x = s.tie[t];
+    int rk = 0;
+    for (int j = 0; j < ties; ++j) rk += s.tie[j] < x;
+    win[t] = rk < need;
+  }
+  __syncthreads();
+  uint64_t m = 0, rest = eq;
+  for (int j = exc; rest; ++j) {
+    const uint64_t low = rest & (0ull - rest);
+    if (win[j]) m |= low;
+    rest &= rest - 1;
+  }
+  __syncthreads();  // the scratch may be reused on return
+  return m;
+}
+
 struct OctResult {
   Selection sel;  // v (k-th best score), above (count scoring > v), all
   uint32_t mine;  // member bits of this thread's 8 items (bit e = item 8t + e)
@@ -45,7 +85,7 @@ struct OctResult {
 };
 
 template <bool VALUE_ONLY, bool POS_IDS, typename IdFn>
-__device__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s) {
+__device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s) {
   OctResult res;
   res.ok = true;
   res.mine = 0;
@@ -128,31 +168,8 @@ __device__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s) {
     res.ok = false;
     return res;
   }
-  // gather the tied IDs, rank them, keep those up to the need-th lowest
-  uint32_t myid[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) myid[e] = 0xffffffffu;
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if ((eq >> e) & 1u) {
-      myid[e] = id(8 * (int)threadIdx.x + e);
-      s.tie[atomicAdd(&s.ntie, 1)] = myid[e];
-    }
-  __syncthreads();
-  if ((int)threadIdx.x < ties) {  // rank = number of smaller tied IDs
-    const uint32_t x = s.tie[threadIdx.x];
-    int r = 0;
-    for (int j = 0; j < ties; ++j) r += s.tie[j] < x;
-    if (r == need - 1) s.sel[2] = (int)x;
-  }
-  __syncthreads();
-  const uint32_t idcut = (uint32_t)s.sel[2];
-  res.sel.idcut = idcut;
-  uint32_t m = 0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) m |= (uint32_t)(((eq >> e) & 1u) && myid[e] <= idcut) << e;
-  res.mine = gt | m;
-  __syncthreads();
+  res.mine = gt | (uint32_t)rank_ties(
+                       eq, ties, need, [](int b) { return 8 * (int)threadIdx.x + b; }, id, s);
   return res;
 }
 

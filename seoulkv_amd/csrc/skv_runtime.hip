@@ -393,6 +393,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.range_cnt = (int4*)ar.take((size_t)G * a.pool_blocks * 16);
     a.surv_cnt = (int*)ar.take((size_t)G * a.pool_blocks * 4);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
+    a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
     a.dense_part = (float*)ar.take((size_t)G * H * std::max(a.dense_slices, 1) * (D + 2) * 4);
     a.selbm = (uint32_t*)ar.take((size_t)G * (nc / 32) * 4);  // cleared by k_front

@@ -91,6 +91,7 @@ struct StepArgs {
   int4* range_cnt;          // [G][pool_blocks] {selected, owned, scanned, work items}
   int* surv_cnt;            // [G][pool_blocks] coarse survivors per range
   int* pool_tok;            // [G][cap]
+  int* pool_post;           // [G][cap] posting index (into post_p2) of each pool key
   uint16_t* s2;             // [G][H][cap] ordered
   uint64_t* bm_u1;          // [G][H][words_u1] top-1600 members
   uint64_t* bm_u2;          // [G][H][words_u2] top-256 members
