@@ -58,12 +58,10 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         # their slice partials out
         "select": G * H * nc * 6 + G * nc // 8 + G * (p.sink + p.local) * 512
         + 16 * ((p.sink + p.local + 255) // 256) * 258 * 4,
-        # CSR bounds + mates of the selected clusters' postings; upper bounds
-        # in and survivor masks out
-        "pool_count": sel * (8 + 4) + scanned * 4 + G * nc * (H * 2 + 1),
-        # CSR, mates, tokens of the selected clusters in; pool tokens and
+        # upper bounds in, survivor masks out; CSR bounds of the selected
+        # lists, mate and token of each of their postings in; pool tokens and
         # posting indices out
-        "pool_emit": sel * (8 + 4 + 4) + scanned * (4 + 4) + pool * 8,
+        "pool": G * nc * (H * 2 + 1) + sel * 8 + scanned * (4 + 4) + pool * 8,
         # posting indices and their 64 B prefix rows in; 2-bit scores out
         "score2": pool * (4 + 64 + H * 2),
         # pool scores in; member bitmaps out

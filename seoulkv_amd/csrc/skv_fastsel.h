@@ -77,12 +77,14 @@ __device__ __forceinline__ bool fs_member(const FastResult& r, uint64_t c, IdFn 
 // Score sources: at(i) = ordered score of item i; oct(o) = the 8 ordered
 // scores of items 8o .. 8o+7 as packed 16-bit pairs.
 struct RowScores {  // a 16-byte aligned row, readable to a multiple of 8 items
+  static constexpr int PRE = 8;  // octets per thread fast_select loads at entry
   const uint16_t* __restrict__ row;
   __device__ uint32_t at(int i) const { return row[i]; }
   __device__ uint4 oct(int o) const { return reinterpret_cast<const uint4*>(row)[o]; }
 };
 
 struct MaskedScores {  // score[i] where gate[i] >= thr, else 0 (excluded)
+  static constexpr int PRE = 4;
   const uint16_t* __restrict__ score;
   const uint16_t* __restrict__ gate;
   uint32_t thr;
@@ -188,6 +190,16 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
     const int i = fs_sample_item(n, u);
     sv[u] = i >= n ? 0u : sample(u, i);
   }
+  // the candidate pass's first Src::PRE octets per thread, loaded now so that
+  // they arrive while the cut is computed
+  static_assert(Src::PRE % FS_OCT == 0, "prefetch whole passes");
+  const int no = (n + 7) >> 3;
+  uint4 pre[Src::PRE];
+#pragma unroll
+  for (int q = 0; q < Src::PRE; ++q) {
+    const int o = (int)threadIdx.x + q * SEL_BLOCK;
+    pre[q] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
+  }
   for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
   if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
@@ -230,16 +242,10 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   // (cut >= 1, so excluded items never pass), then one LDS append per set bit
   {
     const int lane = threadIdx.x & 63;
-    const int no = (n + 7) >> 3;
+    const int base0 = threadIdx.x & ~63;
     const u16x2 cm1 = {(uint16_t)(cut - 1), (uint16_t)(cut - 1)};  // cut >= 1
     uint32_t mx = 0;
-    for (int base = threadIdx.x & ~63; base < no; base += FS_OCT * SEL_BLOCK) {
-      uint4 w[FS_OCT];
-#pragma unroll
-      for (int r = 0; r < FS_OCT; ++r) {
-        const int o = base + r * SEL_BLOCK + lane;
-        w[r] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
-      }
+    auto pass = [&](const uint4 (&w)[FS_OCT], int base) {
       uint32_t mask = 0;
 #pragma unroll
       for (int r = 0; r < FS_OCT; ++r) {
@@ -272,6 +278,24 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
           ++slot;
         }
       }
+    };
+    // passes over the octets loaded at entry, then over the rest
+#pragma unroll
+    for (int p = 0; p < Src::PRE / FS_OCT; ++p) {
+      const int base = base0 + p * FS_OCT * SEL_BLOCK;
+      if (base >= no) break;  // wave-uniform
+      const uint4 w[FS_OCT] = {pre[FS_OCT * p], pre[FS_OCT * p + 1], pre[FS_OCT * p + 2],
+                               pre[FS_OCT * p + 3]};
+      pass(w, base);
+    }
+    for (int base = base0 + Src::PRE * SEL_BLOCK; base < no; base += FS_OCT * SEL_BLOCK) {
+      uint4 w[FS_OCT];
+#pragma unroll
+      for (int r = 0; r < FS_OCT; ++r) {
+        const int o = base + r * SEL_BLOCK + lane;
+        w[r] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
+      }
+      pass(w, base);
     }
     mx = (uint32_t)wave_max((int)mx);
     if (lane == 0) atomicMax(&s.maxo, (int)mx);

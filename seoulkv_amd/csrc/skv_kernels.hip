@@ -327,7 +327,10 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
   if (blockIdx.x == 0) {  // per-step state of the group
     uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
     for (int i = threadIdx.x; i < nc / 32; i += 256) bm[i] = 0;
-    if (threadIdx.x == 0) a.status[g * ST_WORDS + ST_FULLSEL] = 0;
+    if (threadIdx.x == 0) {
+      a.status[g * ST_WORDS + ST_FULLSEL] = 0;
+      a.status[g * ST_WORDS + ST_ERR] = 0;
+    }
   }
   __shared__ __align__(16) QOperand sq;
   prep_operand(a, g, QV_RAW, sp, &sq);
@@ -516,211 +519,275 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
 }
 
 // ============================================================ pool
-// Pool blocks own ranges of 32 consecutive centroids (one selected-bitmap
-// word); their selected clusters are handled one per wave in ascending order.
-__device__ __forceinline__ int nth_set_bit(uint32_t m, int r) {
-  for (int i = 0; i < r; ++i) m &= m - 1;
-  return __ffs(m) - 1;
-}
-
 // Posting j of cluster c is owned iff its mate cluster is larger (or absent)
 // or not selected: the first occurrence in encounter order keeps the token.
 __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint32_t c) {
   return mate > c || !((selbm[mate >> 5] >> (mate & 31)) & 1u);
 }
 
-// Stage the group's selected bitmap and the range's 33 CSR offsets and
-// chunk bases in LDS.
-__device__ __forceinline__ void stage_range(const StepArgs& a, int g, int b, uint32_t* s_bm,
-                                            int* s_off, int* s_cb) {
-  const uint32_t* bm = a.selbm + (size_t)g * (a.nc / 32);
-  for (int i = threadIdx.x; i < a.nc / 32; i += blockDim.x) s_bm[i] = bm[i];
-  if (threadIdx.x <= 32) {
-    const size_t o = (size_t)g * (a.nc + 1) + b * 32 + threadIdx.x;
-    s_off[threadIdx.x] = a.csr_off[o];
-    s_cb[threadIdx.x] = a.chunk_base[o];
-  }
+constexpr int PL_BLOCK = 512;  // pool: one posting per thread and page
+constexpr int PL_WAVES = PL_BLOCK / WAVE;
+constexpr int PL_RANGE = 64;   // centroids per pool block (two selected-bitmap words)
+constexpr int S2_GRID = 320;   // score2 blocks per group (4 waves each)
+constexpr int S2_TILES = 2;    // 16-item tiles per wave and pass (loads issued together)
+
+// Range records for the look-back, one 64-bit word written and read whole:
+// state (bits 62..63) | launch epoch (57..61) | coarse survivors (40..56) |
+// selected clusters (23..39) | owned postings (0..22).  Sums of record values
+// add field by field (a group holds < 2^23 pool keys and <= 65536 clusters).
+// A record of the previous launch (other epoch) reads as not yet published,
+// so nothing is cleared between launches; the records carry every count the
+// scan needs, so no memory fence orders other data before them.
+constexpr unsigned long long LB_A = 1ull << 62;  // the range's own counts
+constexpr unsigned long long LB_P = 2ull << 62;  // counts of all ranges up to this one
+constexpr int LB_SEL = 23, LB_SURV = 40, LB_EPOCH = 57;
+constexpr unsigned long long LB_VAL = (1ull << LB_EPOCH) - 1;
+constexpr unsigned LB_EPOCHS = 32;
+constexpr int LB_SPIN_MAX = 1 << 22;  // polls before a wait is abandoned (ST_ERR 6)
+constexpr int LB_WIN = 4;             // 64-range windows read per poll
+__device__ __forceinline__ int lb_field(unsigned long long v, int shift, int bits) {
+  return (int)((v >> shift) & ((1ull << bits) - 1));
 }
 
-constexpr int PC_BLOCK = 512;   // pool_count: one wave per selected cluster
-constexpr int PC_WAVES = PC_BLOCK / WAVE;
-constexpr int PE_BLOCK = 512;   // pool_emit: one wave per 64-posting chunk
-constexpr int PE_WAVES = PE_BLOCK / WAVE;
-constexpr int S2_GRID = 320;    // score2 blocks per group (4 waves each)
-constexpr int S2_TILES = 2;     // 16-item tiles per wave and pass (loads issued together)
-
-// Work items of a selected cluster: its 64-posting chunks (one item for an
-// empty list, so that every selected cluster is listed).
-__device__ __forceinline__ int cluster_items(int postings) {
-  return max(1, (postings + 63) / 64);
+__device__ __forceinline__ unsigned long long lb_load(const unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Owned postings of every selected cluster of the range (one wave per
-// cluster), per 64-posting chunk and in total, and the range's counts
-// {selected, owned, scanned, work items}.
-__global__ __launch_bounds__(PC_BLOCK) void k_pool_count(StepArgs a) {
+// The pool of one KV group in encounter order: selected clusters ascending,
+// CSR order within a cluster, each token kept at its first occurrence.
+// Block b = the 64-centroid range b (two selected-bitmap words).  Each range
+// publishes its counts, then sums its predecessors' counts (decoupled
+// look-back: a predecessor that already published its inclusive prefix ends
+// the walk) and writes its owned postings at their pool positions, one
+// posting per thread.
+__global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   SKV_TSB(0, 0);
   SKV_TS(5, 0);
-  const int g = blockIdx.y, b = blockIdx.x;
+  const int g = blockIdx.y, nc = a.nc, nb = gridDim.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ uint32_t s_bm[];
-  __shared__ int s_off[33], s_cb[33];
-  __shared__ int s_own[PC_WAVES], s_scan[PC_WAVES], s_items[PC_WAVES];
-  stage_range(a, g, b, s_bm, s_off, s_cb);
-  if (threadIdx.x < 64) {  // survivor head masks of the range: upper_h >= thr_h
-    const int c = b * 32 + (threadIdx.x & 31);
+  __shared__ int s_off[PL_RANGE + 1], s_cum[PL_RANGE + 1], s_cl[PL_RANGE];
+  __shared__ int s_scan[PL_WAVES + 1], s_surv, s_scanned;
+  __shared__ unsigned long long s_excl;
+  // range b = block b: workgroups are dispatched in index order within each
+  // XCD, so the lowest unfinished range always gets a slot and every wait
+  // below ends.  The launch epoch tags this launch's records.
+  const int b = blockIdx.x, c0 = b * PL_RANGE;
+  const int ncr = min(PL_RANGE, nc - c0);  // centroids of the range (a multiple of 32)
+  const unsigned epoch = a.pool_epoch[g];
+  const unsigned long long tag = (unsigned long long)(epoch % LB_EPOCHS) << LB_EPOCH;
+  {
+    const uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
+    for (int i = threadIdx.x; i < nc / 32; i += PL_BLOCK) s_bm[i] = bm[i];
+  }
+  if ((int)threadIdx.x <= ncr) s_off[threadIdx.x] = a.csr_off[(size_t)g * (nc + 1) + c0 + threadIdx.x];
+  if (wave == 1) {  // survivor head masks: upper_h >= thr_h
+    const int c = c0 + lane;
     uint32_t m = 0;
-    if (threadIdx.x < 32) {
+    if (lane < ncr) {
 #pragma unroll
       for (int h = 0; h < H; ++h)
-        m |= (uint32_t)(a.upper[((size_t)g * H + h) * a.nc + c] >= a.thr[g * H + h]) << h;
-      a.masks[(size_t)g * a.nc + c] = (uint8_t)m;
+        m |= (uint32_t)(a.upper[((size_t)g * H + h) * nc + c] >= a.thr[g * H + h]) << h;
+      a.masks[(size_t)g * nc + c] = (uint8_t)m;
     }
     const uint64_t alive = __ballot(m != 0);
-    if (threadIdx.x == 0) a.surv_cnt[(size_t)g * a.pool_blocks + b] = __popcll(alive);
+    if (lane == 0) {
+      s_surv = __popcll(alive);
+      s_scanned = 0;
+    }
   }
   __syncthreads();
-  const uint32_t M = s_bm[b];
-  const int nsel = __popc(M);
-  const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
-  int* own_chunk = a.own_chunk + (size_t)g * a.chunks_max;
-  int own_w = 0, scan_w = 0, items_w = 0;
-  for (int rk = wave; rk < nsel; rk += PC_WAVES) {
-    const int cl = nth_set_bit(M, rk);
-    const uint32_t c = b * 32 + cl;
-    const int j0 = s_off[cl], j1 = s_off[cl + 1];
-    int own = 0;
-    for (int jc = j0, kk = 0; jc < j1; jc += 64, ++kk) {
-      const int j = jc + lane;
-      const bool o = j < j1 && owned(s_bm, (uint32_t)mate[j], c);
-      const int oc = __popcll(__ballot(o));
-      if (lane == 0) own_chunk[s_cb[cl] + kk] = oc;
-      own += oc;
-    }
-    if (lane == 0) a.own_cnt[(size_t)g * a.nc + c] = own;
-    own_w += own;
-    scan_w += j1 - j0;
-    items_w += cluster_items(j1 - j0);
-  }
-  if (lane == 0) {
-    s_own[wave] = own_w;
-    s_scan[wave] = scan_w;
-    s_items[wave] = items_w;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int o = 0, sc = 0, it = 0;
-    for (int w = 0; w < PC_WAVES; ++w) {
-      o += s_own[w];
-      sc += s_scan[w];
-      it += s_items[w];
-    }
-    a.range_cnt[(size_t)g * a.pool_blocks + b] = make_int4(nsel, o, sc, it);
-  }
-  SKV_TSE(0);
-}
-
-// Emit the selected list and the pool tokens in encounter order.  Block b
-// owns the 32-centroid range b; its work items are the 64-posting chunks of
-// the range's selected clusters, one per wave at a time.  A chunk's first
-// pool position is its cluster's (owned counts of the earlier ranges and of
-// the range's earlier selected clusters) plus the owned counts of the
-// cluster's earlier chunks.
-__global__ __launch_bounds__(PE_BLOCK) void k_pool_emit(StepArgs a) {
-  SKV_TSB(1, 0);
-  SKV_TS(6, 0);
-  const int g = blockIdx.y, b = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  extern __shared__ uint32_t s_bm[];
-  __shared__ int s_off[33], s_cb[33];
-  __shared__ int s_pos[32], s_cl[32], s_chb[33];
-  stage_range(a, g, b, s_bm, s_off, s_cb);
-  __syncthreads();
-  const int4* rc = a.range_cnt + (size_t)g * a.pool_blocks;
-  if (wave == 0) {
-    // prefix over the preceding ranges (the last range also writes totals)
-    const bool last = b == a.pool_blocks - 1;
-    const uint32_t M = s_bm[b];
-    const int own_raw = lane < 32 ? a.own_cnt[(size_t)g * a.nc + b * 32 + lane] : 0;
-    int ps = 0, po = 0, ts = 0, to = 0, tn = 0;
-    for (int i0 = lane; i0 <= b; i0 += 256) {
-      int4 x[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) x[u] = i0 + 64 * u <= b ? rc[i0 + 64 * u] : make_int4(0, 0, 0, 0);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (i0 + 64 * u < b) { ps += x[u].x; po += x[u].y; }
-        ts += x[u].x; to += x[u].y; tn += x[u].z;
-      }
-    }
-    ps = wave_sum(ps);
-    po = wave_sum(po);
-    if (last) {
-      int sv = 0;
-      for (int i = lane; i < a.pool_blocks; i += 64) sv += a.surv_cnt[(size_t)g * a.pool_blocks + i];
-      sv = wave_sum(sv);
-      ts = wave_sum(ts);
-      to = wave_sum(to);
-      tn = wave_sum(tn);
-      if (lane == 0) {
-        int err = 0;
-        if (a.pool_capacity > 0 && to > a.pool_capacity) err = 4;
-        else if (to < a.pool_min) err = 5;
-        a.status[g * ST_WORDS + ST_POOL] = min(to, a.cap);
-        a.status[g * ST_WORDS + ST_ERR] = err;
-        a.status[g * ST_WORDS + ST_SEL] = ts;
-        a.status[g * ST_WORDS + ST_SURV] = sv;
-        a.status[g * ST_WORDS + ST_SCANNED] = tn;
-      }
-    }
-    // per selected cluster (centroid order = selection order): pool base,
-    // range offset and first work item
-    const bool is_sel = lane < 32 && ((M >> lane) & 1u);
-    const int rank = __popc(M & ((1u << (lane & 31)) - 1u));
-    const int own = is_sel ? own_raw : 0;
-    const int nch = is_sel ? cluster_items(s_off[lane + 1] - s_off[lane]) : 0;
-    const int inc = wave_incl_scan(own);
-    const int incc = wave_incl_scan(nch);
+  const uint64_t M = (uint64_t)s_bm[c0 / 32] | (ncr > 32 ? (uint64_t)s_bm[c0 / 32 + 1] << 32 : 0ull);
+  const int nsel = __popcll(M);
+  if (wave == 0) {  // the range's selected clusters in order and their posting offsets
+    const bool is_sel = (M >> lane) & 1ull;
+    const int size = is_sel ? s_off[lane + 1] - s_off[lane] : 0;
+    const int inc = wave_incl_scan(size);
     if (is_sel) {
-      s_pos[rank] = po + inc - own;
-      s_cl[rank] = lane;
-      s_chb[rank] = incc - nch;
-      a.sel[(size_t)g * a.nc + ps + rank] = b * 32 + lane;
+      const int r = __popcll(M & ((1ull << lane) - 1ull));
+      s_cl[r] = lane;
+      s_cum[r + 1] = inc;
     }
-    if (lane == 63) s_chb[__popc(M)] = incc;
+    if (lane == 0) s_cum[0] = 0;
   }
   __syncthreads();
-  SKV_TSB(1, 1);
-  const uint32_t M = s_bm[b];
-  const int nsel = __popc(M);
-  const int nitems = s_chb[nsel];
-  const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
+  const int S = s_cum[nsel];  // postings of the selected clusters
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
-  const int* __restrict__ own_chunk = a.own_chunk + (size_t)g * a.chunks_max;
+  const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
+  // posting i of the range's selected lists -> (posting index, owned)
+  auto posting = [&](int i, int& j) {
+    int lo = 0, hi = nsel;  // s_cum[lo] <= i < s_cum[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_cum[mid] <= i) lo = mid;
+      else hi = mid;
+    }
+    const int cl = s_cl[lo];
+    j = s_off[cl] + (i - s_cum[lo]);
+    return owned(s_bm, (uint32_t)mate[j], (uint32_t)(c0 + cl));
+  };
+  // ---- count (the first page stays in registers for the emit)
+  int j0 = 0, t0 = 0;
+  bool o0 = false;
+  if ((int)threadIdx.x < S) {
+    o0 = posting(threadIdx.x, j0);
+    t0 = ptok[j0];
+  }
+  int owned_total;
+  const int ex0 = block_excl_scan(o0 ? 1 : 0, s_scan, &owned_total);
+  const int page0_total = owned_total;
+  for (int base = PL_BLOCK; base < S; base += PL_BLOCK) {
+    int j = 0;
+    const bool o = (int)(base + threadIdx.x) < S && posting(base + threadIdx.x, j);
+    int tot;
+    (void)block_excl_scan(o ? 1 : 0, s_scan, &tot);
+    owned_total += tot;
+  }
+  // ---- publish, then look back for the counts of the earlier ranges
+  unsigned long long* flags = a.pool_flags + (size_t)g * nb;
+  const unsigned long long agg = ((unsigned long long)s_surv << LB_SURV) |
+                                 ((unsigned long long)nsel << LB_SEL) | (unsigned)owned_total;
+  if (wave == 0) {
+    if (lane == 0) {
+      lb_store(&flags[b], (b == 0 ? LB_P : LB_A) | tag | agg);
+      SKV_TSB(0, 2);
+    }
+    // up to LB_WIN * 64 predecessors per poll: entry (k, lane) is range
+    // i - 64 k - lane, k-major in distance
+    unsigned long long excl = 0;
+    int spins = 0;
+    for (int i = b - 1; i >= 0;) {
+      unsigned long long v[LB_WIN];
+      bool cur[LB_WIN];
+      uint64_t pm[LB_WIN], xm[LB_WIN];
+#pragma unroll
+      for (int k = 0; k < LB_WIN; ++k) {
+        const int idx = i - 64 * k - lane;
+        v[k] = idx >= 0 ? lb_load(&flags[idx]) : (LB_P | tag);
+      }
+#pragma unroll
+      for (int k = 0; k < LB_WIN; ++k) {
+        cur[k] = (v[k] & ~LB_VAL & ~(3ull << 62)) == tag;  // published in this launch
+        pm[k] = __ballot(cur[k] && (v[k] >> 62) == 2);
+        xm[k] = __ballot(!cur[k] || (v[k] >> 62) == 0);
+      }
+      // the nearest inclusive prefix ends the walk; every nearer entry is needed
+      int kp = LB_WIN, lp = 63;
+#pragma unroll
+      for (int k = LB_WIN - 1; k >= 0; --k)
+        if (pm[k]) {
+          kp = k;
+          lp = __ffsll((long long)pm[k]) - 1;
+        }
+      bool wait = false;
+#pragma unroll
+      for (int k = 0; k < LB_WIN; ++k) {
+        const uint64_t need = k < kp ? ~0ull : k == kp ? (lp == 63 ? ~0ull : ((1ull << (lp + 1)) - 1ull)) : 0ull;
+        wait = wait || (xm[k] & need) != 0;
+      }
+      if (wait) {  // a needed range has not published yet
+        if (++spins > LB_SPIN_MAX) {
+          if (lane == 0) a.status[g * ST_WORDS + ST_ERR] = 6;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        continue;
+      }
+      int o = 0, sl = 0, sv = 0;
+#pragma unroll
+      for (int k = 0; k < LB_WIN; ++k) {
+        const bool take = k < kp || (k == kp && lane <= lp);
+        if (take) {
+          o += lb_field(v[k], 0, LB_SEL);
+          sl += lb_field(v[k], LB_SEL, LB_SURV - LB_SEL);
+          sv += lb_field(v[k], LB_SURV, LB_EPOCH - LB_SURV);
+        }
+      }
+      o = wave_sum(o);
+      sl = wave_sum(sl);
+      sv = wave_sum(sv);
+      excl += ((unsigned long long)sv << LB_SURV) | ((unsigned long long)sl << LB_SEL) | (unsigned)o;
+      if (kp < LB_WIN) break;
+      i -= 64 * LB_WIN;
+    }
+    if (lane == 0) {
+      if (b > 0) lb_store(&flags[b], LB_P | tag | (excl + agg));
+      s_excl = excl;
+      // every range has published, so every block has read the epoch
+      if (b == nb - 1) a.pool_epoch[g] = epoch + 1;
+#ifdef SKV_TRACE
+      {
+        const unsigned _bb = blockIdx.x + blockIdx.y * gridDim.x;
+        if (_bb < 4096) g_skv_trace_blk[10][_bb][0] = (unsigned long long)spins;
+        if (_bb < 4096) g_skv_trace_blk[10][_bb][1] = (unsigned long long)b;
+        if (_bb < 4096) g_skv_trace_blk[10][_bb][2] = (unsigned long long)S;
+      }
+#endif
+    }
+  } else if (b == nb - 1) {  // the last range: postings of all selected lists
+    // 16 centroids per thread and pass, their 17 CSR offsets loaded together
+    int sc = 0;
+    const int* off = a.csr_off + (size_t)g * (nc + 1);
+    for (int ch = (int)threadIdx.x - WAVE; ch < nc / 16; ch += PL_BLOCK - WAVE) {
+      const uint32_t m16 = (s_bm[ch >> 1] >> (16 * (ch & 1))) & 0xffffu;
+      if (!m16) continue;
+      int o[17];
+#pragma unroll
+      for (int q = 0; q < 17; ++q) o[q] = off[16 * ch + q];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if ((m16 >> q) & 1u) sc += o[q + 1] - o[q];
+    }
+    sc = wave_sum(sc);
+    if (lane == 0) atomicAdd(&s_scanned, sc);
+  }
+  __syncthreads();
+  SKV_TSB(0, 1);
+  const unsigned long long excl = s_excl;
+  const int pos0 = lb_field(excl, 0, LB_SEL), sel0 = lb_field(excl, LB_SEL, LB_SURV - LB_SEL);
+  const int surv0 = lb_field(excl, LB_SURV, LB_EPOCH - LB_SURV);
+  // ---- emit: the selected list and the owned postings at their positions
+  if (wave == 0 && lane < nsel) a.sel[(size_t)g * nc + sel0 + lane] = c0 + s_cl[lane];
   int* pool = a.pool_tok + (size_t)g * a.cap;
   int* pool_post = a.pool_post + (size_t)g * a.cap;
-  for (int it = wave; it < nitems; it += PE_WAVES) {
-    // the item's cluster: the last selected rank whose first item is <= it
-    const uint64_t bal = __ballot(lane < nsel && s_chb[lane] <= it);
-    const int r = 63 - __clzll(bal);
-    const int k = it - s_chb[r];
-    const int cl = s_cl[r];
-    const uint32_t c = b * 32 + cl;
-    const int j = s_off[cl] + 64 * k + lane, j1 = s_off[cl + 1];
-    const int mj = j < j1 ? mate[j] : -1;
-    const int tj = j < j1 ? ptok[j] : 0;
-    int pre = 0;
-    for (int t = lane; t < k; t += 64) pre += own_chunk[s_cb[cl] + t];
-    const int pos = s_pos[r] + (k > 0 ? wave_sum(pre) : 0);
-    const bool o = j < j1 && owned(s_bm, (uint32_t)mj, c);
-    const uint64_t om = __ballot(o);
-    const int p = pos + __popcll(om & ((1ull << lane) - 1));
+  if (o0 && pos0 + ex0 < a.cap) {
+    pool[pos0 + ex0] = t0;
+    pool_post[pos0 + ex0] = j0;
+  }
+  int carry = page0_total;
+  for (int base = PL_BLOCK; base < S; base += PL_BLOCK) {  // ranges over one page
+    int j = 0;
+    const bool o = (int)(base + threadIdx.x) < S && posting(base + threadIdx.x, j);
+    int tot;
+    const int ex = block_excl_scan(o ? 1 : 0, s_scan, &tot);
+    const int p = pos0 + carry + ex;
     if (o && p < a.cap) {
-      pool[p] = tj;
+      pool[p] = ptok[j];
       pool_post[p] = j;
     }
+    carry += tot;
   }
-  SKV_TSE(1);
+  // ---- the last range writes the group's totals
+  if (b == nb - 1 && threadIdx.x == 0) {
+    {
+      const int sv = surv0 + s_surv, sc = s_scanned;
+      const int to = pos0 + owned_total, ts = sel0 + nsel;
+      int err = a.status[g * ST_WORDS + ST_ERR];
+      if (err == 0) {
+        if (a.pool_capacity > 0 && to > a.pool_capacity) err = 4;
+        else if (to < a.pool_min) err = 5;
+      }
+      a.status[g * ST_WORDS + ST_POOL] = min(to, a.cap);
+      a.status[g * ST_WORDS + ST_ERR] = err;
+      a.status[g * ST_WORDS + ST_SEL] = ts;
+      a.status[g * ST_WORDS + ST_SURV] = sv;
+      a.status[g * ST_WORDS + ST_SCANNED] = sc;
+    }
+  }
+  SKV_TSE(0);
 }
 
 // 2-bit pool scores s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) from each pool
@@ -1227,8 +1294,8 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
-    "front", "select", "pool_count", "pool_emit", "score2", "top1600", "union_score4",
-    "top256", "union_score8", "top100_sdpa"};
+    "front", "select", "pool", "score2", "top1600", "union_score4", "top256", "union_score8",
+    "top100_sdpa"};
 
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
@@ -1245,27 +1312,24 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
                          w.select_lds, st, a);
       break;
     case 2:
-      hipLaunchKernelGGL(k_pool_count, dim3(a.pool_blocks, G), dim3(PC_BLOCK), bm_lds, st, a);
+      hipLaunchKernelGGL(k_pool, dim3((a.nc + PL_RANGE - 1) / PL_RANGE, G), dim3(PL_BLOCK), bm_lds, st, a);
       break;
     case 3:
-      hipLaunchKernelGGL(k_pool_emit, dim3(a.pool_blocks, G), dim3(PE_BLOCK), bm_lds, st, a);
-      break;
-    case 4:
       hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);
       break;
-    case 5:
+    case 4:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
       break;
-    case 6:
+    case 5:
       hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(US_BLOCK), 0, st, a);
       break;
-    case 7:
+    case 6:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
       break;
-    case 8:
+    case 7:
       hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(US_BLOCK), 0, st, a);
       break;
-    case 9:
+    case 8:
       hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
       break;
     default:

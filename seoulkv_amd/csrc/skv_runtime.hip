@@ -335,18 +335,6 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   a.words_u1 = words1;
   a.words_u2 = words2;
   a.pool_blocks = nc / 32;
-  // 64-posting chunks of every cluster (static prefix over the CSR lists)
-  std::vector<int> chunk_base((size_t)G * (nc + 1));
-  a.chunks_max = 1;
-  for (int g = 0; g < G; ++g) {
-    int acc = 0;
-    for (int c = 0; c < nc; ++c) {
-      chunk_base[(size_t)g * (nc + 1) + c] = acc;
-      acc += (ix->cells[g].offsets[c + 1] - ix->cells[g].offsets[c] + 63) / 64;
-    }
-    chunk_base[(size_t)g * (nc + 1) + nc] = acc;
-    a.chunks_max = std::max(a.chunks_max, acc);
-  }
   a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
 
   // ---- static arena
@@ -359,7 +347,6 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.resid = (float*)ar.take((size_t)G * nc * 4);
     a.gfs = (float*)ar.take((size_t)G * (nc / 32) * 4);
     a.csr_off = (int*)ar.take((size_t)G * (nc + 1) * 4);
-    a.chunk_base = (int*)ar.take((size_t)G * (nc + 1) * 4);
     a.post_tok = (int*)ar.take((size_t)G * np_max * 4);
     a.post_mate = (int*)ar.take((size_t)G * np_max * 4);
     a.post_p2 = (uint8_t*)ar.take((size_t)G * np_max * 64);
@@ -388,10 +375,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.fine_ord = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.fine_bits = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.sel = (int*)ar.take((size_t)G * nc * 4);
-    a.own_cnt = (int*)ar.take((size_t)G * nc * 4);
-    a.own_chunk = (int*)ar.take((size_t)G * a.chunks_max * 4);
-    a.range_cnt = (int4*)ar.take((size_t)G * a.pool_blocks * 16);
-    a.surv_cnt = (int*)ar.take((size_t)G * a.pool_blocks * 4);
+    a.pool_flags = (unsigned long long*)ar.take((size_t)G * a.pool_blocks * 8);
+    a.pool_epoch = (unsigned*)ar.take((size_t)G * 4);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
     a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
@@ -459,7 +444,6 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
       up_copy(a.resid, resid.data(), resid.size() * 4) ||
       up_copy(a.gfs, gfs.data(), gfs.size() * 4) ||
       up_copy(a.csr_off, off.data(), off.size() * 4) ||
-      up_copy(a.chunk_base, chunk_base.data(), chunk_base.size() * 4) ||
       up_copy(a.post_tok, ptok.data(), ptok.size() * 4) ||
       up_copy(a.post_mate, pmate.data(), pmate.size() * 4)) {
     fail(h, SKV_EHIP, "index upload failed");

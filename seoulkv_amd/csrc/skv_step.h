@@ -58,7 +58,7 @@ struct StepArgs {
   float lam[G];
   int pool_min, pool_capacity, debug;
   int exact_select;         // 1: always run the full selections (no sampled cut)
-  int pool_blocks;          // nc / 32: 32-centroid ranges of the pool kernels
+  int pool_blocks;          // nc / 32: 32-centroid ranges of the pool kernel
   int words_u1, words_u2;   // bitmap words per (group, head)
   int dense_slices;         // DENSE_SLICE_KEYS-key sink/local attention slices per query head
   // static device data
@@ -70,8 +70,6 @@ struct StepArgs {
   const float* resid;       // [G][nc]
   const float* gfs;         // [G][nc/32]
   const int* csr_off;       // [G][nc+1]
-  const int* chunk_base;    // [G][nc+1] first 64-posting chunk of each cluster
-  int chunks_max;           // chunks per group (row stride of own_chunk)
   const int* post_tok;      // [G][np_max]
   const int* post_mate;     // [G][np_max] (-1: no mate)
   const uint8_t* post_p2;   // [G][np_max][64]
@@ -86,10 +84,8 @@ struct StepArgs {
   uint16_t* fine_ord;       // [G][H][nc] ordered fine score of every centroid
   uint16_t* fine_bits;      // [G][H][nc] BF16 fine score (debug)
   int* sel;                 // [G][nc] selected clusters, ascending
-  int* own_cnt;             // [G][nc] owned postings per selected cluster
-  int* own_chunk;           // [G][chunks_max] owned postings per chunk of a selected cluster
-  int4* range_cnt;          // [G][pool_blocks] {selected, owned, scanned, work items}
-  int* surv_cnt;            // [G][pool_blocks] coarse survivors per range
+  unsigned long long* pool_flags;  // [G][pool_blocks] look-back records (epoch-tagged)
+  unsigned* pool_epoch;     // [G] launches of the pool kernel (tags the look-back records)
   int* pool_tok;            // [G][cap]
   int* pool_post;           // [G][cap] posting index (into post_p2) of each pool key
   uint16_t* s2;             // [G][H][cap] ordered
@@ -133,7 +129,7 @@ constexpr int ATTN_WAVES = 16;
 constexpr size_t ATTN_SCRATCH_BYTES = (size_t)ATTN_WAVES * (2 + D) * 4;
 constexpr int DENSE_SLICE_KEYS = ATTN_WAVES * 16;
 
-constexpr int N_STEP_KERNELS = 10;
+constexpr int N_STEP_KERNELS = 9;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 // Kernel k (0 .. N_STEP_KERNELS - 1, in step order) of one decode step.
