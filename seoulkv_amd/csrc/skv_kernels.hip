@@ -527,7 +527,7 @@ __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint
 
 constexpr int PL_BLOCK = 512;  // pool: one posting per thread and page
 constexpr int PL_WAVES = PL_BLOCK / WAVE;
-constexpr int PL_RANGE = 64;   // centroids per pool block (two selected-bitmap words)
+constexpr int PL_RANGE_MAX = PL_BLOCK;  // centroids per pool block: one per thread
 constexpr int S2_GRID = 320;   // score2 blocks per group (4 waves each)
 constexpr int S2_TILES = 2;    // 16-item tiles per wave and pass (loads issued together)
 
@@ -558,7 +558,7 @@ __device__ __forceinline__ void lb_store(unsigned long long* p, unsigned long lo
 
 // The pool of one KV group in encounter order: selected clusters ascending,
 // CSR order within a cluster, each token kept at its first occurrence.
-// Block b = the 64-centroid range b (two selected-bitmap words).  Each range
+// Block b = range b of pool_range centroids (a multiple of 32).  Each range
 // publishes its counts, then sums its predecessors' counts (decoupled
 // look-back: a predecessor that already published its inclusive prefix ends
 // the walk) and writes its owned postings at their pool positions, one
@@ -567,52 +567,54 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   SKV_TSB(0, 0);
   SKV_TS(5, 0);
   const int g = blockIdx.y, nc = a.nc, nb = gridDim.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
   extern __shared__ uint32_t s_bm[];
-  __shared__ int s_off[PL_RANGE + 1], s_cum[PL_RANGE + 1], s_cl[PL_RANGE];
+  __shared__ int s_off[PL_RANGE_MAX + 1], s_cum[PL_RANGE_MAX + 1], s_cl[PL_RANGE_MAX];
   __shared__ int s_scan[PL_WAVES + 1], s_surv, s_scanned;
   __shared__ unsigned long long s_excl;
   // range b = block b: workgroups are dispatched in index order within each
   // XCD, so the lowest unfinished range always gets a slot and every wait
   // below ends.  The launch epoch tags this launch's records.
-  const int b = blockIdx.x, c0 = b * PL_RANGE;
-  const int ncr = min(PL_RANGE, nc - c0);  // centroids of the range (a multiple of 32)
+  const int b = blockIdx.x, c0 = b * a.pool_range;
+  const int ncr = min(a.pool_range, nc - c0);  // centroids of the range (a multiple of 32)
   const unsigned epoch = a.pool_epoch[g];
   const unsigned long long tag = (unsigned long long)(epoch % LB_EPOCHS) << LB_EPOCH;
   {
     const uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
-    for (int i = threadIdx.x; i < nc / 32; i += PL_BLOCK) s_bm[i] = bm[i];
+    for (int i = t; i < nc / 32; i += PL_BLOCK) s_bm[i] = bm[i];
   }
-  if ((int)threadIdx.x <= ncr) s_off[threadIdx.x] = a.csr_off[(size_t)g * (nc + 1) + c0 + threadIdx.x];
-  if (wave == 1) {  // survivor head masks: upper_h >= thr_h
-    const int c = c0 + lane;
-    uint32_t m = 0;
-    if (lane < ncr) {
+  for (int i = t; i <= ncr; i += PL_BLOCK) s_off[i] = a.csr_off[(size_t)g * (nc + 1) + c0 + i];
+  if (t == 0) {
+    s_surv = 0;
+    s_scanned = 0;
+  }
+  // survivor head masks (upper_h >= thr_h) of the range's centroids
+  uint32_t m = 0;
+  if (t < ncr) {
+    const int c = c0 + t;
 #pragma unroll
-      for (int h = 0; h < H; ++h)
-        m |= (uint32_t)(a.upper[((size_t)g * H + h) * nc + c] >= a.thr[g * H + h]) << h;
-      a.masks[(size_t)g * nc + c] = (uint8_t)m;
-    }
-    const uint64_t alive = __ballot(m != 0);
-    if (lane == 0) {
-      s_surv = __popcll(alive);
-      s_scanned = 0;
-    }
+    for (int h = 0; h < H; ++h)
+      m |= (uint32_t)(a.upper[((size_t)g * H + h) * nc + c] >= a.thr[g * H + h]) << h;
+    a.masks[(size_t)g * nc + c] = (uint8_t)m;
   }
   __syncthreads();
-  const uint64_t M = (uint64_t)s_bm[c0 / 32] | (ncr > 32 ? (uint64_t)s_bm[c0 / 32 + 1] << 32 : 0ull);
-  const int nsel = __popcll(M);
-  if (wave == 0) {  // the range's selected clusters in order and their posting offsets
-    const bool is_sel = (M >> lane) & 1ull;
-    const int size = is_sel ? s_off[lane + 1] - s_off[lane] : 0;
-    const int inc = wave_incl_scan(size);
-    if (is_sel) {
-      const int r = __popcll(M & ((1ull << lane) - 1ull));
-      s_cl[r] = lane;
-      s_cum[r + 1] = inc;
-    }
-    if (lane == 0) s_cum[0] = 0;
+  {
+    const int alive = __popcll(__ballot(m != 0));
+    if (lane == 0 && alive) atomicAdd(&s_surv, alive);
   }
+  // the range's selected clusters in order and their posting offsets: one
+  // scan of (postings << 10 | selected) over the range's centroids
+  const bool is_sel = t < ncr && ((s_bm[(c0 + t) >> 5] >> (t & 31)) & 1u);
+  const int size = is_sel ? s_off[t + 1] - s_off[t] : 0;
+  int tot;
+  const unsigned ex = (unsigned)block_excl_scan((size << 10) | (is_sel ? 1 : 0), s_scan, &tot);
+  const int nsel = (unsigned)tot & 1023u;
+  if (is_sel) {
+    const int r = ex & 1023u;
+    s_cl[r] = t;
+    s_cum[r] = (int)(ex >> 10);
+  }
+  if (t == 0) s_cum[nsel] = (int)((unsigned)tot >> 10);
   __syncthreads();
   const int S = s_cum[nsel];  // postings of the selected clusters
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
@@ -750,7 +752,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   const int pos0 = lb_field(excl, 0, LB_SEL), sel0 = lb_field(excl, LB_SEL, LB_SURV - LB_SEL);
   const int surv0 = lb_field(excl, LB_SURV, LB_EPOCH - LB_SURV);
   // ---- emit: the selected list and the owned postings at their positions
-  if (wave == 0 && lane < nsel) a.sel[(size_t)g * nc + sel0 + lane] = c0 + s_cl[lane];
+  for (int r = t; r < nsel; r += PL_BLOCK) a.sel[(size_t)g * nc + sel0 + r] = c0 + s_cl[r];
   int* pool = a.pool_tok + (size_t)g * a.cap;
   int* pool_post = a.pool_post + (size_t)g * a.cap;
   if (o0 && pos0 + ex0 < a.cap) {
@@ -1312,7 +1314,8 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
                          w.select_lds, st, a);
       break;
     case 2:
-      hipLaunchKernelGGL(k_pool, dim3((a.nc + PL_RANGE - 1) / PL_RANGE, G), dim3(PL_BLOCK), bm_lds, st, a);
+      hipLaunchKernelGGL(k_pool, dim3((a.nc + a.pool_range - 1) / a.pool_range, G), dim3(PL_BLOCK),
+                         bm_lds, st, a);
       break;
     case 3:
       hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);

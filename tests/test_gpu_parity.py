@@ -84,6 +84,17 @@ def test_step_parity(runtimes, name, qi):
     rt.enqueue()
     status = rt.synchronize()
     traces, out = oracle_step(p, q)
+    index = case(**p)[0]
+    # status words: no error (the pool kernel's look-back never gave up) and
+    # the stage sizes of the oracle
+    assert status["err"] == [0, 0, 0, 0]
+    for g, tr in enumerate(traces):
+        off = index.cells[g]["offsets"].numpy().astype(np.int64)
+        assert status["pool"][g] == len(tr.pool), f"g{g} pool size"
+        assert status["selected"][g] == len(tr.selected), f"g{g} selected"
+        assert status["survivors"][g] == len(tr.survivors), f"g{g} survivors"
+        scanned = int((off[tr.selected + 1] - off[tr.selected]).sum())
+        assert status["scanned"][g] == scanned, f"g{g} scanned postings"
     for g, tr in enumerate(traces):
         qp = tr.extra["qprep"]
         dq = rt.read_stage("qprep", g)
