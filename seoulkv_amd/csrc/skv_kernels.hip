@@ -1020,7 +1020,13 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   __shared__ int s_tok[US_CHUNK * 64];
   auto word = [&](int w) { return bm[w] | bm[W + w] | bm[2 * W + w] | bm[3 * W + w]; };
 
-  // members in words [0, w_lo): 4 words (16 loads) in flight per thread
+  // issued together: the member counts of words [0, w_lo) (4 words, 16
+  // loads in flight per thread), the first chunk's words (one bitmap word per
+  // thread < 4 US_CHUNK) and its input tokens (one per thread)
+  const int nw0 = min(US_CHUNK, w_hi - w_lo);
+  uint64_t hw = 0;
+  if ((int)threadIdx.x < H * nw0) hw = bm[(threadIdx.x / nw0) * W + w_lo + threadIdx.x % nw0];
+  const int tok0 = (int)threadIdx.x < 64 * nw0 ? tok_in[64 * w_lo + threadIdx.x] : 0;
   int cnt = 0;
   for (int w = threadIdx.x; w < w_lo; w += 4 * US_BLOCK) {
     uint64_t m[4];
@@ -1032,9 +1038,11 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) cnt += __popcll(m[u]);
   }
+  if (threadIdx.x < US_CHUNK) s_word[threadIdx.x] = 0;
   cnt = wave_sum(cnt);
   if (lane == 0) s_red[wave] = cnt;
   __syncthreads();
+  if (hw) atomicOr(reinterpret_cast<unsigned long long*>(&s_word[threadIdx.x % nw0]), hw);
   int base = 0;
 #pragma unroll
   for (int i = 0; i < US_BLOCK / WAVE; ++i) base += s_red[i];
@@ -1046,14 +1054,17 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
   const int row = lane & 15, kb = lane >> 4;
   for (int c0 = w_lo; c0 < w_hi; c0 += US_CHUNK) {
     const int nw = min(US_CHUNK, w_hi - c0);
-    if (threadIdx.x < 64) {  // wave 0: the chunk's words and their member bases
-      const uint64_t m = lane < nw ? word(c0 + lane) : 0ull;
+    const bool first = c0 == w_lo;
+    if (!first) {  // later chunks (long inputs): the union words now
+      __syncthreads();
+      if (threadIdx.x < US_CHUNK) s_word[threadIdx.x] = (int)threadIdx.x < nw ? word(c0 + threadIdx.x) : 0ull;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {  // wave 0: the member base of each word
+      const uint64_t m = lane < US_CHUNK ? s_word[lane] : 0ull;
       const int pc = __popcll(m);
       const int inc = wave_incl_scan(pc);
-      if (lane < US_CHUNK) {
-        s_word[lane] = m;
-        s_wbase[lane] = inc - pc;
-      }
+      if (lane < US_CHUNK) s_wbase[lane] = inc - pc;
       if (lane == US_CHUNK - 1) s_wbase[US_CHUNK] = inc;
     }
     __syncthreads();
@@ -1064,7 +1075,7 @@ __global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
       const uint64_t m = s_word[j];
       if ((m >> bit) & 1ull) {
         const int r = s_wbase[j] + __popcll(m & ((1ull << bit) - 1));
-        const int t = tok_in[64 * (c0 + j) + bit];
+        const int t = first ? tok0 : tok_in[64 * (c0 + j) + bit];
         s_tok[r] = t;
         if (base + r < cap_out) tok_out[base + r] = t;
       }

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import decode as od
-from seoulkv_amd import SeoulKV4, SeoulKV4Config, _hip
+from seoulkv_amd import SeoulKV4, SeoulKV4Config, SeoulKV4Index, _hip
 from tests.helpers import bits, case, cosine, oracle_step
 
 pytestmark = pytest.mark.gpu
@@ -192,5 +192,48 @@ def test_time_kernel_keeps_the_step_consistent():
         assert torch.equal(rt.debug_ids(), ids)
         with pytest.raises(RuntimeError):
             rt.time_kernel(n, reps=1)
+    finally:
+        rt.close()
+
+
+def test_index_built_on_the_gpu():
+    """SeoulKV4Index.build(build_device="cuda") clusters with the same torch
+    code on the GPU: the cells pass the index invariants, every token is
+    listed exactly twice (spill 2), and the decode step on that index is
+    bit-exact against the oracle run on the same cells."""
+    from oracle import decode as od
+    from seoulkv_amd.synthetic import make_cache
+    from tests.helpers import bits, cosine
+
+    k, v, qs = make_cache(8192, 256, clustered=True, seed_k=4321, seed_v=4322, seed_q=4323,
+                          n_queries=1)
+    print("[gpu] index build on cuda:0", flush=True)
+    index = SeoulKV4Index.build(k, v, nprobe=64, n_centroids=512, build_device="cuda:0")
+    zones = index.zones
+    retrieval = np.arange(zones.sink, zones.local_begin)
+    for cell in index.cells:
+        values = cell["values"].numpy()
+        assert cell["upper"].device.type == "cpu"
+        counts = np.bincount(values, minlength=zones.local_begin)
+        assert np.all(counts[retrieval] == 2)
+        assert counts[: zones.sink].sum() == 0
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    try:
+        rt.bind_query(qs[0])
+        rt.enqueue()
+        status = rt.synchronize()
+        assert status["err"] == [0, 0, 0, 0]
+        cells = [od.GroupCell.from_cell(c) for c in index.cells]
+        code8, scales = od.key_codec(bits(k))
+        k8, v8 = od.fp8_records(bits(k), bits(v))
+        traces, out = od.decode_step(cells, code8, scales, k8, v8,
+                                     bits(qs[0]).reshape(16, 256), sink=zones.sink,
+                                     local=zones.local)
+        for g, tr in enumerate(traces):
+            np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected)
+            np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
+        got = rt.read_output().float().numpy().reshape(16, 256)
+        for j in range(16):
+            assert cosine(got[j], out[j]) >= 0.999
     finally:
         rt.close()
