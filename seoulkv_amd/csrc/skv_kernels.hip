@@ -47,8 +47,42 @@ struct QPrepScratch {
   int X[H][D];
 };
 
+__device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out, int h,
+                          int lane);
+
+// Fixed-point operand of query variant v for KV group g (waves 0..3 form
+// one head each, then the whole block writes the B image).
 __device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out) {
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+  if (h < H) prep_head(a, g, v, s, out, h, lane);
+  __syncthreads();
+  // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
+  // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.
+  for (int w = threadIdx.x; w < 4 * WAVE * 4; w += blockDim.x) {
+    const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
+    const int col = l & 15, hh = col >> 2, limb = col & 3;
+    const int4 x4 = *reinterpret_cast<const int4*>(&s.X[hh][(l >> 4) * 64 + kc * 16 + 4 * m]);
+    const int xs[4] = {x4.x, x4.y, x4.z, x4.w};
+    uint32_t word = 0;
+#pragma unroll
+    for (int byte = 0; byte < 4; ++byte) {
+      const int x = xs[byte];
+      const int l0 = (int)(int8_t)(x & 0xff);
+      const int x1 = (x - l0) >> 8;
+      const int l1 = (int)(int8_t)(x1 & 0xff);
+      const int l2 = (x1 - l1) >> 8;
+      const int limbv = limb == 0 ? l0 : limb == 1 ? l1 : limb == 2 ? l2 : 0;
+      word |= (uint32_t)(limbv & 0xff) << (8 * byte);
+    }
+    out->bimg[kc][l][m] = word;
+  }
+  __syncthreads();
+}
+
+// One wave per head: the integers X, their sum, the scale exponent and
+// ||q|| lambda (raw variant) of query head 4g + h.
+__device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out, int h,
+                          int lane) {
   const uint2 qw = *reinterpret_cast<const uint2*>(a.q + (g * H + h) * D + 4 * lane);
   const uint32_t qb[4] = {qw.x & 0xffffu, qw.x >> 16, qw.y & 0xffffu, qw.y >> 16};
   uint32_t bits[4];
@@ -98,30 +132,6 @@ __device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, Q
       out->norm[h] = 0.f;
     }
   }
-  __syncthreads();
-  // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
-  // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int w = threadIdx.x + 256 * i;  // 0..1023
-    const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
-    const int col = l & 15, hh = col >> 2, limb = col & 3;
-    const int4 x4 = *reinterpret_cast<const int4*>(&s.X[hh][(l >> 4) * 64 + kc * 16 + 4 * m]);
-    const int xs[4] = {x4.x, x4.y, x4.z, x4.w};
-    uint32_t word = 0;
-#pragma unroll
-    for (int byte = 0; byte < 4; ++byte) {
-      const int x = xs[byte];
-      const int l0 = (int)(int8_t)(x & 0xff);
-      const int x1 = (x - l0) >> 8;
-      const int l1 = (int)(int8_t)(x1 & 0xff);
-      const int l2 = (x1 - l1) >> 8;
-      const int limbv = limb == 0 ? l0 : limb == 1 ? l1 : limb == 2 ? l2 : 0;
-      word |= (uint32_t)(limbv & 0xff) << (8 * byte);
-    }
-    out->bimg[kc][l][m] = word;
-  }
-  __syncthreads();
 }
 
 // Load the 16-register B operand of a query variant for this lane.
@@ -282,6 +292,10 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 }
 
 // ============================================================ front
+constexpr int FR_BLOCK = 256;   // front: one 16-centroid tile per wave
+constexpr int FR_WAVES = FR_BLOCK / WAVE;
+constexpr int FR_CENTROIDS = 16 * FR_WAVES;
+
 // One wave tile = 16 centroids x 4 heads.  Every block first forms the raw
 // query operand of its group in LDS (its centroid-plane loads are already in
 // flight), then per centroid and head:
@@ -292,12 +306,12 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 // Block 0 of each group also publishes the raw operand and clears the
 // group's per-step state; two extra blocks per group publish the q15 / qs
 // operands for the later kernels.
-__global__ __launch_bounds__(256) void k_front(StepArgs a) {
+__global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   SKV_TSB(4, 0);
   SKV_TS(0, 0);
   const int g = blockIdx.y, nc = a.nc;
   __shared__ __align__(16) QPrepScratch sp;
-  const int tiles_blocks = (nc + 63) / 64;
+  const int tiles_blocks = (nc + FR_CENTROIDS - 1) / FR_CENTROIDS;
   if ((int)blockIdx.x >= tiles_blocks) {
     const int v = QV_Q15 + (blockIdx.x - tiles_blocks);
     prep_operand(a, g, v, sp, &a.qop[g * QV_COUNT + v]);
@@ -305,7 +319,7 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
   const bool has = tile * 16 < nc;
   const int row = lane & 15, kb = lane >> 4;
   uint4 wu = make_uint4(0, 0, 0, 0), wl = make_uint4(0, 0, 0, 0);
@@ -326,7 +340,7 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
   }
   if (blockIdx.x == 0) {  // per-step state of the group
     uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
-    for (int i = threadIdx.x; i < nc / 32; i += 256) bm[i] = 0;
+    for (int i = threadIdx.x; i < nc / 32; i += FR_BLOCK) bm[i] = 0;
     if (threadIdx.x == 0) {
       a.status[g * ST_WORDS + ST_FULLSEL] = 0;
       a.status[g * ST_WORDS + ST_ERR] = 0;
@@ -384,7 +398,7 @@ __global__ __launch_bounds__(256) void k_front(StepArgs a) {
   if (blockIdx.x == 0) {  // publish the raw operand (a copy of sq)
     const uint32_t* src = reinterpret_cast<const uint32_t*>(&sq);
     uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + QV_RAW]);
-    for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += 256) dst[i] = src[i];
+    for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += FR_BLOCK) dst[i] = src[i];
   }
   SKV_TSE(4);
 }
@@ -1314,11 +1328,11 @@ const char* const kKernelNames[N_STEP_KERNELS] = {
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
 // ev[N_STEP_KERNELS] after the last one.
 void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) {
-  const int tiles_blocks = (a.nc + 63) / 64;
+  const int tiles_blocks = (a.nc + FR_CENTROIDS - 1) / FR_CENTROIDS;
   const size_t bm_lds = (size_t)(a.nc / 32) * 4;
   switch (k) {
     case 0:
-      hipLaunchKernelGGL(k_front, dim3(tiles_blocks + 2, G), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(k_front, dim3(tiles_blocks + 2, G), dim3(FR_BLOCK), 0, st, a);
       break;
     case 1:
       hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),

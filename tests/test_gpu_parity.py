@@ -25,6 +25,9 @@ CASES = {
     "t8192_iid_p128": dict(context=8192, components=1, nc=512, nprobe=128, clustered=False),
     "t8192_p16_sink0": dict(context=8192, components=64, nc=256, nprobe=16, sink=0, local=64),
     "t16384_nc1024_p256": dict(context=16384, components=512, nc=1024, nprobe=256, seed_shift=7),
+    # sizes that are not multiples of 64: context, sink, local, centroids
+    "t8200_nc160_odd": dict(context=8200, components=64, nc=160, nprobe=32, sink=40, local=200,
+                            seed_shift=3),
 }
 
 
