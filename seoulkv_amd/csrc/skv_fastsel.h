@@ -54,7 +54,10 @@ struct FastScratch {
   int scan[SEL_WAVES + 1];
 };
 
-__device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40); }
+// Candidate key: ordered score (bits 40..55) | position (bits 0..19); a key
+// tied at the k-th score also carries its ID (bits 20..39, flag bit 56).
+constexpr uint64_t CAND_HAS_ID = 1ull << 56;
+__device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40) & 0xffffu; }
 __device__ __forceinline__ int cand_pos(uint64_t c) { return (int)(c & 0xfffffu); }
 
 struct FastResult {
@@ -71,7 +74,9 @@ __device__ __forceinline__ bool fs_member(const FastResult& r, uint64_t c, IdFn 
   if (o == 0) return false;
   if (r.sel.all || o > r.sel.v) return true;
   if (o < r.sel.v) return false;
-  return r.sel.idcut == 0xffffffffu || id(cand_pos(c)) <= r.sel.idcut;
+  if (r.sel.idcut == 0xffffffffu) return true;
+  const uint32_t cid = (c & CAND_HAS_ID) ? (uint32_t)(c >> 20) & 0xfffffu : id(cand_pos(c));
+  return cid <= r.sel.idcut;
 }
 
 // Score sources: at(i) = ordered score of item i; oct(o) = the 8 ordered
@@ -315,6 +320,15 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
     return res;
   }
   SKV_TS(ts, 4);
+  // the candidates' IDs, needed only for ties at the k-th score: loaded now
+  // so that they arrive while that score is found
+  constexpr int CPT = CAND_CAP / SEL_BLOCK;  // candidates per thread
+  uint32_t pid[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = (int)threadIdx.x + u * SEL_BLOCK;
+    pid[u] = (!VALUE_ONLY && c < nc) ? id(cand_pos(s.cand[c])) : 0u;
+  }
   // ---- 3. exact k-th score among the candidates (nc >= k here)
   const uint32_t maxo = (uint32_t)s.maxo;
   int shift = 0;
@@ -354,11 +368,18 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   const int need = k - above;
   if (VALUE_ONLY || need >= ties) return res;  // every tie is a member
 
-  // ---- ties at v: the `need` lowest IDs win
+  // ---- ties at v: the `need` lowest IDs win (tied keys keep their ID for
+  // fs_member)
   if (ties <= FS_TIE_RANK) {
-    for (int c = threadIdx.x; c < nc; c += SEL_BLOCK) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = (int)threadIdx.x + u * SEL_BLOCK;
+      if (c >= nc) break;
       const uint64_t key = s.cand[c];
-      if (cand_ord(key) == v) s.tie[atomicAdd(&s.ntie, 1)] = id(cand_pos(key));
+      if (cand_ord(key) == v) {
+        s.tie[atomicAdd(&s.ntie, 1)] = pid[u];
+        s.cand[c] = key | CAND_HAS_ID | ((uint64_t)pid[u] << 20);
+      }
     }
     __syncthreads();
     if ((int)threadIdx.x < ties) {  // rank = number of smaller tied IDs

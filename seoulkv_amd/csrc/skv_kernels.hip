@@ -918,15 +918,20 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   }
   if (t.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    // the member bitmap: in LDS beside the scratch (cleared before the
+    // selection) when it fits, else in place
+    const int words = (n + 63) / 64;
+    const bool local = words <= TOPK_LDS_WORDS;
+    uint64_t* mb = local ? reinterpret_cast<uint64_t*>(dyn + sizeof(FastScratch)) : bm;
+    if (local)
+      for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
     const FastResult r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
     if (r.ok) {
       SKV_TS(ts, 6);
-      const int words = (n + 63) / 64;
-      // the histogram space is free after the selection: 2048 bitmap words
-      const bool local = words <= 2048;
-      uint64_t* mb = local ? reinterpret_cast<uint64_t*>(fs.hist) : bm;
-      for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
-      __syncthreads();
+      if (!local) {
+        for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
+        __syncthreads();
+      }
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
         if (fs_member(r, key, id)) {

@@ -506,8 +506,9 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   // the sink/local blocks, whichever is largest (they are never live together).
   const size_t fs_bytes = sizeof(FastScratch);
   w.select_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES});
-  w.top_u1_lds = std::max(fs_bytes, (size_t)w.top_u1.lds_items * 2);
-  w.top_u2_lds = std::max(fs_bytes, (size_t)w.top_u2.lds_items * 2);
+  const size_t topk_bytes = fs_bytes + (size_t)TOPK_LDS_WORDS * 8;  // + member bitmap
+  w.top_u1_lds = std::max(topk_bytes, (size_t)w.top_u1.lds_items * 2);
+  w.top_u2_lds = std::max(topk_bytes, (size_t)w.top_u2.lds_items * 2);
 
   if (hipHostMalloc((void**)&h->q_host, 16 * D * 2, hipHostMallocDefault) != hipSuccess ||
       hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess) {

@@ -130,6 +130,9 @@ constexpr int ATTN_WAVES = 16;
 constexpr size_t ATTN_SCRATCH_BYTES = (size_t)ATTN_WAVES * (2 + D) * 4;
 constexpr int DENSE_SLICE_KEYS = ATTN_WAVES * 16;
 
+// member-bitmap words the top-k kernel keeps in LDS beside its scratch
+constexpr int TOPK_LDS_WORDS = 2048;
+
 constexpr int N_STEP_KERNELS = 9;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
