@@ -38,7 +38,9 @@ enum {
   SKV_ENOMEM = 3,          /* device allocation failed */
   SKV_EPOOL_OVERFLOW = 4,  /* candidate pool above capacity (reference ingest err 4) */
   SKV_EPOOL_UNDERFLOW = 5, /* candidate pool below 2048 (reference ingest err 5) */
-  SKV_ESTATE = 6           /* call out of order / handle closed */
+  SKV_ESTATE = 6,          /* call out of order / handle closed */
+  SKV_EPOOL_WAIT = 7       /* device status only: the pool kernel abandoned a bounded
+                              wait for an earlier centroid range (never expected) */
 };
 
 /* One index cell (KV head) as produced by SeoulKV4Index
@@ -88,7 +90,7 @@ int skv_enqueue(void *handle);
 /* Reference synchronize (api.py:112-115).  Waits for the stream and, if
  * status is non-NULL, stores the per-group device status words [4][8]:
  * 0 pool size, 1 error code (0, 4 pool above capacity, 5 pool below the
- * minimum), 2 selected clusters, 3 coarse survivors, 4 |U1|, 5 |U2|,
+ * minimum, 7 pool kernel wait abandoned), 2 selected clusters, 3 coarse survivors, 4 |U1|, 5 |U2|,
  * 6 postings scanned, 7 full-selection bits (see skv_select_mode). */
 int skv_sync(void *handle, int32_t *status);
 

@@ -28,7 +28,8 @@ STAGES = {
 }
 STATUS_FIELDS = ("pool", "err", "selected", "survivors", "u1", "u2", "scanned", "full_select")
 ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "out of device memory",
-          4: "pool above capacity", 5: "pool below minimum", 6: "invalid state"}
+          4: "pool above capacity", 5: "pool below minimum", 6: "invalid state",
+          7: "pool kernel wait abandoned"}
 
 
 class CellDesc(ctypes.Structure):

@@ -8,9 +8,10 @@
 //   select      per head: the P-th largest lower bound, then the top-P fine
 //               scores among centroids whose upper bound reaches it ->
 //               selected bitmap (union); extra blocks: sink/local attention
-//   pool_count  survivor masks; per selected cluster and 64-posting chunk:
-//               postings owned under the spill-2 mate rule
-//   pool_emit   selected list + pool tokens in encounter order
+//               and the q15 / qs operands
+//   pool        survivor masks; postings owned under the spill-2 mate rule;
+//               selected list + pool tokens in encounter order (one pass,
+//               decoupled look-back over the centroid ranges)
 //   score2      2-bit scores of the pool
 //   top1600     per head: top-1600 of the pool -> membership bitmap
 //   union_score4  U1 = union over heads in pool order + 4-bit scores of U1
@@ -304,20 +305,13 @@ constexpr int FR_CENTROIDS = 16 * FR_WAVES;
 //   fine    bf16(RNE(sum q (2 code4 - 15)) * group_fine_scale)  (ordered;
 //           eligibility is applied by the selection kernel)
 // Block 0 of each group also publishes the raw operand and clears the
-// group's per-step state; two extra blocks per group publish the q15 / qs
-// operands for the later kernels.
+// group's per-step state (the q15 / qs operands of the later kernels are
+// formed by extra blocks of the selection launch).
 __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   SKV_TSB(4, 0);
   SKV_TS(0, 0);
   const int g = blockIdx.y, nc = a.nc;
   __shared__ __align__(16) QPrepScratch sp;
-  const int tiles_blocks = (nc + FR_CENTROIDS - 1) / FR_CENTROIDS;
-  if ((int)blockIdx.x >= tiles_blocks) {
-    const int v = QV_Q15 + (blockIdx.x - tiles_blocks);
-    prep_operand(a, g, v, sp, &a.qop[g * QV_COUNT + v]);
-    SKV_TSE(4);
-    return;
-  }
   const int lane = threadIdx.x & 63;
   const int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
   const bool has = tile * 16 < nc;
@@ -446,6 +440,13 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   SKV_TSB(5, 0);
   SKV_TS(2, 0);
   extern __shared__ __align__(16) unsigned char dyn[];
+  const int n_dense = G * H * a.dense_slices;
+  if ((int)blockIdx.x >= G * H + n_dense) {  // the q15 / qs operands of the later scorers
+    const int i = blockIdx.x - G * H - n_dense, g = i / 2, v = QV_Q15 + i % 2;
+    prep_operand(a, g, v, *reinterpret_cast<QPrepScratch*>(dyn), &a.qop[g * QV_COUNT + v]);
+    SKV_TSE(5);
+    return;
+  }
   if (blockIdx.x >= G * H) {  // sink/local attention slices (depend only on Q)
     dense_attend(a, blockIdx.x - G * H, *reinterpret_cast<AttnScratch*>(dyn));
     SKV_TSE(5);
@@ -557,7 +558,7 @@ constexpr unsigned long long LB_P = 2ull << 62;  // counts of all ranges up to t
 constexpr int LB_SEL = 23, LB_SURV = 40, LB_EPOCH = 57;
 constexpr unsigned long long LB_VAL = (1ull << LB_EPOCH) - 1;
 constexpr unsigned LB_EPOCHS = 32;
-constexpr int LB_SPIN_MAX = 1 << 22;  // polls before a wait is abandoned (ST_ERR 6)
+constexpr int LB_SPIN_MAX = 1 << 22;  // polls before a wait is abandoned (SKV_EPOOL_WAIT)
 constexpr int LB_WIN = 4;             // 64-range windows read per poll
 __device__ __forceinline__ int lb_field(unsigned long long v, int shift, int bits) {
   return (int)((v >> shift) & ((1ull << bits) - 1));
@@ -706,7 +707,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
       }
       if (wait) {  // a needed range has not published yet
         if (++spins > LB_SPIN_MAX) {
-          if (lane == 0) a.status[g * ST_WORDS + ST_ERR] = 6;
+          if (lane == 0) a.status[g * ST_WORDS + ST_ERR] = SKV_EPOOL_WAIT;
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -1337,10 +1338,10 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
   const size_t bm_lds = (size_t)(a.nc / 32) * 4;
   switch (k) {
     case 0:
-      hipLaunchKernelGGL(k_front, dim3(tiles_blocks + 2, G), dim3(FR_BLOCK), 0, st, a);
+      hipLaunchKernelGGL(k_front, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a);
       break;
     case 1:
-      hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices)), dim3(SEL_BLOCK),
+      hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
                          w.select_lds, st, a);
       break;
     case 2:

@@ -7,9 +7,9 @@
 //   k_select         _kernels/stage1_coarse/seoulkv4_coarse_select.py:297-310 (threshold);
 //                    codegen/fine.py:1848-1861 (head masks),
 //                    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73 (top-P union)
-//   k_pool_count     _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379 (survivor
-//                    masks); codegen/stage15.py:275-345 (mate-ownership dedup)
-//   k_pool_emit      codegen/stage15.py:275-345 (encounter-order pool)
+//   k_pool           _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379 (survivor
+//                    masks); codegen/stage15.py:275-345 (mate-ownership dedup,
+//                    encounter-order pool)
 //   k_score2         codegen/stage15.py:886-995 (2-bit scores)
 //   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
 //   k_union_score<4> codegen/stage15.py:1519-1597 (U1) +
@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/seoulkv4_hip.h"
 #include "skv_device.h"
 
 namespace skv {
@@ -31,7 +32,7 @@ namespace skv {
 // status words per KV group
 enum {
   ST_POOL = 0,     // pool size (clamped to the buffer)
-  ST_ERR = 1,      // 0 ok, 4 pool above capacity, 5 pool below minimum
+  ST_ERR = 1,      // 0 ok, else an SKV_EPOOL_* code (include/seoulkv4_hip.h)
   ST_SEL = 2,      // selected clusters
   ST_SURV = 3,     // coarse survivors
   ST_U1 = 4,       // |U1|
