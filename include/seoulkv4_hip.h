@@ -105,6 +105,21 @@ int skv_read_output(void *handle, uint16_t *host_out);
  * [4 groups][4 heads][100], best first. */
 int skv_debug_ids(void *handle, uint32_t *host_out);
 
+/* Dense FP8 decode (a comparison path with no counterpart in the reference,
+ * whose published comparison is TTNN's dense FlashDecode, README.md:7):
+ * softmax attention of the bound query's 16 heads over all T keys, from the
+ * same FP8 [V || K] records as the sparse step (scale 1/16, FP32
+ * accumulation), into its own [16][256] BF16 output.  Enqueued on the
+ * handle's stream; skv_read_dense_output syncs and copies. */
+int skv_dense_decode(void *handle);
+int skv_dense_output_device(void *handle, void **dev_ptr);
+int skv_read_dense_output(void *handle, uint16_t *host_out);
+
+/* Mean milliseconds per launch over `reps` back-to-back launches of
+ * mean_ms[0] the dense partial kernel, mean_ms[1] its merge kernel and
+ * mean_ms[2] both (one dense decode).  Needs one skv_dense_decode first. */
+int skv_time_dense(void *handle, int reps, float *mean_ms);
+
 /* Stage outputs for parity checks (sync + copy).  stage is one of SKV_STAGE_*;
  * copies at most cap elements for one KV group, stores the element count. */
 enum {
@@ -150,7 +165,7 @@ int skv_select_mode(void *handle, int exact);
 /* Launch mode (no counterpart in the reference, whose programs are enqueued
  * by TT-Metal): enable = 1 captures the step's kernels into a HIP graph on
  * the next skv_enqueue and replays it with one host call per step; 0 (the
- * default) launches the 10 kernels one by one.  The graph saves host time
+ * default) launches the step's kernels one by one.  The graph saves host time
  * but, measured on MI355X with ROCm 7.2, consecutive graph launches leave
  * ~8 us of device idle between them, so back-to-back steps run slower.
  * Per-kernel profiling (skv_profile) always launches one by one.  Results

@@ -88,6 +88,10 @@ def load_library() -> ctypes.CDLL:
         "skv_select_mode": (i32, [vp, i32]),
         "skv_graph_mode": (i32, [vp, i32]),
         "skv_time_kernel": (i32, [vp, i32, i32, vp]),
+        "skv_dense_decode": (i32, [vp]),
+        "skv_dense_output_device": (i32, [vp, ctypes.POINTER(vp)]),
+        "skv_read_dense_output": (i32, [vp, vp]),
+        "skv_time_dense": (i32, [vp, i32, vp]),
         "skv_profile_read": (i32, [vp, vp, i32, vp]),
         "skv_kernel_count": (i32, []),
         "skv_kernel_name": (ctypes.c_char_p, [i32]),
@@ -236,6 +240,23 @@ class Runtime:
         p = ctypes.c_void_p()
         self._check(self.lib.skv_output_device(self.handle, ctypes.byref(p)), "output")
         return int(p.value)
+
+    def dense_decode(self) -> None:
+        """Enqueue the dense FP8 decode of the bound query over all T keys
+        (the comparison path; its output is separate from the step's)."""
+        self._check(self.lib.skv_dense_decode(self.handle), "dense_decode")
+
+    def read_dense_output(self) -> torch.Tensor:
+        out = np.zeros((16, D), dtype=np.uint16)
+        self._check(self.lib.skv_read_dense_output(self.handle, _ptr(out)), "read_dense_output")
+        return torch.from_numpy(out.view(np.int16)).view(torch.bfloat16).reshape(1, 1, 16, D)
+
+    def time_dense(self, reps: int = 50) -> tuple[float, float, float]:
+        """Mean milliseconds per launch of the dense partial kernel, its merge
+        kernel and the pair, each over ``reps`` back-to-back launches."""
+        ms = np.zeros(3, dtype=np.float32)
+        self._check(self.lib.skv_time_dense(self.handle, int(reps), _ptr(ms)), "time_dense")
+        return float(ms[0]), float(ms[1]), float(ms[2])
 
     def debug_ids(self) -> torch.Tensor:
         out = np.zeros((G, H, TOPK), dtype=np.uint32)

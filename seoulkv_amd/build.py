@@ -16,7 +16,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libseoulkv4_hip.so"
-SOURCES = ["skv_runtime.hip", "skv_kernels.hip"]
+SOURCES = ["skv_runtime.hip", "skv_kernels.hip", "skv_dense.hip"]
 ARCH = os.environ.get("SKV_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [

@@ -94,6 +94,14 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
 
 __device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+// Four FP8 e4m3 values -> FP32 with the gfx950 converter (OCP e4m3fn; exact).
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
+}
+
 // RNE_f32(Dv * 2^e) for |Dv| < 2^53.
 __device__ __forceinline__ float scaled_f32(int64_t Dv, int e) {
   return __double2float_rn(ldexp((double)Dv, e));

@@ -157,14 +157,6 @@ static_assert(U2_MAX <= OCT_ITEMS && U1_MAX <= OCT_ITEMS, "unions fit the regist
 static_assert(DENSE_BLOCK_KEYS == DENSE_SLICE_KEYS && SEL_BLOCK / WAVE == ATTN_WAVES,
               "attention slices follow the selection block size");
 
-// Four FP8 e4m3 values -> FP32 with the gfx950 converter (OCP e4m3fn; exact).
-__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
-  typedef float v2f __attribute__((ext_vector_type(2)));
-  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
-}
-
 __device__ __forceinline__ void load_q4(const StepArgs& a, int j, float q[4]) {
   const int lane = threadIdx.x & 63;
   const uint2 qw = *reinterpret_cast<const uint2*>(a.q + j * D + 4 * lane);

@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "../../include/seoulkv4_hip.h"
+#include "skv_dense.h"
 #include "skv_device.h"
 #include "skv_fastsel.h"
 #include "skv_select.h"
@@ -56,6 +57,8 @@ struct Handle {
   size_t static_bytes = 0, work_bytes = 0;
   StepArgs a{};
   StepWork w{};
+  DenseArgs dn{};  // dense FP8 decode over every key (comparison path)
+  bool dense_ran = false;
   bool bound = false, ran = false;
   size_t lds_per_block = 0;
   // per-kernel event timing (skv_profile)
@@ -339,6 +342,12 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   // predecessor), at least 64 centroids per range
   a.pool_range = std::max(64, (nc / 128 + 31) / 32 * 32);
   a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
+  h->dn.T = T;
+  dense_shape(T, h->dn.iters, h->dn.nb);
+  if (h->dn.nb > DN_TARGET_BLOCKS) {  // the merge kernel holds at most this many partials
+    fail(h, SKV_EINVAL, "dense decode shape: %d blocks per group", h->dn.nb);
+    return bail(SKV_EINVAL);
+  }
 
   // ---- static arena
   Arena s;
@@ -394,6 +403,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.out = (uint16_t*)ar.take(16 * D * 2);
     a.bm_u1 = (uint64_t*)ar.take((size_t)G * H * words1 * 8);
     a.bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
+    h->dn.part = (float*)ar.take((size_t)G * h->dn.nb * H * (D + 2) * 4);
+    h->dn.out = (uint16_t*)ar.take(16 * D * 2);
   };
   plan_work(wk);
   h->work_bytes = wk.used;
@@ -404,6 +415,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   wk.base = (char*)h->work_mem;
   wk.used = 0;
   plan_work(wk);
+  h->dn.kv8 = a.kv8;
+  h->dn.q = a.q;
   if (hipMemsetAsync(h->work_mem, 0, h->work_bytes, h->stream) != hipSuccess) {
     fail(h, SKV_EHIP, "workspace clear failed");
     return bail(SKV_EHIP);
@@ -634,6 +647,63 @@ int skv_time_kernel(void* handle, int kernel, int reps, float* mean_ms) {
   // a full step restores every downstream buffer (query prep clears state)
   launch_step(h->a, h->w, h->stream, nullptr);
   HIPCHK(h, hipStreamSynchronize(h->stream));
+  return SKV_OK;
+}
+
+int skv_dense_decode(void* handle) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  if (!h->bound) return fail(h, SKV_ESTATE, "bind a query before the dense decode");
+  HIPCHK(h, hipSetDevice(h->device));
+  launch_dense(h->dn, h->stream, 0);
+  launch_dense(h->dn, h->stream, 1);
+  HIPCHK(h, hipGetLastError());
+  h->dense_ran = true;
+  return SKV_OK;
+}
+
+int skv_dense_output_device(void* handle, void** dev_ptr) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !dev_ptr) return SKV_EINVAL;
+  *dev_ptr = h->dn.out;
+  return SKV_OK;
+}
+
+int skv_read_dense_output(void* handle, uint16_t* host_out) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !host_out) return SKV_EINVAL;
+  if (!h->dense_ran) return fail(h, SKV_ESTATE, "no dense decode has run");
+  HIPCHK(h, hipStreamSynchronize(h->stream));
+  HIPCHK(h, hipMemcpy(host_out, h->dn.out, 16 * D * 2, hipMemcpyDeviceToHost));
+  return SKV_OK;
+}
+
+int skv_time_dense(void* handle, int reps, float* mean_ms) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h) return SKV_ESTATE;
+  if (reps < 1 || !mean_ms) return fail(h, SKV_EINVAL, "reps %d out of range", reps);
+  if (!h->dense_ran) return fail(h, SKV_ESTATE, "no dense decode has run");
+  hipEvent_t ev[4] = {};
+  for (hipEvent_t& e : ev) HIPCHK(h, hipEventCreate(&e));
+  // both kernels are functions of their inputs: repeats recompute the same
+  // partials and output
+  HIPCHK(h, hipEventRecord(ev[0], h->stream));
+  for (int r = 0; r < reps; ++r) launch_dense(h->dn, h->stream, 0);
+  HIPCHK(h, hipEventRecord(ev[1], h->stream));
+  for (int r = 0; r < reps; ++r) launch_dense(h->dn, h->stream, 1);
+  HIPCHK(h, hipEventRecord(ev[2], h->stream));
+  for (int r = 0; r < reps; ++r) {
+    launch_dense(h->dn, h->stream, 0);
+    launch_dense(h->dn, h->stream, 1);
+  }
+  HIPCHK(h, hipEventRecord(ev[3], h->stream));
+  HIPCHK(h, hipEventSynchronize(ev[3]));
+  for (int i = 0; i < 3; ++i) {
+    float ms = 0.f;
+    HIPCHK(h, hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+    mean_ms[i] = ms / (float)reps;
+  }
+  for (hipEvent_t e : ev) (void)hipEventDestroy(e);
   return SKV_OK;
 }
 
