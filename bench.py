@@ -5,8 +5,9 @@ One "step" is one ``SeoulKV4.run`` decode step (all 16 query heads of the 4 KV
 heads of one layer) with the query already resident on the device.  Prints one
 JSON line: µs per layer-step (device time, HIP events), the roofline of the
 dominant kernel, the step's algorithmic HBM bytes and GB/s, whether the
-top-100 IDs match the CPU oracle bit for bit, and the oracle's own CPU time on
-a bounded sample of the same workload.
+top-100 IDs match the CPU oracle bit for bit, the oracle's own CPU time on a
+bounded sample of the same workload, and the dense FP8 decode over all T keys
+on the same GPU (the sparse step's comparison).
 
     python bench.py [--steps K] [--warmup W] [--config cfg2] [--no-cpu-baseline]
 """
@@ -30,6 +31,7 @@ from seoulkv_amd import SeoulKV4, SeoulKV4Config, SeoulKV4Index  # noqa: E402
 from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+G_KV = 4  # KV heads of the layer
 METRIC = "µs/layer decode step at T=128K (1 GPU); achieved HBM GB/s; top-100 ID match"
 
 
@@ -114,6 +116,7 @@ def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
         t = time.perf_counter()
         od.dense_decode(kf, vf, qf)
         dt.append(time.perf_counter() - t)
+    dense_fp8 = od.dense_decode(k8, v8, qf)  # the GPU dense path's reference
     threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
     return {
         "value": statistics.median(times) * 1e6,
@@ -126,7 +129,7 @@ def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
             "top-k, FP8 SDPA), median; prefill untimed"
         ),
         "dense_fp32_us": statistics.median(dt) * 1e6,
-    }, match, out
+    }, match, out, dense_fp8
 
 
 def calibrate_copy(mib: int) -> int:
@@ -248,6 +251,12 @@ def main() -> int:
                     for i, name in enumerate(names)}
         attn.synchronize()
 
+        # the dense FP8 decode over all T keys, the sparse step's comparison
+        rt.dense_decode()
+        dense_gpu = rt.read_dense_output().float().numpy().reshape(16, 256)
+        dn_kernel_ms, dn_merge_ms, dn_ms = rt.time_dense(reps=max(20, args.steps // 4))
+        log(f"dense FP8 decode {dn_ms * 1e3:.1f} µs (partials {dn_kernel_ms * 1e3:.1f} µs)")
+
     nbytes = kernel_bytes(status, p, p.n_centroids)
     total_bytes = sum(nbytes.values())
     dominant = max(alone_ms, key=alone_ms.get)
@@ -263,14 +272,18 @@ def main() -> int:
 
     cpu = None
     match = None
+    dense_err = None
+    dense_bytes = G_KV * p.context * 512  # every FP8 [V || K] record once
     if not args.no_cpu_baseline:
-        cpu, match, out_ref = cpu_baseline(index, k, v, q, top_gpu, args.cpu_budget)
+        cpu, match, out_ref, dense_ref = cpu_baseline(index, k, v, q, top_gpu, args.cpu_budget)
         err = np.abs(out_gpu - out_ref).max()
         cos = min(
             float(out_gpu[j] @ out_ref[j] / (np.linalg.norm(out_gpu[j]) * np.linalg.norm(out_ref[j])))
             for j in range(16)
         )
         log(f"oracle: top-100 match {match:.4f}, output max-abs {err:.3g}, min cosine {cos:.6f}")
+        dense_err = float(np.abs(dense_gpu - dense_ref).max())
+        log(f"dense FP8 decode vs oracle: max-abs {dense_err:.3g}")
 
     result = {
         "metric": METRIC,
@@ -312,6 +325,17 @@ def main() -> int:
             "bytes_per_launch": int(nbytes.get(dominant, 0)),
         },
         "kernels": per_kernel,
+        "dense_fp8": {
+            "us": round(dn_ms * 1e3, 2),
+            "kernel_us": round(dn_kernel_ms * 1e3, 2),
+            "merge_us": round(dn_merge_ms * 1e3, 2),
+            "bytes": int(dense_bytes),
+            "GB/s": round(dense_bytes / (dn_kernel_ms * 1e-3) / 1e9, 1),
+            "frac": round(dense_bytes / (dn_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("dense_fp8"),
+            "max_abs_vs_oracle": dense_err,
+            "sparse_over_dense": round(ms_per_step / dn_ms, 3),
+        },
         "profiled_steps": n_prof,
         "stage_sizes": {k_: status[k_] for k_ in ("survivors", "selected", "pool", "u1", "u2")},
         "cpu_baseline": cpu,

@@ -320,15 +320,6 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
     return res;
   }
   SKV_TS(ts, 4);
-  // the candidates' IDs, needed only for ties at the k-th score: loaded now
-  // so that they arrive while that score is found
-  constexpr int CPT = CAND_CAP / SEL_BLOCK;  // candidates per thread
-  uint32_t pid[CPT];
-#pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    const int c = (int)threadIdx.x + u * SEL_BLOCK;
-    pid[u] = (!VALUE_ONLY && c < nc) ? id(cand_pos(s.cand[c])) : 0u;
-  }
   // ---- 3. exact k-th score among the candidates (nc >= k here)
   const uint32_t maxo = (uint32_t)s.maxo;
   int shift = 0;
@@ -343,6 +334,19 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   __syncthreads();
   const int b2 = s.sel[0];
   int above = s.sel[1];
+  // the IDs of the candidates in the k-th score's bin (the only possible
+  // ties), loaded now so that they arrive while the score itself is found
+  constexpr int CPT = CAND_CAP / SEL_BLOCK;  // candidates per thread
+  uint32_t pid[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = (int)threadIdx.x + u * SEL_BLOCK;
+    pid[u] = 0u;
+    if (!VALUE_ONLY && c < nc) {
+      const uint64_t key = s.cand[c];
+      if ((int)((cand_ord(key) - cut) >> shift) == b2) pid[u] = id(cand_pos(key));
+    }
+  }
   uint32_t v;
   int ties;
   if (shift == 0) {
