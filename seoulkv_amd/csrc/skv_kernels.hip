@@ -24,6 +24,8 @@
 // Selection keys are (ordered BF16 score, lowest ID first); all score dots
 // are exact integers on the int8 matrix cores (see skv_device.h).
 
+#include <algorithm>
+
 #include "skv_device.h"
 #include "skv_fastsel.h"
 #include "skv_octsel.h"
@@ -288,6 +290,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 constexpr int FR_BLOCK = 256;   // front: one 16-centroid tile per wave
 constexpr int FR_WAVES = FR_BLOCK / WAVE;
 constexpr int FR_CENTROIDS = 16 * FR_WAVES;
+constexpr int FR_MAX_BLOCKS = 256;  // front blocks per group (each loops over its tiles)
 
 // One wave tile = 16 centroids x 4 heads.  Every block first forms the raw
 // query operand of its group in LDS (its centroid-plane loads are already in
@@ -299,31 +302,94 @@ constexpr int FR_CENTROIDS = 16 * FR_WAVES;
 // Block 0 of each group also publishes the raw operand and clears the
 // group's per-step state (the q15 / qs operands of the later kernels are
 // formed by extra blocks of the selection launch).
+// Loads of one 16-centroid tile for one wave: the two planes (lane row
+// l % 16, dims (l / 16) * 16 ..) and the per-centroid factors of the lane's
+// output centroids c0 .. c0 + 3 (one 32-centroid block).
+struct FrTile {
+  uint4 wu, wl;
+  float4 rs;
+  float sc4, gf;
+};
+
+__device__ __forceinline__ FrTile fr_load(const StepArgs& a, int g, int tile, int lane) {
+  const int nc = a.nc, row = lane & 15, kb = lane >> 4;
+  FrTile t;
+  t.wu = t.wl = make_uint4(0, 0, 0, 0);
+  t.rs = make_float4(0.f, 0.f, 0.f, 0.f);
+  t.sc4 = t.gf = 0.f;
+  if (tile * 16 < nc) {
+    const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
+    t.wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
+    t.wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
+    const int c0 = tile * 16 + 4 * kb;
+    if ((lane & 3) == 0) {
+      t.rs = *reinterpret_cast<const float4*>(a.resid + (size_t)g * nc + c0);
+      t.sc4 = a.scale4[(size_t)g * (nc / 32) + (c0 >> 5)];
+      t.gf = a.gfs[(size_t)g * (nc / 32) + (c0 >> 5)];
+    }
+  }
+  return t;
+}
+
+// Coarse bounds and fine scores of one tile's 16 centroids x 4 heads.
+__device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int lane, const FrTile& t,
+                                         const uint32_t (&b)[4][4], const QOperand& sq) {
+  const int nc = a.nc, kb = lane >> 4;
+  const uint32_t up[4] = {t.wu.x, t.wu.y, t.wu.z, t.wu.w};
+  const uint32_t lo[4] = {t.wl.x, t.wl.y, t.wl.z, t.wl.w};
+  v4i acc_c = {0, 0, 0, 0}, acc_f = {0, 0, 0, 0};
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) {
+    uint32_t eu[4], el[4], a4[4];
+    expand2(up[kc], eu);
+    expand2(lo[kc], el);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a4[m] = (eu[m] << 2) | el[m];
+    acc_c = mfma_i8(eu, b[kc], acc_c);
+    acc_f = mfma_i8(a4, b[kc], acc_f);
+  }
+  int64_t dc[4], df[4];
+  combine_limbs(acc_c, dc);
+  combine_limbs(acc_f, df);
+  if ((lane & 3) == 0) {
+    const int h = (lane & 15) >> 2;
+    const int64_t S = sq.sum[h];
+    const int fx = sq.fx[h];
+    const float norm = sq.norm[h];
+    const float res[4] = {t.rs.x, t.rs.y, t.rs.z, t.rs.w};
+    const int c0 = tile * 16 + 4 * kb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = c0 + r;
+      const float val = scaled_f32(2 * dc[r] - 3 * S, fx);
+      const float value = __fmul_rn(val, t.sc4);
+      const float margin = __fmul_rn(norm, res[r]);
+      const size_t o = ((size_t)g * H + h) * nc + c;
+      a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
+      a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
+      const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
+      const uint32_t fb = bf16_rne(__fmul_rn(fv, t.gf));
+      a.fine_ord[o] = (uint16_t)ordered16(fb);
+      if (a.debug) a.fine_bits[o] = (uint16_t)fb;
+    }
+  }
+}
+
+// Block (x, g) forms group g's fixed-point query operand once, then its
+// waves score 16-centroid tiles x*FR_WAVES + wave and, when LOOP (more tiles
+// than one pass of the grid covers), every FR_WAVES * gridDim.x tiles after
+// it, with the next tile's loads in flight while one is scored.
+template <bool LOOP>
 __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   SKV_TSB(4, 0);
   SKV_TS(0, 0);
   const int g = blockIdx.y, nc = a.nc;
   __shared__ __align__(16) QPrepScratch sp;
   const int lane = threadIdx.x & 63;
-  const int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
-  const bool has = tile * 16 < nc;
-  const int row = lane & 15, kb = lane >> 4;
-  uint4 wu = make_uint4(0, 0, 0, 0), wl = make_uint4(0, 0, 0, 0);
-  if (has) {
-    const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
-    wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
-    wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
-  }
-  // the per-centroid factors of this lane's output centroids c0 .. c0+3
-  // (one 32-centroid block), loaded with the planes
-  const int c0 = tile * 16 + 4 * kb;
-  float4 rs = make_float4(0.f, 0.f, 0.f, 0.f);
-  float sc4 = 0.f, gf = 0.f;
-  if (has && (lane & 3) == 0) {
-    rs = *reinterpret_cast<const float4*>(a.resid + (size_t)g * nc + c0);
-    sc4 = a.scale4[(size_t)g * (nc / 32) + (c0 >> 5)];
-    gf = a.gfs[(size_t)g * (nc / 32) + (c0 >> 5)];
-  }
+  const int ntiles = nc / 16;
+  const int step = FR_WAVES * (int)gridDim.x;
+  int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
+  FrTile cur = fr_load(a, g, tile, lane);
   if (blockIdx.x == 0) {  // per-step state of the group
     uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
     for (int i = threadIdx.x; i < nc / 32; i += FR_BLOCK) bm[i] = 0;
@@ -335,48 +401,23 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   __shared__ __align__(16) QOperand sq;
   prep_operand(a, g, QV_RAW, sp, &sq);
   SKV_TS(0, 1);
-  if (has) {
+  if (tile < ntiles) {
     uint32_t b[4][4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const uint4 w = *reinterpret_cast<const uint4*>(&sq.bimg[kc][lane][0]);
       b[kc][0] = w.x; b[kc][1] = w.y; b[kc][2] = w.z; b[kc][3] = w.w;
     }
-    const uint32_t up[4] = {wu.x, wu.y, wu.z, wu.w};
-    const uint32_t lo[4] = {wl.x, wl.y, wl.z, wl.w};
-    v4i acc_c = {0, 0, 0, 0}, acc_f = {0, 0, 0, 0};
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      uint32_t eu[4], el[4], a4[4];
-      expand2(up[kc], eu);
-      expand2(lo[kc], el);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) a4[m] = (eu[m] << 2) | el[m];
-      acc_c = mfma_i8(eu, b[kc], acc_c);
-      acc_f = mfma_i8(a4, b[kc], acc_f);
-    }
-    int64_t dc[4], df[4];
-    combine_limbs(acc_c, dc);
-    combine_limbs(acc_f, df);
-    if ((lane & 3) == 0) {
-      const int h = (lane & 15) >> 2;
-      const int64_t S = sq.sum[h];
-      const int fx = sq.fx[h];
-      const float norm = sq.norm[h];
-      const float res[4] = {rs.x, rs.y, rs.z, rs.w};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = c0 + r;
-        const float val = scaled_f32(2 * dc[r] - 3 * S, fx);
-        const float value = __fmul_rn(val, sc4);
-        const float margin = __fmul_rn(norm, res[r]);
-        const size_t o = ((size_t)g * H + h) * nc + c;
-        a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
-        a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
-        const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
-        const uint32_t fb = bf16_rne(__fmul_rn(fv, gf));
-        a.fine_ord[o] = (uint16_t)ordered16(fb);
-        if (a.debug) a.fine_bits[o] = (uint16_t)fb;
+    if (!LOOP) {
+      fr_score(a, g, tile, lane, cur, b, sq);
+    } else {
+      for (;;) {
+        const int next = tile + step;
+        const FrTile nxt = fr_load(a, g, next, lane);
+        fr_score(a, g, tile, lane, cur, b, sq);
+        if (next >= ntiles) break;
+        cur = nxt;
+        tile = next;
       }
     }
   }
@@ -1326,11 +1367,14 @@ const char* const kKernelNames[N_STEP_KERNELS] = {
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
 // ev[N_STEP_KERNELS] after the last one.
 void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) {
-  const int tiles_blocks = (a.nc + FR_CENTROIDS - 1) / FR_CENTROIDS;
+  const int tiles_blocks = std::min((a.nc + FR_CENTROIDS - 1) / FR_CENTROIDS, FR_MAX_BLOCKS);
   const size_t bm_lds = (size_t)(a.nc / 32) * 4;
   switch (k) {
     case 0:
-      hipLaunchKernelGGL(k_front, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a);
+      if (tiles_blocks * FR_CENTROIDS >= a.nc)
+        hipLaunchKernelGGL(k_front<false>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a);
+      else
+        hipLaunchKernelGGL(k_front<true>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a);
       break;
     case 1:
       hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
