@@ -51,13 +51,20 @@ struct QPrepScratch {
 };
 
 __device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out, int h,
-                          int lane);
+                          int lane, uint2 qw);
+
+// This lane's 4 BF16 query elements of head h of group g (dims 4 lane ..).
+__device__ __forceinline__ uint2 load_qw(const StepArgs& a, int g, int h, int lane) {
+  return *reinterpret_cast<const uint2*>(a.q + (g * H + h) * D + 4 * lane);
+}
 
 // Fixed-point operand of query variant v for KV group g (waves 0..3 form
-// one head each, then the whole block writes the B image).
-__device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out) {
+// one head each from qw, their lanes' query words, then the whole block
+// writes the B image).
+__device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out,
+                             uint2 qw) {
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
-  if (h < H) prep_head(a, g, v, s, out, h, lane);
+  if (h < H) prep_head(a, g, v, s, out, h, lane, qw);
   __syncthreads();
   // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
   // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.
@@ -85,8 +92,7 @@ __device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, Q
 // One wave per head: the integers X, their sum, the scale exponent and
 // ||q|| lambda (raw variant) of query head 4g + h.
 __device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out, int h,
-                          int lane) {
-  const uint2 qw = *reinterpret_cast<const uint2*>(a.q + (g * H + h) * D + 4 * lane);
+                          int lane, uint2 qw) {
   const uint32_t qb[4] = {qw.x & 0xffffu, qw.x >> 16, qw.y & 0xffffu, qw.y >> 16};
   uint32_t bits[4];
   if (v != QV_RAW) {
@@ -289,6 +295,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 // ============================================================ front
 constexpr int FR_BLOCK = 256;   // front: one 16-centroid tile per wave
 constexpr int FR_WAVES = FR_BLOCK / WAVE;
+static_assert(FR_WAVES == H, "front: wave w forms query head w");
 constexpr int FR_CENTROIDS = 16 * FR_WAVES;
 constexpr int FR_MAX_BLOCKS = 256;  // front blocks per group (each loops over its tiles)
 
@@ -311,23 +318,19 @@ struct FrTile {
   float sc4, gf;
 };
 
+// Branch-free (a tile past the end reloads the last one, unused), so the
+// compiler can wait for earlier loads while these are in flight.
 __device__ __forceinline__ FrTile fr_load(const StepArgs& a, int g, int tile, int lane) {
   const int nc = a.nc, row = lane & 15, kb = lane >> 4;
+  const int tt = min(tile, nc / 16 - 1);
   FrTile t;
-  t.wu = t.wl = make_uint4(0, 0, 0, 0);
-  t.rs = make_float4(0.f, 0.f, 0.f, 0.f);
-  t.sc4 = t.gf = 0.f;
-  if (tile * 16 < nc) {
-    const size_t rowoff = ((size_t)g * nc + tile * 16 + row) * 64 + kb * 16;
-    t.wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
-    t.wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
-    const int c0 = tile * 16 + 4 * kb;
-    if ((lane & 3) == 0) {
-      t.rs = *reinterpret_cast<const float4*>(a.resid + (size_t)g * nc + c0);
-      t.sc4 = a.scale4[(size_t)g * (nc / 32) + (c0 >> 5)];
-      t.gf = a.gfs[(size_t)g * (nc / 32) + (c0 >> 5)];
-    }
-  }
+  const size_t rowoff = ((size_t)g * nc + tt * 16 + row) * 64 + kb * 16;
+  t.wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
+  t.wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
+  const int c0 = tt * 16 + 4 * kb;
+  t.rs = *reinterpret_cast<const float4*>(a.resid + (size_t)g * nc + c0);
+  t.sc4 = a.scale4[(size_t)g * (nc / 32) + (c0 >> 5)];
+  t.gf = a.gfs[(size_t)g * (nc / 32) + (c0 >> 5)];
   return t;
 }
 
@@ -389,17 +392,13 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   const int ntiles = nc / 16;
   const int step = FR_WAVES * (int)gridDim.x;
   int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
+  // the query first: forming its operand then waits for it alone while the
+  // plane loads are still in flight (FR_WAVES == H: wave = head)
+  const uint2 qw = load_qw(a, g, threadIdx.x >> 6, lane);
+  __builtin_amdgcn_sched_barrier(0);  // keep the query load ahead of the tile's
   FrTile cur = fr_load(a, g, tile, lane);
-  if (blockIdx.x == 0) {  // per-step state of the group
-    uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
-    for (int i = threadIdx.x; i < nc / 32; i += FR_BLOCK) bm[i] = 0;
-    if (threadIdx.x == 0) {
-      a.status[g * ST_WORDS + ST_FULLSEL] = 0;
-      a.status[g * ST_WORDS + ST_ERR] = 0;
-    }
-  }
   __shared__ __align__(16) QOperand sq;
-  prep_operand(a, g, QV_RAW, sp, &sq);
+  prep_operand(a, g, QV_RAW, sp, &sq, qw);
   SKV_TS(0, 1);
   if (tile < ntiles) {
     uint32_t b[4][4];
@@ -422,6 +421,14 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
     }
   }
   SKV_TS(0, 2);
+  if (blockIdx.x == 0) {  // per-step state of the group (read by later kernels)
+    uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
+    for (int i = threadIdx.x; i < nc / 32; i += FR_BLOCK) bm[i] = 0;
+    if (threadIdx.x == 0) {
+      a.status[g * ST_WORDS + ST_FULLSEL] = 0;
+      a.status[g * ST_WORDS + ST_ERR] = 0;
+    }
+  }
   if (blockIdx.x == 0) {  // publish the raw operand (a copy of sq)
     const uint32_t* src = reinterpret_cast<const uint32_t*>(&sq);
     uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + QV_RAW]);
@@ -476,7 +483,9 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   const int n_dense = G * H * a.dense_slices;
   if ((int)blockIdx.x >= G * H + n_dense) {  // the q15 / qs operands of the later scorers
     const int i = blockIdx.x - G * H - n_dense, g = i / 2, v = QV_Q15 + i % 2;
-    prep_operand(a, g, v, *reinterpret_cast<QPrepScratch*>(dyn), &a.qop[g * QV_COUNT + v]);
+    const int hq = min((int)(threadIdx.x >> 6), H - 1);
+    prep_operand(a, g, v, *reinterpret_cast<QPrepScratch*>(dyn), &a.qop[g * QV_COUNT + v],
+                 load_qw(a, g, hq, threadIdx.x & 63));
     SKV_TSE(5);
     return;
   }
