@@ -634,13 +634,31 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   // below ends.  The launch epoch tags this launch's records.
   const int b = blockIdx.x, c0 = b * a.pool_range;
   const int ncr = min(a.pool_range, nc - c0);  // centroids of the range (a multiple of 32)
+  // every load of the prologue is issued before the first wait: the group's
+  // selected-cluster bitmap (<= 2048 words), the range's CSR offsets
+  // (<= 513), and its centroids' upper bounds and the thresholds
   const unsigned epoch = a.pool_epoch[g];
   const unsigned long long tag = (unsigned long long)(epoch % LB_EPOCHS) << LB_EPOCH;
-  {
-    const uint32_t* bm = a.selbm + (size_t)g * (nc / 32);
-    for (int i = t; i < nc / 32; i += PL_BLOCK) s_bm[i] = bm[i];
+  constexpr int BM_PER = 65536 / 32 / PL_BLOCK;
+  const int nbw = nc / 32;
+  const uint32_t* bm = a.selbm + (size_t)g * nbw;
+  const int* off = a.csr_off + (size_t)g * (nc + 1) + c0;
+  uint32_t bmw[BM_PER];
+#pragma unroll
+  for (int u = 0; u < BM_PER; ++u) bmw[u] = bm[min(t + u * PL_BLOCK, nbw - 1)];
+  const int off0 = off[min(t, ncr)], off1 = off[min(t + PL_BLOCK, ncr)];
+  const int cu = c0 + min(t, ncr - 1);
+  uint32_t upv[H], thv[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    upv[h] = a.upper[((size_t)g * H + h) * nc + cu];
+    thv[h] = a.thr[g * H + h];
   }
-  for (int i = t; i <= ncr; i += PL_BLOCK) s_off[i] = a.csr_off[(size_t)g * (nc + 1) + c0 + i];
+#pragma unroll
+  for (int u = 0; u < BM_PER; ++u)
+    if (t + u * PL_BLOCK < nbw) s_bm[t + u * PL_BLOCK] = bmw[u];
+  if (t <= ncr) s_off[t] = off0;
+  if (t + PL_BLOCK <= ncr) s_off[t + PL_BLOCK] = off1;
   if (t == 0) {
     s_surv = 0;
     s_scanned = 0;
@@ -648,11 +666,9 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   // survivor head masks (upper_h >= thr_h) of the range's centroids
   uint32_t m = 0;
   if (t < ncr) {
-    const int c = c0 + t;
 #pragma unroll
-    for (int h = 0; h < H; ++h)
-      m |= (uint32_t)(a.upper[((size_t)g * H + h) * nc + c] >= a.thr[g * H + h]) << h;
-    a.masks[(size_t)g * nc + c] = (uint8_t)m;
+    for (int h = 0; h < H; ++h) m |= (uint32_t)(upv[h] >= thv[h]) << h;
+    a.masks[(size_t)g * nc + c0 + t] = (uint8_t)m;
   }
   __syncthreads();
   {
