@@ -354,8 +354,9 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
   int64_t dc[4], df[4];
   combine_limbs(acc_c, dc);
   combine_limbs(acc_f, df);
+  const int h = (lane & 15) >> 2;
+  uint32_t lmax = 0;  // max ordered lower bound of the lane's 4 centroids
   if ((lane & 3) == 0) {
-    const int h = (lane & 15) >> 2;
     const int64_t S = sq.sum[h];
     const int fx = sq.fx[h];
     const float norm = sq.norm[h];
@@ -368,13 +369,20 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
       const float value = __fmul_rn(val, t.sc4);
       const float margin = __fmul_rn(norm, res[r]);
       const size_t o = ((size_t)g * H + h) * nc + c;
-      a.lower[o] = (uint16_t)ordered16(bf16_rne(__fsub_rn(value, margin)));
+      const uint32_t lo16 = ordered16(bf16_rne(__fsub_rn(value, margin)));
+      lmax = max(lmax, lo16);
+      a.lower[o] = (uint16_t)lo16;
       a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
       const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
       const uint32_t fb = bf16_rne(__fmul_rn(fv, t.gf));
       a.fine_ord[o] = (uint16_t)ordered16(fb);
       if (a.debug) a.fine_bits[o] = (uint16_t)fb;
     }
+  }
+  if (a.tmax_lo) {  // 8-centroid tile maxima: rows 4kb.. and 4(kb+1).. (lanes l, l + 16)
+    lmax = max(lmax, (uint32_t)__shfl_xor((int)lmax, 16));
+    if ((lane & 3) == 0 && (kb & 1) == 0)
+      a.tmax_lo[((size_t)g * H + h) * (nc / 8) + tile * 2 + (kb >> 1)] = (uint16_t)lmax;
   }
 }
 
@@ -518,7 +526,35 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   }
   // ---- threshold: the P-th largest lower bound (its value)
   bool done = false;
-  if (a.exact_select != 1) {
+  if (a.exact_select == 0 && a.tmax_lo) {
+    // From the 8-centroid tile maxima: x, the P-th largest of them, is at
+    // most the P-th largest lower bound (P tiles hold a bound >= x), so every
+    // bound at or above that value lies in a tile whose max is >= x.  Those
+    // tiles (at most one octet per thread) are gathered and the exact value
+    // selected among them in registers.
+    FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
+    const int nt8 = nc / 8;
+    const uint4 wt = load_oct(a.tmax_lo + ((size_t)g * H + h) * nt8, nt8);
+    const OctResult rt = oct_select<true, false>(wt, a.P[g], cid, fs);
+    const uint32_t x = rt.sel.all ? 1u : rt.sel.v;
+    const u32x4 wtv = {wt.x, wt.y, wt.z, wt.w};
+    uint32_t fl = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) fl |= (uint32_t)(oct_half(wtv, e) >= x) << e;
+    int ntiles;
+    int j = block_excl_scan(__popc(fl), fs.scan, &ntiles);  // ends with a barrier
+    if (ntiles <= SEL_BLOCK) {
+      int* tl = reinterpret_cast<int*>(fs.cand);
+      for (uint32_t rest = fl; rest; rest &= rest - 1) tl[j++] = 8 * (int)threadIdx.x + __ffs(rest) - 1;
+      __syncthreads();
+      uint4 wg = make_uint4(0, 0, 0, 0);
+      if ((int)threadIdx.x < ntiles) wg = reinterpret_cast<const uint4*>(lo)[tl[threadIdx.x]];
+      const OctResult rg = oct_select<true, false>(wg, a.P[g], cid, fs);
+      if (threadIdx.x == 0) s_thr = rg.sel.all ? 0u : rg.sel.v;
+      done = true;
+    }
+  }
+  if (!done && a.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
     const FastResult r = fast_select<true>(RowScores{lo}, nc, a.P[g], cid, fs, force, 2);
     if (r.ok) {
