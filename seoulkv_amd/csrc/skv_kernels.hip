@@ -1093,14 +1093,18 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
 // owns a contiguous span of bitmap words: it counts the members in all
 // earlier words (its output base), lists its own members in LDS, copies
 // their tokens to the output list and scores them 16 keys per MFMA tile.
-constexpr int US_BLOCK = 512;
-constexpr int US_CHUNK = US_BLOCK / 64;  // bitmap words listed per pass (1 item per thread)
-constexpr int US_GRID_U1 = 96;  // blocks per group over the pool
+// U1: 64 blocks of 1024 threads per group, one per CU across the 4 groups,
+// each listing up to 16 words per pass (config 2: one pass); U2: 16 blocks
+// of 512 threads per group over at most 100 words.
+constexpr int us_block(int stage) { return stage == 4 ? 1024 : 512; }
+constexpr int US_GRID_U1 = 64;  // blocks per group over the pool
 constexpr int US_GRID_U2 = 16;  // blocks per group over U1 (<= 100 words)
 
 template <int STAGE>
-__global__ __launch_bounds__(US_BLOCK) void k_union_score(StepArgs a) {
+__global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
   constexpr bool U1 = STAGE == 4;
+  constexpr int US_BLOCK = us_block(STAGE);
+  constexpr int US_CHUNK = US_BLOCK / 64;  // bitmap words listed per pass (1 item per thread)
   SKV_TSB((U1 ? 3 : 8), 0);
   const int ts = U1 ? 8 : 11;
   SKV_TS(ts, 0);
@@ -1452,13 +1456,13 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
       break;
     case 5:
-      hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(US_BLOCK), 0, st, a);
+      hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(us_block(4)), 0, st, a);
       break;
     case 6:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
       break;
     case 7:
-      hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(US_BLOCK), 0, st, a);
+      hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(us_block(8)), 0, st, a);
       break;
     case 8:
       hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
