@@ -618,7 +618,7 @@ __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint
   return mate > c || !((selbm[mate >> 5] >> (mate & 31)) & 1u);
 }
 
-constexpr int PL_BLOCK = 512;  // pool: one posting per thread and page
+constexpr int PL_BLOCK = 1024;  // pool: one posting per thread and page, one block per CU
 constexpr int PL_WAVES = PL_BLOCK / WAVE;
 constexpr int PL_RANGE_MAX = PL_BLOCK;  // centroids per pool block: one per thread
 constexpr int S2_GRID = 320;   // score2 blocks per group (4 waves each)

@@ -338,9 +338,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   a.words_u1 = words1;
   a.words_u2 = words2;
   a.pool_blocks = nc / 32;
-  // at most 128 ranges per group (one look-back poll reaches every
-  // predecessor), at least 64 centroids per range
-  a.pool_range = std::max(64, (nc / 128 + 31) / 32 * 32);
+  // at most 64 ranges per group (one pool block per CU over the 4 groups;
+  // one look-back poll reaches every predecessor), at least 128 centroids
+  // per range
+  a.pool_range = std::max(128, (nc / 64 + 31) / 32 * 32);
   a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
   h->dn.T = T;
   dense_shape(T, h->dn.iters, h->dn.nb);

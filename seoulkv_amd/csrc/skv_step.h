@@ -60,7 +60,7 @@ struct StepArgs {
   int pool_min, pool_capacity, debug;
   int exact_select;         // 1: always run the full selections (no sampled cut)
   int pool_blocks;          // nc / 32: 32-centroid bitmap words
-  int pool_range;           // centroids per pool-kernel block (a multiple of 32, <= 512)
+  int pool_range;           // centroids per pool-kernel block (a multiple of 32, <= 1024)
   int words_u1, words_u2;   // bitmap words per (group, head)
   int dense_slices;         // DENSE_SLICE_KEYS-key sink/local attention slices per query head
   // static device data
