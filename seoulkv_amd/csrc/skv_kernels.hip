@@ -621,7 +621,8 @@ __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint
 constexpr int PL_BLOCK = 1024;  // pool: one posting per thread and page, one block per CU
 constexpr int PL_WAVES = PL_BLOCK / WAVE;
 constexpr int PL_RANGE_MAX = PL_BLOCK;  // centroids per pool block: one per thread
-constexpr int S2_GRID = 320;   // score2 blocks per group (4 waves each)
+constexpr int S2_BLOCK = 256;  // score2 threads per block
+constexpr int S2_GRID = 320;   // score2 blocks per group
 constexpr int S2_TILES = 2;    // 16-item tiles per wave and pass (loads issued together)
 
 // Range records for the look-back, one 64-bit word written and read whole:
@@ -904,14 +905,15 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
 // 2-bit pool scores s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) from each pool
 // key's prefix plane (its row in the posting-ordered copy), 16 pool items per
 // matrix-core tile, tiles spread over the grid (grid-stride).
-__global__ __launch_bounds__(256) void k_score2(StepArgs a) {
+__global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
   SKV_TSB(2, 0);
   SKV_TS(14, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int n = a.status[g * ST_WORDS + ST_POOL];
   const int ntiles = (n + 15) / 16;
-  const int w0 = blockIdx.x * 4 + (threadIdx.x >> 6), wstride = gridDim.x * 4;
+  constexpr int WPB = S2_BLOCK / WAVE;
+  const int w0 = blockIdx.x * WPB + (threadIdx.x >> 6), wstride = gridDim.x * WPB;
   if (w0 >= ntiles) {
     SKV_TSE(2);
     return;
@@ -1450,7 +1452,7 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
                          bm_lds, st, a);
       break;
     case 3:
-      hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(S2_BLOCK), 0, st, a);
       break;
     case 4:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
