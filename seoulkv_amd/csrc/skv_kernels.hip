@@ -293,11 +293,11 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 }
 
 // ============================================================ front
-constexpr int FR_BLOCK = 256;   // front: one 16-centroid tile per wave
+constexpr int FR_BLOCK = 512;   // front: one 16-centroid tile per wave
 constexpr int FR_WAVES = FR_BLOCK / WAVE;
-static_assert(FR_WAVES == H, "front: wave w forms query head w");
+static_assert(FR_WAVES >= H, "front: wave w < H forms query head w");
 constexpr int FR_CENTROIDS = 16 * FR_WAVES;
-constexpr int FR_MAX_BLOCKS = 256;  // front blocks per group (each loops over its tiles)
+constexpr int FR_MAX_BLOCKS = 128;  // front blocks per group (each loops over its tiles)
 
 // One wave tile = 16 centroids x 4 heads.  Every block first forms the raw
 // query operand of its group in LDS (its centroid-plane loads are already in
@@ -401,8 +401,8 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   const int step = FR_WAVES * (int)gridDim.x;
   int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
   // the query first: forming its operand then waits for it alone while the
-  // plane loads are still in flight (FR_WAVES == H: wave = head)
-  const uint2 qw = load_qw(a, g, threadIdx.x >> 6, lane);
+  // plane loads are still in flight (waves 0 .. H-1 form heads 0 .. H-1)
+  const uint2 qw = load_qw(a, g, min((int)(threadIdx.x >> 6), H - 1), lane);
   __builtin_amdgcn_sched_barrier(0);  // keep the query load ahead of the tile's
   FrTile cur = fr_load(a, g, tile, lane);
   __shared__ __align__(16) QOperand sq;
