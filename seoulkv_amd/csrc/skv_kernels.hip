@@ -729,29 +729,42 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   const int S = s_cum[nsel];  // postings of the selected clusters
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
   const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
-  // posting i of the range's selected lists -> (posting index, owned)
-  auto posting = [&](int i, int& j) {
+  // posting i of the range's selected lists -> posting index j (its cluster
+  // in cl), and whether the range owns it
+  auto locate = [&](int i, int& cl) {
     int lo = 0, hi = nsel;  // s_cum[lo] <= i < s_cum[hi]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (s_cum[mid] <= i) lo = mid;
       else hi = mid;
     }
-    const int cl = s_cl[lo];
-    j = s_off[cl] + (i - s_cum[lo]);
+    cl = s_cl[lo];
+    return s_off[cl] + (i - s_cum[lo]);
+  };
+  auto posting = [&](int i, int& j) {
+    int cl;
+    j = locate(i, cl);
     return owned(s_bm, (uint32_t)mate[j], (uint32_t)(c0 + cl));
   };
-  // ---- count (the first page stays in registers for the emit)
-  int j0 = 0, t0 = 0;
-  bool o0 = false;
-  if ((int)threadIdx.x < S) {
-    o0 = posting(threadIdx.x, j0);
-    t0 = ptok[j0];
-  }
+  // ---- count: the first two pages stay in registers for the emit (their
+  // mate and token loads issued together); later pages are re-walked
+  const bool h0 = (int)threadIdx.x < S, h1 = (int)threadIdx.x + PL_BLOCK < S;
+  int cl0 = 0, cl1 = 0;
+  const int j0 = h0 ? locate(threadIdx.x, cl0) : 0;
+  const int j1 = h1 ? locate(threadIdx.x + PL_BLOCK, cl1) : 0;
+  const int m0 = h0 ? mate[j0] : -1, m1 = h1 ? mate[j1] : -1;
+  const int t0 = h0 ? ptok[j0] : 0, t1 = h1 ? ptok[j1] : 0;
+  const bool o0 = h0 && owned(s_bm, (uint32_t)m0, (uint32_t)(c0 + cl0));
+  const bool o1 = h1 && owned(s_bm, (uint32_t)m1, (uint32_t)(c0 + cl1));
   int owned_total;
   const int ex0 = block_excl_scan(o0 ? 1 : 0, s_scan, &owned_total);
   const int page0_total = owned_total;
-  for (int base = PL_BLOCK; base < S; base += PL_BLOCK) {
+  int ex1 = 0, page1_total = 0;
+  if (S > PL_BLOCK) {  // block-uniform
+    ex1 = block_excl_scan(o1 ? 1 : 0, s_scan, &page1_total);
+    owned_total += page1_total;
+  }
+  for (int base = 2 * PL_BLOCK; base < S; base += PL_BLOCK) {
     int j = 0;
     const bool o = (int)(base + threadIdx.x) < S && posting(base + threadIdx.x, j);
     int tot;
@@ -869,8 +882,12 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     pool[pos0 + ex0] = t0;
     pool_post[pos0 + ex0] = j0;
   }
-  int carry = page0_total;
-  for (int base = PL_BLOCK; base < S; base += PL_BLOCK) {  // ranges over one page
+  if (o1 && pos0 + page0_total + ex1 < a.cap) {
+    pool[pos0 + page0_total + ex1] = t1;
+    pool_post[pos0 + page0_total + ex1] = j1;
+  }
+  int carry = page0_total + page1_total;
+  for (int base = 2 * PL_BLOCK; base < S; base += PL_BLOCK) {  // ranges over two pages
     int j = 0;
     const bool o = (int)(base + threadIdx.x) < S && posting(base + threadIdx.x, j);
     int tot;
