@@ -177,34 +177,13 @@ __device__ __forceinline__ int fs_sample_item(int n, int u) {
   return n <= FS_SAMPLE ? j : (int)(((uint64_t)j * (uint64_t)n) >> 12);
 }
 
-template <bool VALUE_ONLY, typename Src, typename IdFn, typename SampleFn>
-__device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastScratch& s,
-                                    bool force_miss, int ts, SampleFn sample) {
-  FastResult res;
-  res.ok = true;
-  res.ncand = 0;
-  res.sel.idcut = 0xffffffffu;
-  res.sel.all = false;
-  res.sel.above = 0;
+// Phase 1 of the sampled selection: from this thread's FS_PER sample scores
+// sv (0 = excluded), the cut that about k + 4 sqrt(k) + 8 of n items reach
+// (the rank-th best sample, rank scaled to the sample); also resets the
+// candidate list.  Returns cut >= 1 (1: every valid item).
+__device__ __forceinline__ uint32_t fs_cut(const uint32_t (&sv)[FS_PER], int n, int k,
+                                           bool force_miss, FastScratch& s, int ts) {
   const bool full = n <= FS_SAMPLE;
-
-  // ---- 1. sample
-  uint32_t sv[FS_PER];
-#pragma unroll
-  for (int u = 0; u < FS_PER; ++u) {
-    const int i = fs_sample_item(n, u);
-    sv[u] = i >= n ? 0u : sample(u, i);
-  }
-  // the candidate pass's first Src::PRE octets per thread, loaded now so that
-  // they arrive while the cut is computed
-  static_assert(Src::PRE % FS_OCT == 0, "prefetch whole passes");
-  const int no = (n + 7) >> 3;
-  uint4 pre[Src::PRE];
-#pragma unroll
-  for (int q = 0; q < Src::PRE; ++q) {
-    const int o = (int)threadIdx.x + q * SEL_BLOCK;
-    pre[q] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
-  }
   for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
   if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
@@ -242,70 +221,19 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   }
   __syncthreads();
   SKV_TS(ts, 2);
+  return cut;
+}
 
-  // ---- 2. candidate positions: packed compares into a per-lane bit mask
-  // (cut >= 1, so excluded items never pass), then one LDS append per set bit
-  {
-    const int lane = threadIdx.x & 63;
-    const int base0 = threadIdx.x & ~63;
-    const u16x2 cm1 = {(uint16_t)(cut - 1), (uint16_t)(cut - 1)};  // cut >= 1
-    uint32_t mx = 0;
-    auto pass = [&](const uint4 (&w)[FS_OCT], int base) {
-      uint32_t mask = 0;
-#pragma unroll
-      for (int r = 0; r < FS_OCT; ++r) {
-        // bit 2e: low half of word e >= cut; bit 2e + 1: high half
-        const uint32_t m = ge_cut2(w[r].x, cm1) | (ge_cut2(w[r].y, cm1) << 2) |
-                           (ge_cut2(w[r].z, cm1) << 4) | (ge_cut2(w[r].w, cm1) << 6);
-        uint32_t m8 = (m & 0x55u) | ((m >> 15) & 0xaau);
-        const int valid = n - 8 * (base + r * SEL_BLOCK + lane);
-        if (valid < 8) m8 &= valid > 0 ? (1u << valid) - 1u : 0u;
-        mask |= m8 << (8 * r);
-      }
-      const int cnt = __popc(mask);
-      const int inc = wave_incl_scan(cnt);
-      int wbase = 0;
-      if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
-      wbase = __builtin_amdgcn_readlane(wbase, 63);
-      int slot = wbase + inc - cnt;
-#pragma unroll
-      for (int r = 0; r < FS_OCT; ++r) {  // compile-time octet: no indexed arrays
-        uint32_t m8 = (mask >> (8 * r)) & 0xffu;
-        const u32x4 wv = {w[r].x, w[r].y, w[r].z, w[r].w};
-        const int pos0 = 8 * (base + r * SEL_BLOCK + lane);
-        while (m8) {
-          const int e = __ffs(m8) - 1;
-          m8 &= m8 - 1;
-          const uint32_t word = wv[e >> 1];
-          const uint32_t o = (e & 1) ? word >> 16 : word & 0xffffu;
-          mx = max(mx, o);
-          if (slot < CAND_CAP) s.cand[slot] = ((uint64_t)o << 40) | (uint64_t)(pos0 + e);
-          ++slot;
-        }
-      }
-    };
-    // passes over the octets loaded at entry, then over the rest
-#pragma unroll
-    for (int p = 0; p < Src::PRE / FS_OCT; ++p) {
-      const int base = base0 + p * FS_OCT * SEL_BLOCK;
-      if (base >= no) break;  // wave-uniform
-      const uint4 w[FS_OCT] = {pre[FS_OCT * p], pre[FS_OCT * p + 1], pre[FS_OCT * p + 2],
-                               pre[FS_OCT * p + 3]};
-      pass(w, base);
-    }
-    for (int base = base0 + Src::PRE * SEL_BLOCK; base < no; base += FS_OCT * SEL_BLOCK) {
-      uint4 w[FS_OCT];
-#pragma unroll
-      for (int r = 0; r < FS_OCT; ++r) {
-        const int o = base + r * SEL_BLOCK + lane;
-        w[r] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
-      }
-      pass(w, base);
-    }
-    mx = (uint32_t)wave_max((int)mx);
-    if (lane == 0) atomicMax(&s.maxo, (int)mx);
-  }
-  __syncthreads();
+// Phases 3 on: the exact top-k among the candidates s.cand[0 .. s.ncand)
+// (every item scoring >= cut; s.maxo their best score).
+template <bool VALUE_ONLY, typename IdFn>
+__device__ FastResult fs_finish(int k, IdFn id, FastScratch& s, uint32_t cut, int ts) {
+  FastResult res;
+  res.ok = true;
+  res.ncand = 0;
+  res.sel.idcut = 0xffffffffu;
+  res.sel.all = false;
+  res.sel.above = 0;
   SKV_TS(ts, 3);
   const int nc = s.ncand;
   res.ncand = nc;
@@ -406,6 +334,174 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   const uint64_t kth = block_kth<24>(nc, need, val, s.k);
   res.sel.idcut = 0xfffffu - (uint32_t)kth;
   return res;
+}
+
+template <bool VALUE_ONLY, typename Src, typename IdFn, typename SampleFn>
+__device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastScratch& s,
+                                    bool force_miss, int ts, SampleFn sample) {
+  // ---- 1. sample
+  uint32_t sv[FS_PER];
+#pragma unroll
+  for (int u = 0; u < FS_PER; ++u) {
+    const int i = fs_sample_item(n, u);
+    sv[u] = i >= n ? 0u : sample(u, i);
+  }
+  // the candidate pass's first Src::PRE octets per thread, loaded now so that
+  // they arrive while the cut is computed
+  static_assert(Src::PRE % FS_OCT == 0, "prefetch whole passes");
+  const int no = (n + 7) >> 3;
+  uint4 pre[Src::PRE];
+#pragma unroll
+  for (int q = 0; q < Src::PRE; ++q) {
+    const int o = (int)threadIdx.x + q * SEL_BLOCK;
+    pre[q] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
+  }
+  const uint32_t cut = fs_cut(sv, n, k, force_miss, s, ts);
+
+  // ---- 2. candidate positions: packed compares into a per-lane bit mask
+  // (cut >= 1, so excluded items never pass), then one LDS append per set bit
+  {
+    const int lane = threadIdx.x & 63;
+    const int base0 = threadIdx.x & ~63;
+    const u16x2 cm1 = {(uint16_t)(cut - 1), (uint16_t)(cut - 1)};  // cut >= 1
+    uint32_t mx = 0;
+    auto pass = [&](const uint4 (&w)[FS_OCT], int base) {
+      uint32_t mask = 0;
+#pragma unroll
+      for (int r = 0; r < FS_OCT; ++r) {
+        // bit 2e: low half of word e >= cut; bit 2e + 1: high half
+        const uint32_t m = ge_cut2(w[r].x, cm1) | (ge_cut2(w[r].y, cm1) << 2) |
+                           (ge_cut2(w[r].z, cm1) << 4) | (ge_cut2(w[r].w, cm1) << 6);
+        uint32_t m8 = (m & 0x55u) | ((m >> 15) & 0xaau);
+        const int valid = n - 8 * (base + r * SEL_BLOCK + lane);
+        if (valid < 8) m8 &= valid > 0 ? (1u << valid) - 1u : 0u;
+        mask |= m8 << (8 * r);
+      }
+      const int cnt = __popc(mask);
+      const int inc = wave_incl_scan(cnt);
+      int wbase = 0;
+      if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
+      wbase = __builtin_amdgcn_readlane(wbase, 63);
+      int slot = wbase + inc - cnt;
+#pragma unroll
+      for (int r = 0; r < FS_OCT; ++r) {  // compile-time octet: no indexed arrays
+        uint32_t m8 = (mask >> (8 * r)) & 0xffu;
+        const u32x4 wv = {w[r].x, w[r].y, w[r].z, w[r].w};
+        const int pos0 = 8 * (base + r * SEL_BLOCK + lane);
+        while (m8) {
+          const int e = __ffs(m8) - 1;
+          m8 &= m8 - 1;
+          const uint32_t word = wv[e >> 1];
+          const uint32_t o = (e & 1) ? word >> 16 : word & 0xffffu;
+          mx = max(mx, o);
+          if (slot < CAND_CAP) s.cand[slot] = ((uint64_t)o << 40) | (uint64_t)(pos0 + e);
+          ++slot;
+        }
+      }
+    };
+    // passes over the octets loaded at entry, then over the rest
+#pragma unroll
+    for (int p = 0; p < Src::PRE / FS_OCT; ++p) {
+      const int base = base0 + p * FS_OCT * SEL_BLOCK;
+      if (base >= no) break;  // wave-uniform
+      const uint4 w[FS_OCT] = {pre[FS_OCT * p], pre[FS_OCT * p + 1], pre[FS_OCT * p + 2],
+                               pre[FS_OCT * p + 3]};
+      pass(w, base);
+    }
+    for (int base = base0 + Src::PRE * SEL_BLOCK; base < no; base += FS_OCT * SEL_BLOCK) {
+      uint4 w[FS_OCT];
+#pragma unroll
+      for (int r = 0; r < FS_OCT; ++r) {
+        const int o = base + r * SEL_BLOCK + lane;
+        w[r] = o < no ? src.oct(o) : make_uint4(0, 0, 0, 0);
+      }
+      pass(w, base);
+    }
+    mx = (uint32_t)wave_max((int)mx);
+    if (lane == 0) atomicMax(&s.maxo, (int)mx);
+  }
+  __syncthreads();
+  return fs_finish<VALUE_ONLY>(k, id, s, cut, ts);
+}
+
+// Exact top-k of a row of n (FS_SAMPLE < n <= 64 x SEL_BLOCK) ordered scores
+// whose producer also wrote the max of every 16-item tile (tmx): the same
+// sample and cut as fast_select, then the candidate pass over the tiles
+// whose max reaches the cut only (their scores loaded then), one tile per
+// thread and round.  The candidates are exactly fast_select's, so is the
+// result; the row is read in full only by the sample.
+template <typename IdFn>
+__device__ FastResult tiled_select(const uint16_t* __restrict__ row, const uint16_t* __restrict__ tmx,
+                                   int n, int k, IdFn id, FastScratch& s, int ts) {
+  // ---- 1. the sample and this thread's 4 tile maxima, loaded together
+  uint32_t sv[FS_PER];
+#pragma unroll
+  for (int u = 0; u < FS_PER; ++u) sv[u] = row[fs_sample_item(n, u)];
+  const int ntile = (n + 15) >> 4;
+  const int t4 = 4 * (int)threadIdx.x;
+  const uint2 tm = t4 < ntile ? *reinterpret_cast<const uint2*>(tmx + t4) : make_uint2(0, 0);
+  const uint32_t cut = fs_cut(sv, n, k, false, s, ts);
+  // ---- 2. the tiles whose max reaches the cut, listed in s.hist (free
+  // until fs_finish)
+  const uint32_t tv[4] = {tm.x & 0xffffu, tm.x >> 16, tm.y & 0xffffu, tm.y >> 16};
+  uint32_t hot = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hot |= (uint32_t)(t4 + e < ntile && tv[e] >= cut) << e;
+  int nhot;
+  int at = block_excl_scan(__popc(hot), s.scan, &nhot);  // ends with a barrier
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if ((hot >> e) & 1u) s.hist[at++] = (uint32_t)(t4 + e);
+  __syncthreads();
+  // ---- 3. candidates of the listed tiles (packed compares, one LDS append
+  // per set bit, as fast_select's pass)
+  const int lane = threadIdx.x & 63;
+  const u16x2 cm1 = {(uint16_t)(cut - 1), (uint16_t)(cut - 1)};  // cut >= 1
+  uint32_t mx = 0;
+  for (int base = 0; base < nhot; base += SEL_BLOCK) {  // block-uniform
+    const int i = base + (int)threadIdx.x;
+    const int tile = i < nhot ? (int)s.hist[i] : -1;
+    uint4 w[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    if (tile >= 0) {
+      const uint4* r4 = reinterpret_cast<const uint4*>(row) + 2 * tile;
+      w[0] = r4[0];
+      w[1] = r4[1];
+    }
+    uint32_t mask = 0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t m = ge_cut2(w[r].x, cm1) | (ge_cut2(w[r].y, cm1) << 2) |
+                         (ge_cut2(w[r].z, cm1) << 4) | (ge_cut2(w[r].w, cm1) << 6);
+      mask |= ((m & 0x55u) | ((m >> 15) & 0xaau)) << (8 * r);
+    }
+    if (tile < 0) mask = 0;
+    else if (n - 16 * tile < 16) mask &= (1u << (n - 16 * tile)) - 1u;
+    const int cnt = __popc(mask);
+    const int inc = wave_incl_scan(cnt);
+    int wbase = 0;
+    if (lane == 63) wbase = atomicAdd(&s.ncand, inc);
+    wbase = __builtin_amdgcn_readlane(wbase, 63);
+    int slot = wbase + inc - cnt;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {  // compile-time octet: no indexed arrays
+      uint32_t m8 = (mask >> (8 * r)) & 0xffu;
+      const u32x4 wv = {w[r].x, w[r].y, w[r].z, w[r].w};
+      const int pos0 = 16 * tile + 8 * r;
+      while (m8) {
+        const int e = __ffs(m8) - 1;
+        m8 &= m8 - 1;
+        const uint32_t word = wv[e >> 1];
+        const uint32_t o = (e & 1) ? word >> 16 : word & 0xffffu;
+        mx = max(mx, o);
+        if (slot < CAND_CAP) s.cand[slot] = ((uint64_t)o << 40) | (uint64_t)(pos0 + e);
+        ++slot;
+      }
+    }
+  }
+  mx = (uint32_t)wave_max((int)mx);
+  if (lane == 0) atomicMax(&s.maxo, (int)mx);
+  __syncthreads();
+  return fs_finish<false>(k, id, s, cut, ts);
 }
 
 template <bool VALUE_ONLY = false, typename Src, typename IdFn>

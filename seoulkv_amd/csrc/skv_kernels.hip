@@ -973,15 +973,22 @@ __global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
       }
       int64_t dot[4];
       combine_limbs(acc, dot);
+      uint32_t vmax = 0;  // max of the tile for this lane's head
       if ((lane & 3) == 0) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int ii = tile * 16 + 4 * kb + rr;
-          if (ii < n)
-            s2[(size_t)h * a.cap + ii] =
-                (uint16_t)ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
+          if (ii < n) {
+            const uint32_t o = ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
+            s2[(size_t)h * a.cap + ii] = (uint16_t)o;
+            vmax = max(vmax, o);
+          }
         }
       }
+      vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 16));
+      vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 32));
+      if (lane < 16 && (lane & 3) == 0)
+        a.s2_tmax[((size_t)g * H + h) * (a.cap / 16) + tile] = (uint16_t)vmax;
     }
   }
   SKV_TS(14, 15);
@@ -1039,7 +1046,15 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
     uint64_t* mb = local ? reinterpret_cast<uint64_t*>(dyn + sizeof(FastScratch)) : bm;
     if (local)
       for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
-    const FastResult r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
+    FastResult r{};
+    r.ok = false;
+    if (t.tile_max && t.exact_select == 0 && n > OCT_ITEMS && (n + 15) / 16 <= 4 * SEL_BLOCK) {
+      // the producer wrote the max of every 16-item tile: only the tiles
+      // reaching the cut are read for candidates
+      r = tiled_select(sc, t.tile_max + ((size_t)g * H + h) * t.tile_stride, n, t.k, id, fs, ts);
+      __syncthreads();
+    }
+    if (!r.ok) r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
     if (r.ok) {
       SKV_TS(ts, 6);
       if (!local) {

@@ -394,6 +394,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
     a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
+    a.s2_tmax = (uint16_t*)ar.take((size_t)G * H * (a.cap / 16) * 2);
     a.dense_part = (float*)ar.take((size_t)G * H * std::max(a.dense_slices, 1) * (D + 2) * 4);
     a.selbm = (uint32_t*)ar.take((size_t)G * (nc / 32) * 4);  // cleared by k_front
     a.u1_tok = (int*)ar.take((size_t)G * U1_MAX * 4);
@@ -513,9 +514,9 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     return bail(SKV_EINVAL);
   }
   w.top_u1 = TopkArgs{a.s2, a.pool_tok, a.cap, M15, a.bm_u1, words1, a.status, ST_POOL,
-                      std::min(lds_items, a.cap), 0, FS_TOP1600};
+                      std::min(lds_items, a.cap), 0, FS_TOP1600, a.s2_tmax, a.cap / 16};
   w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, a.bm_u2, words2, a.status, ST_U1, U1_MAX,
-                      0, FS_TOP256};
+                      0, FS_TOP256, nullptr, 0};
   // Dynamic LDS of the selection kernels: the sampled-cut scratch, or the
   // LDS-resident scores of the full selection, or the attention scratch of
   // the sink/local blocks, whichever is largest (they are never live together).

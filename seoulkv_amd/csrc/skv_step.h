@@ -93,6 +93,7 @@ struct StepArgs {
   int* pool_tok;            // [G][cap]
   int* pool_post;           // [G][cap] posting index (into post_p2) of each pool key
   uint16_t* s2;             // [G][H][cap] ordered
+  uint16_t* s2_tmax;        // [G][H][cap/16] max of every 16-key tile of s2
   uint64_t* bm_u1;          // [G][H][words_u1] top-1600 members
   uint64_t* bm_u2;          // [G][H][words_u2] top-256 members
   float* dense_part;        // [16][dense_slices][D + 2] sink/local partial (o, max, sum)
@@ -118,6 +119,8 @@ struct TopkArgs {
   int lds_items;            // scores held in LDS when count <= lds_items
   int exact_select;         // 1: skip the sampled cut
   int fullsel_bit;          // FS_* bit recorded when the full selection runs
+  const uint16_t* tile_max; // [G][H][tile_stride] max of every 16-item tile (or NULL)
+  int tile_stride;
 };
 
 
