@@ -424,19 +424,40 @@ __device__ FastResult fast_select_s(const Src& src, int n, int k, IdFn id, FastS
   return fs_finish<VALUE_ONLY>(k, id, s, cut, ts);
 }
 
-// Exact top-k of a row of n (FS_SAMPLE < n <= 64 x SEL_BLOCK) ordered scores
-// whose producer also wrote the max of every 16-item tile (tmx): the same
-// sample and cut as fast_select, then the candidate pass over the tiles
-// whose max reaches the cut only (their scores loaded then), one tile per
-// thread and round.  The candidates are exactly fast_select's, so is the
-// result; the row is read in full only by the sample.
-template <typename IdFn>
-__device__ FastResult tiled_select(const uint16_t* __restrict__ row, const uint16_t* __restrict__ tmx,
-                                   int n, int k, IdFn id, FastScratch& s, int ts) {
-  // ---- 1. the sample and this thread's 4 tile maxima, loaded together
-  uint32_t sv[FS_PER];
-#pragma unroll
-  for (int u = 0; u < FS_PER; ++u) sv[u] = row[fs_sample_item(n, u)];
+// 16-item tiles of a 16-byte aligned row of ordered scores.
+struct RowTiles {
+  const uint16_t* __restrict__ row;
+  __device__ void tile(int t, uint4 (&w)[2]) const {
+    const uint4* r4 = reinterpret_cast<const uint4*>(row) + 2 * t;
+    w[0] = r4[0];
+    w[1] = r4[1];
+  }
+};
+// 16-item tiles of MaskedScores (score where gate >= thr, else excluded).
+struct MaskedTiles {
+  const uint16_t* __restrict__ score;
+  const uint16_t* __restrict__ gate;
+  uint32_t thr;
+  __device__ void tile(int t, uint4 (&w)[2]) const {
+    const uint4* s4 = reinterpret_cast<const uint4*>(score) + 2 * t;
+    const uint4* g4 = reinterpret_cast<const uint4*>(gate) + 2 * t;
+    const uint4 s0 = s4[0], s1 = s4[1], g0 = g4[0], g1 = g4[1];
+    w[0] = MaskedScores::pick4(s0, g0, thr);
+    w[1] = MaskedScores::pick4(s1, g1, thr);
+  }
+};
+
+// Exact top-k of n (FS_SAMPLE < n <= 64 x SEL_BLOCK) ordered scores whose
+// producer also wrote an upper bound of every 16-item tile (tmx, e.g. the
+// tile's max): from this thread's fast_select sample sv the same cut as
+// fast_select, then the candidate pass over the tiles whose bound reaches
+// the cut only (their scores loaded then from src), one tile per thread and
+// round.  The candidates are exactly fast_select's, so is the result.
+template <typename TileSrc, typename IdFn>
+__device__ FastResult tiled_select(const TileSrc& src, const uint16_t* __restrict__ tmx,
+                                   const uint32_t (&sv)[FS_PER], int n, int k, IdFn id,
+                                   FastScratch& s, int ts) {
+  // ---- 1. this thread's 4 tile bounds (loaded with the caller's sample)
   const int ntile = (n + 15) >> 4;
   const int t4 = 4 * (int)threadIdx.x;
   const uint2 tm = t4 < ntile ? *reinterpret_cast<const uint2*>(tmx + t4) : make_uint2(0, 0);
@@ -462,11 +483,7 @@ __device__ FastResult tiled_select(const uint16_t* __restrict__ row, const uint1
     const int i = base + (int)threadIdx.x;
     const int tile = i < nhot ? (int)s.hist[i] : -1;
     uint4 w[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-    if (tile >= 0) {
-      const uint4* r4 = reinterpret_cast<const uint4*>(row) + 2 * tile;
-      w[0] = r4[0];
-      w[1] = r4[1];
-    }
+    if (tile >= 0) src.tile(tile, w);
     uint32_t mask = 0;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {

@@ -355,7 +355,7 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
   combine_limbs(acc_c, dc);
   combine_limbs(acc_f, df);
   const int h = (lane & 15) >> 2;
-  uint32_t lmax = 0;  // max ordered lower bound of the lane's 4 centroids
+  uint32_t lmax = 0, fmax = 0;  // max ordered lower bound / fine score of the lane's 4 centroids
   if ((lane & 3) == 0) {
     const int64_t S = sq.sum[h];
     const int fx = sq.fx[h];
@@ -375,7 +375,9 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
       a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
       const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
       const uint32_t fb = bf16_rne(__fmul_rn(fv, t.gf));
-      a.fine_ord[o] = (uint16_t)ordered16(fb);
+      const uint32_t fo = ordered16(fb);
+      fmax = max(fmax, fo);
+      a.fine_ord[o] = (uint16_t)fo;
       if (a.debug) a.fine_bits[o] = (uint16_t)fb;
     }
   }
@@ -383,6 +385,10 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
     lmax = max(lmax, (uint32_t)__shfl_xor((int)lmax, 16));
     if ((lane & 3) == 0 && (kb & 1) == 0)
       a.tmax_lo[((size_t)g * H + h) * (nc / 8) + tile * 2 + (kb >> 1)] = (uint16_t)lmax;
+    // and the fine-score maximum of the whole 16-centroid tile (4 row groups)
+    fmax = max(fmax, (uint32_t)__shfl_xor((int)fmax, 16));
+    fmax = max(fmax, (uint32_t)__shfl_xor((int)fmax, 32));
+    if (lane < 16 && (lane & 3) == 0) a.tmax_fi[((size_t)g * H + h) * (nc / 16) + tile] = (uint16_t)fmax;
   }
 }
 
@@ -581,9 +587,21 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   done = false;
   if (a.exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select_s<false>(
-        MaskedScores{fi, up, thr}, nc, a.P[g], cid, fs, force, 4,
-        [&](int u, int) { return pg[u] >= thr ? pf[u] : 0u; });
+    FastResult r{};
+    r.ok = false;
+    if (a.exact_select == 0 && a.tmax_fi && nc / 16 <= 4 * SEL_BLOCK) {
+      // only the 16-centroid tiles whose max fine score reaches the cut can
+      // hold a candidate: their scores and gates are loaded, no others
+      uint32_t sv[FS_PER];
+#pragma unroll
+      for (int u = 0; u < FS_PER; ++u) sv[u] = pg[u] >= thr ? pf[u] : 0u;
+      r = tiled_select(MaskedTiles{fi, up, thr}, a.tmax_fi + ((size_t)g * H + h) * (nc / 16), sv, nc,
+                       a.P[g], cid, fs, 4);
+      __syncthreads();
+    }
+    if (!r.ok)
+      r = fast_select_s<false>(MaskedScores{fi, up, thr}, nc, a.P[g], cid, fs, force, 4,
+                               [&](int u, int) { return pg[u] >= thr ? pf[u] : 0u; });
     if (r.ok) {
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
         const uint64_t key = fs.cand[c];
@@ -1051,7 +1069,11 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
     if (t.tile_max && t.exact_select == 0 && n > OCT_ITEMS && (n + 15) / 16 <= 4 * SEL_BLOCK) {
       // the producer wrote the max of every 16-item tile: only the tiles
       // reaching the cut are read for candidates
-      r = tiled_select(sc, t.tile_max + ((size_t)g * H + h) * t.tile_stride, n, t.k, id, fs, ts);
+      uint32_t sv[FS_PER];
+#pragma unroll
+      for (int u = 0; u < FS_PER; ++u) sv[u] = sc[fs_sample_item(n, u)];
+      r = tiled_select(RowTiles{sc}, t.tile_max + ((size_t)g * H + h) * t.tile_stride, sv, n, t.k,
+                       id, fs, ts);
       __syncthreads();
     }
     if (!r.ok) r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);

@@ -388,6 +388,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.fine_ord = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.fine_bits = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.tmax_lo = nc > 8 * SEL_BLOCK ? (uint16_t*)ar.take((size_t)G * H * (nc / 8) * 2) : nullptr;
+    a.tmax_fi = nc > 8 * SEL_BLOCK ? (uint16_t*)ar.take((size_t)G * H * (nc / 16) * 2) : nullptr;
     a.sel = (int*)ar.take((size_t)G * nc * 4);
     a.pool_flags = (unsigned long long*)ar.take((size_t)G * a.pool_blocks * 8);
     a.pool_epoch = (unsigned*)ar.take((size_t)G * 4);

@@ -86,7 +86,8 @@ struct StepArgs {
   uint16_t* fine_ord;       // [G][H][nc] ordered fine score of every centroid
   uint16_t* fine_bits;      // [G][H][nc] BF16 fine score (debug)
   uint16_t* tmax_lo;        // [G][H][nc/8] max ordered lower bound of each 8-centroid tile
-                            // (written when nc > 8 x SEL_BLOCK, else NULL)
+  uint16_t* tmax_fi;        // [G][H][nc/16] max ordered fine score of each 16-centroid tile
+                            // (both written when nc > 8 x SEL_BLOCK, else NULL)
   int* sel;                 // [G][nc] selected clusters, ascending
   unsigned long long* pool_flags;  // [G][pool_blocks] look-back records (epoch-tagged)
   unsigned* pool_epoch;     // [G] launches of the pool kernel (tags the look-back records)
