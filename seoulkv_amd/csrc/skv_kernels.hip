@@ -990,23 +990,27 @@ __global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
         acc = mfma_i8(av, bq[kc], acc);
       }
       int64_t dot[4];
-      combine_limbs(acc, dot);
-      uint32_t vmax = 0;  // max of the tile for this lane's head
-      if ((lane & 3) == 0) {
+      combine_limbs(acc, dot);  // rows 4kb + r of head h, in the quad's first lane
+      // spread the quad's 4 rows over its 4 lanes: lane (kb, h, q) scores row
+      // 4kb + q of head h, so every lane converts one score
+      const int q = lane & 3;
+      int64_t dq = 0;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int ii = tile * 16 + 4 * kb + rr;
-          if (ii < n) {
-            const uint32_t o = ordered16(bf16_rne(scaled_f32(2 * dot[rr] - 3 * S, fx)));
-            s2[(size_t)h * a.cap + ii] = (uint16_t)o;
-            vmax = max(vmax, o);
-          }
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)dot[r], 0x00, 0xf, 0xf, false);
+        const int hi = __builtin_amdgcn_update_dpp(0, (int)(dot[r] >> 32), 0x00, 0xf, 0xf, false);
+        if (r == q) dq = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
       }
+      const int ii = tile * 16 + 4 * kb + q;
+      const uint32_t o = ii < n ? ordered16(bf16_rne(scaled_f32(2 * dq - 3 * S, fx))) : 0u;
+      if (ii < n) s2[(size_t)h * a.cap + ii] = (uint16_t)o;
+      // the tile's max for each head: over the quad, then the 4 row groups
+      uint32_t vmax = o;
+      vmax = max(vmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)vmax, 0xB1, 0xf, 0xf, false));
+      vmax = max(vmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)vmax, 0x4E, 0xf, 0xf, false));
       vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 16));
       vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 32));
-      if (lane < 16 && (lane & 3) == 0)
-        a.s2_tmax[((size_t)g * H + h) * (a.cap / 16) + tile] = (uint16_t)vmax;
+      if (lane < 16 && q == 0) a.s2_tmax[((size_t)g * H + h) * (a.cap / 16) + tile] = (uint16_t)vmax;
     }
   }
   SKV_TS(14, 15);
