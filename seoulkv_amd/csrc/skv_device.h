@@ -272,4 +272,19 @@ __device__ __forceinline__ void combine_limbs(v4i acc, int64_t out[4]) {
   }
 }
 
+// After combine_limbs: the quad's first lane holds rows 4 (l/16) + r of its
+// column's head in out[r]; returns, in every lane, row 4 (l/16) + (l % 4) of
+// that head (the quad's 4 rows spread over its 4 lanes).
+__device__ __forceinline__ int64_t quad_spread(const int64_t out[4]) {
+  const int q = threadIdx.x & 3;
+  int64_t d = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)out[r], 0x00, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(out[r] >> 32), 0x00, 0xf, 0xf, false);
+    if (r == q) d = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);  // quad_perm [0,0,0,0]
+  }
+  return d;
+}
+
 }  // namespace skv

@@ -354,41 +354,36 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
   int64_t dc[4], df[4];
   combine_limbs(acc_c, dc);
   combine_limbs(acc_f, df);
-  const int h = (lane & 15) >> 2;
-  uint32_t lmax = 0, fmax = 0;  // max ordered lower bound / fine score of the lane's 4 centroids
-  if ((lane & 3) == 0) {
-    const int64_t S = sq.sum[h];
-    const int fx = sq.fx[h];
-    const float norm = sq.norm[h];
-    const float res[4] = {t.rs.x, t.rs.y, t.rs.z, t.rs.w};
-    const int c0 = tile * 16 + 4 * kb;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = c0 + r;
-      const float val = scaled_f32(2 * dc[r] - 3 * S, fx);
-      const float value = __fmul_rn(val, t.sc4);
-      const float margin = __fmul_rn(norm, res[r]);
-      const size_t o = ((size_t)g * H + h) * nc + c;
-      const uint32_t lo16 = ordered16(bf16_rne(__fsub_rn(value, margin)));
-      lmax = max(lmax, lo16);
-      a.lower[o] = (uint16_t)lo16;
-      a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
-      const float fv = scaled_f32(2 * df[r] - 15 * S, fx);
-      const uint32_t fb = bf16_rne(__fmul_rn(fv, t.gf));
-      const uint32_t fo = ordered16(fb);
-      fmax = max(fmax, fo);
-      a.fine_ord[o] = (uint16_t)fo;
-      if (a.debug) a.fine_bits[o] = (uint16_t)fb;
-    }
-  }
-  if (a.tmax_lo) {  // 8-centroid tile maxima: rows 4kb.. and 4(kb+1).. (lanes l, l + 16)
+  // lane (kb, h, q) converts centroid 4kb + q of the tile for head h
+  const int h = (lane & 15) >> 2, q = lane & 3;
+  const int64_t dcq = quad_spread(dc), dfq = quad_spread(df);
+  const int64_t S = sq.sum[h];
+  const int fx = sq.fx[h];
+  const float res = q == 0 ? t.rs.x : q == 1 ? t.rs.y : q == 2 ? t.rs.z : t.rs.w;
+  const float value = __fmul_rn(scaled_f32(2 * dcq - 3 * S, fx), t.sc4);
+  const float margin = __fmul_rn(sq.norm[h], res);
+  const size_t o = ((size_t)g * H + h) * nc + tile * 16 + 4 * kb + q;
+  const uint32_t lo16 = ordered16(bf16_rne(__fsub_rn(value, margin)));
+  a.lower[o] = (uint16_t)lo16;
+  a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
+  const uint32_t fb = bf16_rne(__fmul_rn(scaled_f32(2 * dfq - 15 * S, fx), t.gf));
+  const uint32_t fo = ordered16(fb);
+  a.fine_ord[o] = (uint16_t)fo;
+  if (a.debug) a.fine_bits[o] = (uint16_t)fb;
+  if (a.tmax_lo) {
+    // 8-centroid tile maxima: the quad's 4 rows, then rows 4kb.. and 4(kb+1)..
+    // (lanes l, l + 16); the fine-score maximum of the whole 16-centroid tile
+    uint32_t lmax = lo16, fmax = fo;
+    lmax = max(lmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lmax, 0xB1, 0xf, 0xf, false));
+    lmax = max(lmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lmax, 0x4E, 0xf, 0xf, false));
     lmax = max(lmax, (uint32_t)__shfl_xor((int)lmax, 16));
-    if ((lane & 3) == 0 && (kb & 1) == 0)
+    if (q == 0 && (kb & 1) == 0)
       a.tmax_lo[((size_t)g * H + h) * (nc / 8) + tile * 2 + (kb >> 1)] = (uint16_t)lmax;
-    // and the fine-score maximum of the whole 16-centroid tile (4 row groups)
+    fmax = max(fmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)fmax, 0xB1, 0xf, 0xf, false));
+    fmax = max(fmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)fmax, 0x4E, 0xf, 0xf, false));
     fmax = max(fmax, (uint32_t)__shfl_xor((int)fmax, 16));
     fmax = max(fmax, (uint32_t)__shfl_xor((int)fmax, 32));
-    if (lane < 16 && (lane & 3) == 0) a.tmax_fi[((size_t)g * H + h) * (nc / 16) + tile] = (uint16_t)fmax;
+    if (lane < 16 && q == 0) a.tmax_fi[((size_t)g * H + h) * (nc / 16) + tile] = (uint16_t)fmax;
   }
 }
 
@@ -991,16 +986,9 @@ __global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
       }
       int64_t dot[4];
       combine_limbs(acc, dot);  // rows 4kb + r of head h, in the quad's first lane
-      // spread the quad's 4 rows over its 4 lanes: lane (kb, h, q) scores row
-      // 4kb + q of head h, so every lane converts one score
+      // lane (kb, h, q) scores row 4kb + q of head h: every lane converts one
       const int q = lane & 3;
-      int64_t dq = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)dot[r], 0x00, 0xf, 0xf, false);
-        const int hi = __builtin_amdgcn_update_dpp(0, (int)(dot[r] >> 32), 0x00, 0xf, 0xf, false);
-        if (r == q) dq = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-      }
+      const int64_t dq = quad_spread(dot);
       const int ii = tile * 16 + 4 * kb + q;
       const uint32_t o = ii < n ? ordered16(bf16_rne(scaled_f32(2 * dq - 3 * S, fx))) : 0u;
       if (ii < n) s2[(size_t)h * a.cap + ii] = (uint16_t)o;
