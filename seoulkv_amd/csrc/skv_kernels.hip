@@ -1276,34 +1276,28 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
           acc = mfma_i8(hi[kc], b[kc], acc);
           acc_lo = mfma_i8(lo[kc], b[kc], acc_lo);
         }
-        // 8-bit dot = 16 x (code4 dot) + (residual-4 dot)
+        // 8-bit dot = 16 x (code4 dot) + (residual-4 dot); lane (kb, h, q)
+        // converts key 4kb + q of the tile for head h
         int64_t dh[4], dl[4];
         combine_limbs(acc, dh);
         combine_limbs(acc_lo, dl);
-        if ((lane & 3) == 0) {
-          const int h = (lane & 15) >> 2;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = tile * 16 + 4 * kb + r, o = base + i;
-            if (i >= nloc || o >= cap_out) continue;
-            s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
-                bf16_rne(scaled_f32(2 * (16 * dh[r] + dl[r]) - 255 * q->sum[h], q->fx[h])));
-          }
-        }
+        const int64_t dhq = quad_spread(dh), dlq = quad_spread(dl);
+        const int h = (lane & 15) >> 2;
+        const int i = tile * 16 + 4 * kb + (lane & 3), o = base + i;
+        if (i < nloc && o < cap_out)
+          s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
+              bf16_rne(scaled_f32(2 * (16 * dhq + dlq) - 255 * q->sum[h], q->fx[h])));
         continue;
       }
       int64_t dot[4];
       combine_limbs(acc, dot);
-      if ((lane & 3) == 0) {
-        const int h = (lane & 15) >> 2;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = tile * 16 + 4 * kb + r, o = base + i;
-          if (i >= nloc || o >= cap_out) continue;
-          s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
-              bf16_rne(scaled_f32(2 * dot[r] - 15 * q->sum[h], q->fx[h] + 4)));
-        }
-      }
+      // lane (kb, h, q) converts key 4kb + q of the tile for head h
+      const int64_t dq = quad_spread(dot);
+      const int h = (lane & 15) >> 2;
+      const int i = tile * 16 + 4 * kb + (lane & 3), o = base + i;
+      if (i < nloc && o < cap_out)
+        s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
+            bf16_rne(scaled_f32(2 * dq - 15 * q->sum[h], q->fx[h] + 4)));
     }
     base += nloc;
     __syncthreads();
