@@ -32,6 +32,7 @@ from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 G_KV = 4  # KV heads of the layer
+APPEND_TOKENS = 128  # tokens appended after the measured steps (cache-append check)
 METRIC = "µs/layer decode step at T=128K (1 GPU); achieved HBM GB/s; top-100 ID match"
 
 
@@ -202,7 +203,7 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     stream = torch.cuda.Stream(dev)
-    config = SeoulKV4Config(stage15_capacity=None, debug=True)
+    config = SeoulKV4Config(stage15_capacity=None, debug=True, append_capacity=APPEND_TOKENS)
     with torch.cuda.stream(stream):
         attn = SeoulKV4(device=dev, k=k, v=v, index=index, config=config)
         t0 = time.time()
@@ -256,6 +257,30 @@ def main() -> int:
         dense_gpu = rt.read_dense_output().float().numpy().reshape(16, 256)
         dn_kernel_ms, dn_merge_ms, dn_ms = rt.time_dense(reps=max(20, args.steps // 4))
         log(f"dense FP8 decode {dn_ms * 1e3:.1f} µs (partials {dn_kernel_ms * 1e3:.1f} µs)")
+
+        # cache append (after every measurement above: it grows the local
+        # window): single-token host appends, one device append, then the
+        # step over the grown window
+        half = APPEND_TOKENS // 2
+        kn, vn = k[:, -APPEND_TOKENS:].clone(), v[:, -APPEND_TOKENS:].clone()
+        attn.synchronize()
+        t = time.perf_counter()
+        for i in range(half):
+            attn.append(kn[:, i:i + 1], vn[:, i:i + 1])
+        attn.synchronize()
+        app_host_us = (time.perf_counter() - t) / half * 1e6
+        kd, vd = kn[:, half:].to(dev), vn[:, half:].to(dev)
+        t = time.perf_counter()
+        attn.append(kd, vd)
+        app_dev_us = (time.perf_counter() - t) * 1e6
+        start.record(stream)
+        for _ in range(args.steps):
+            attn._run_bound()
+        end.record(stream)
+        end.synchronize()
+        grown_us = start.elapsed_time(end) / args.steps * 1e3
+        log(f"append: {app_host_us:.1f} µs per 1-token host append, {app_dev_us:.1f} µs for "
+            f"{APPEND_TOKENS - half} tokens from device; step after {APPEND_TOKENS}: {grown_us:.1f} µs")
 
     nbytes = kernel_bytes(status, p, p.n_centroids)
     total_bytes = sum(nbytes.values())
@@ -335,6 +360,14 @@ def main() -> int:
             "traffic": measured_traffic("dense_fp8"),
             "max_abs_vs_oracle": dense_err,
             "sparse_over_dense": round(ms_per_step / dn_ms, 3),
+        },
+        "append": {
+            "host_1token_us": round(app_host_us, 1),
+            "device_tokens": APPEND_TOKENS - half,
+            "device_us": round(app_dev_us, 1),
+            "step_us_after": round(grown_us, 2),
+            "appended": APPEND_TOKENS,
+            "note": "wall time incl. host sync; the step attends the grown local window",
         },
         "profiled_steps": n_prof,
         "stage_sizes": {k_: status[k_] for k_ in ("survivors", "selected", "pool", "u1", "u2")},

@@ -66,6 +66,9 @@ typedef struct {
   int32_t pool_capacity;       /* pool upper bound; <= 0 means no bound */
   int32_t debug;               /* nonzero: keep stage outputs readable */
   skv_cell_desc cells[SKV_GROUPS];
+  int32_t append_capacity;     /* tokens per KV head skv_append may add (0: static
+                                  cache, the reference's only mode); context plus
+                                  capacity <= 2^20 */
 } skv_index_desc;
 
 /* Reference _runtime.initialize (_runtime.py:36-177): uploads the index, runs
@@ -104,6 +107,21 @@ int skv_read_output(void *handle, uint16_t *host_out);
 /* Reference debug_snapshot (api.py:127-134): sync + copy final token IDs
  * [4 groups][4 heads][100], best first. */
 int skv_debug_ids(void *handle, uint32_t *host_out);
+
+/* Cache append (the next step after the reference's static PoC cache, which
+ * leaves cache append out: README.md:68-69).  Writes the FP8 [V || K]
+ * records of n new tokens after the current context T and grows the context
+ * and the local window by n: later steps attend [0, S) + [T0 - L, T) densely
+ * plus the top-100 of the prefill index, whose key codec, CSR and retrieval
+ * region [S, T0 - L) stay as built (T0 = the context at skv_create, L = its
+ * local window).  k, v: [4][n][256] BF16, host memory (skv_append, staged
+ * through a device buffer) or device memory (skv_append_device, 8-byte
+ * aligned).  Enqueued on the handle's stream; fails with SKV_EINVAL, the
+ * cache unchanged, when n < 1 or n exceeds the capacity left. */
+int skv_append(void *handle, const uint16_t *k_bf16, const uint16_t *v_bf16,
+               int n);
+int skv_append_device(void *handle, const void *k_dev, const void *v_dev,
+                      int n);
 
 /* Dense FP8 decode (a comparison path with no counterpart in the reference,
  * whose published comparison is TTNN's dense FlashDecode, README.md:7):

@@ -293,11 +293,14 @@ def attention_ids(context: int, sink: int, local: int, top: np.ndarray) -> np.nd
     )
 
 
-def decode_step(cells, code8, scales, k8, v8, q_bits, *, sink, local):
+def decode_step(cells, code8, scales, k8, v8, q_bits, *, sink, local, context=None):
     """Full step.  ``cells``: 4 GroupCell; ``code8`` [4, T, 256]; ``scales``
     [4, 256]; ``k8``/``v8`` FP32 values of the FP8 records [4, T, 256];
-    ``q_bits`` [16, 256] BF16 bits.  Returns (traces, out [16, 256] f64)."""
-    context = code8.shape[1]
+    ``q_bits`` [16, 256] BF16 bits.  Returns (traces, out [16, 256] f64).
+    ``context`` (default T): a cache grown by appended tokens after the
+    prefill of T keys: ``k8``/``v8`` hold ``context`` rows, ``local`` is the
+    grown window, while the codes, scales and cells stay the prefill's."""
+    context = code8.shape[1] if context is None else context
     q_bits = np.asarray(q_bits, dtype=np.uint16).reshape(16, 256)
     traces, out = [], np.zeros((16, 256))
     for g in range(4):

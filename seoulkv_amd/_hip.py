@@ -56,6 +56,7 @@ class IndexDesc(ctypes.Structure):
         ("pool_capacity", ctypes.c_int32),
         ("debug", ctypes.c_int32),
         ("cells", CellDesc * G),
+        ("append_capacity", ctypes.c_int32),
     ]
 
 
@@ -88,6 +89,8 @@ def load_library() -> ctypes.CDLL:
         "skv_select_mode": (i32, [vp, i32]),
         "skv_graph_mode": (i32, [vp, i32]),
         "skv_time_kernel": (i32, [vp, i32, i32, vp]),
+        "skv_append": (i32, [vp, vp, vp, i32]),
+        "skv_append_device": (i32, [vp, vp, vp, i32]),
         "skv_dense_decode": (i32, [vp]),
         "skv_dense_output_device": (i32, [vp, ctypes.POINTER(vp)]),
         "skv_read_dense_output": (i32, [vp, vp]),
@@ -127,7 +130,8 @@ def _np(t: torch.Tensor, dtype) -> np.ndarray:
     return np.ascontiguousarray(t.numpy()).view(dtype)
 
 
-def index_desc(index, *, pool_min: int, pool_capacity: int | None, debug: bool):
+def index_desc(index, *, pool_min: int, pool_capacity: int | None, debug: bool,
+               append_capacity: int = 0):
     """``skv_index_desc`` of a :class:`SeoulKV4Index`.  Returns ``(desc, keep)``;
     the numpy arrays in ``keep`` back the descriptor's pointers and must
     outlive every call that reads it."""
@@ -142,6 +146,7 @@ def index_desc(index, *, pool_min: int, pool_capacity: int | None, debug: bool):
     desc.pool_min = int(pool_min)
     desc.pool_capacity = int(pool_capacity or 0)
     desc.debug = int(bool(debug))
+    desc.append_capacity = int(append_capacity)
     for g, cell in enumerate(cells):
         arrays = dict(
             upper=_np(cell["upper"], np.uint8),
@@ -165,10 +170,11 @@ class Runtime:
     """One device instance of the decode path (the reference's ``state``)."""
 
     def __init__(self, device: int, k: torch.Tensor, v: torch.Tensor, index, *,
-                 pool_min: int, pool_capacity: int | None, debug: bool, stream=None):
+                 pool_min: int, pool_capacity: int | None, debug: bool, stream=None,
+                 append_capacity: int = 0):
         self.lib = load_library()
         desc, keep = index_desc(index, pool_min=pool_min, pool_capacity=pool_capacity,
-                                debug=debug)
+                                debug=debug, append_capacity=append_capacity)
         kb = _np(k, np.uint16)
         vb = _np(v, np.uint16)
         handle = ctypes.c_void_p()
@@ -182,7 +188,8 @@ class Runtime:
         self.handle = handle
         self.device = int(device)
         self.nc = desc.n_centroids
-        self.context = desc.context
+        self.context = desc.context  # prefill context: key records, pool bound
+        self.T = desc.context  # current context (grows with append)
         self.debug = bool(debug)
         self._qbuf = np.zeros((16, D), dtype=np.uint16)
 
@@ -241,6 +248,27 @@ class Runtime:
         self._check(self.lib.skv_output_device(self.handle, ctypes.byref(p)), "output")
         return int(p.value)
 
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Append n tokens: ``k``, ``v`` [4, n, 256] BF16, CPU (staged copy)
+        or on this device (read in place).  The local window grows by n."""
+        if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.shape != v.shape \
+                or k.dim() != 3 or k.shape[0] != G or k.shape[2] != D:
+            raise ValueError("expected BF16 K/V [4, n, 256] of one shape")
+        n = int(k.shape[1])
+        if k.device.type == "cpu" and v.device.type == "cpu":
+            kb, vb = _np(k, np.uint16), _np(v, np.uint16)
+            code = self.lib.skv_append(self.handle, _ptr(kb), _ptr(vb), n)
+        elif k.device == v.device and k.device.type == "cuda" and k.device.index == self.device:
+            k, v = k.contiguous(), v.contiguous()
+            torch.cuda.synchronize(self.device)  # k/v written by torch's streams
+            code = self.lib.skv_append_device(self.handle, k.data_ptr(), v.data_ptr(), n)
+            if code == 0:  # read on the handle's stream: keep k/v alive until done
+                self._check(self.lib.skv_sync(self.handle, None), "append sync")
+        else:
+            raise ValueError("K/V must both be CPU tensors or both on the runtime's device")
+        self._check(code, "append")
+        self.T += n
+
     def dense_decode(self) -> None:
         """Enqueue the dense FP8 decode of the bound query over all T keys
         (the comparison path; its output is separate from the step's)."""
@@ -274,7 +302,7 @@ class Runtime:
             "u1": (6400, np.int32), "s4": (H * 6400, np.uint16), "u2": (1024, np.int32),
             "s8": (H * 1024, np.uint16), "top": (H * TOPK, np.int32),
             "qprep": (3 * H * 260, np.int32), "keyrec": (T * 256, np.uint8),
-            "kv8": (T * 512, np.uint8), "kscale": (D, np.float32),
+            "kv8": (self.T * 512, np.uint8), "kscale": (D, np.float32),
         }
         cap, dtype = caps[name]
         buf = np.zeros(cap, dtype=dtype)

@@ -53,6 +53,8 @@ class SeoulKV4:
             ):
                 raise ValueError(f"expected CPU BF16 {name} [4,{context},256]")
         index._check_keys(k)
+        if context + self._config.append_capacity > MAX_CONTEXT:
+            raise ValueError("context plus append_capacity exceeds 2^20 tokens")
         self._device = ordinal
         self._index = index
         self._host_kv = (k, v)
@@ -98,6 +100,7 @@ class SeoulKV4:
             pool_capacity=self._args.stage15_capacity,
             debug=self._args.debug,
             stream=stream or None,
+            append_capacity=self._config.append_capacity,
         )
         try:
             # First step is checked like the reference's initialisation
@@ -143,6 +146,18 @@ class SeoulKV4:
             self._host_kv = None
         self._bind_query(q)
         return self._run_bound()
+
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Append ``n`` decoded tokens to the cache: ``k``, ``v`` [4, n, 256]
+        BF16 post-RoPE keys and values, on the CPU or on this device.  Later
+        runs attend them densely with the local window (which grows by n);
+        the index, its retrieval region and the key codec stay the prefill's.
+        Requires ``SeoulKV4Config(append_capacity=...)`` and an initialised
+        instance; raises, the cache unchanged, when the capacity is exceeded."""
+        state = self._require_initialized()
+        if self._config.append_capacity == 0:
+            raise RuntimeError("append requires SeoulKV4Config(append_capacity > 0)")
+        state.append(k, v)
 
     def synchronize(self) -> None:
         """Wait for enqueued work; raise if a step reported a pool error."""

@@ -1,11 +1,13 @@
 """Configuration of the single-cache sparse decode profile.
 
-Mirrors the reference ``config.py:1-40``.  The one extension is
+Mirrors the reference ``config.py:1-40``.  Two extensions:
 ``stage15_capacity=None``: the reference caps the deduplicated candidate pool
 per KV group at 12288..24576 keys because its pool lives in Tensix L1.  On
 MI355X the pool lives in HBM and is sized for the worst case (every retrieval
 token), so ``None`` lifts the cap; an integer keeps the reference's
 "error, never truncate" capacity check bit for bit.
+``append_capacity``: tokens per KV head that ``SeoulKV4.append`` may add after
+the prefill (0, the default, is the reference's static cache).
 """
 
 from __future__ import annotations
@@ -32,10 +34,12 @@ MAX_CENTROIDS = 65536
 class SeoulKV4Config:
     """``stage15_capacity``: pool capacity per KV group (multiple of 768 in
     [12288, 24576], as in the reference) or ``None`` for an HBM-sized pool.
-    ``debug``: keep the final top-100 IDs readable via ``debug_snapshot``."""
+    ``debug``: keep the final top-100 IDs readable via ``debug_snapshot``.
+    ``append_capacity``: tokens per KV head ``append`` may add (0: static)."""
 
     stage15_capacity: int | None = 13056
     debug: bool = False
+    append_capacity: int = 0
 
     def __post_init__(self):
         n = self.stage15_capacity
@@ -48,6 +52,8 @@ class SeoulKV4Config:
             )
         if type(self.debug) is not bool:
             raise TypeError("debug must be a bool")
+        if type(self.append_capacity) is not int or not 0 <= self.append_capacity <= MAX_CONTEXT:
+            raise ValueError("append_capacity must be an int in [0, 2^20]")
 
 
 @dataclass(frozen=True)

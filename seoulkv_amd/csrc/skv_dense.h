@@ -17,9 +17,10 @@ constexpr int DN_TARGET_BLOCKS = 64;       // partials per KV group (upper bound
 constexpr int DN_MERGE_SLICES = 32;        // 8-dim output slices per query head in the merge
 
 struct DenseArgs {
-  const uint8_t* kv8;   // [G][T][512]: fp8 V | fp8 K
+  const uint8_t* kv8;   // [G][rows][512]: fp8 V | fp8 K
   const uint16_t* q;    // [16][256] bf16
-  int T;
+  int T;                // keys attended (rows 0 .. T-1 of each group)
+  int rows;             // records per group in kv8
   int iters;            // 16-key tiles per wave
   int nb;               // blocks (partials) per KV group
   float* part;          // [G][nb][H][D + 2]: unnormalised o, max (log2 units), sum

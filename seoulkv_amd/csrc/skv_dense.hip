@@ -182,7 +182,7 @@ __global__ __launch_bounds__(DN_BLOCK) void k_dense(DenseArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, kb = lane >> 4;
   const int T = a.T;
-  const uint8_t* __restrict__ kv = a.kv8 + (size_t)g * T * 512;
+  const uint8_t* __restrict__ kv = a.kv8 + (size_t)g * a.rows * 512;
   __shared__ float s_o[DN_WAVES][H][D];
   __shared__ float s_m[DN_WAVES][H], s_l[DN_WAVES][H];
 

@@ -456,12 +456,12 @@ struct MaskedTiles {
 template <typename TileSrc, typename IdFn>
 __device__ FastResult tiled_select(const TileSrc& src, const uint16_t* __restrict__ tmx,
                                    const uint32_t (&sv)[FS_PER], int n, int k, IdFn id,
-                                   FastScratch& s, int ts) {
+                                   FastScratch& s, bool force_miss, int ts) {
   // ---- 1. this thread's 4 tile bounds (loaded with the caller's sample)
   const int ntile = (n + 15) >> 4;
   const int t4 = 4 * (int)threadIdx.x;
   const uint2 tm = t4 < ntile ? *reinterpret_cast<const uint2*>(tmx + t4) : make_uint2(0, 0);
-  const uint32_t cut = fs_cut(sv, n, k, false, s, ts);
+  const uint32_t cut = fs_cut(sv, n, k, force_miss, s, ts);
   // ---- 2. the tiles whose max reaches the cut, listed in s.hist (free
   // until fs_finish)
   const uint32_t tv[4] = {tm.x & 0xffffu, tm.x >> 16, tm.y & 0xffffu, tm.y >> 16};

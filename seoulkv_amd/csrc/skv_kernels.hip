@@ -277,7 +277,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
   const int i = r * DENSE_BLOCK_KEYS + wave * SDPA_WAVE_KEYS + lane;
   if (lane < SDPA_WAVE_KEYS && i < ndense) tk = i < a.sink ? i : a.T - a.local + (i - a.sink);
   float m, l, o[4];
-  wave_attend(a.kv8 + (size_t)g * a.T * 512, q, tk, m, l, o);
+  wave_attend(a.kv8 + (size_t)g * a.kv_rows * 512, q, tk, m, l, o);
   stash_wave(s, m, l, o);
   __syncthreads();
   if (threadIdx.x < D) {
@@ -584,14 +584,14 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
     FastResult r{};
     r.ok = false;
-    if (a.exact_select == 0 && a.tmax_fi && nc / 16 <= 4 * SEL_BLOCK) {
+    if (a.tmax_fi && nc / 16 <= 4 * SEL_BLOCK) {
       // only the 16-centroid tiles whose max fine score reaches the cut can
       // hold a candidate: their scores and gates are loaded, no others
       uint32_t sv[FS_PER];
 #pragma unroll
       for (int u = 0; u < FS_PER; ++u) sv[u] = pg[u] >= thr ? pf[u] : 0u;
       r = tiled_select(MaskedTiles{fi, up, thr}, a.tmax_fi + ((size_t)g * H + h) * (nc / 16), sv, nc,
-                       a.P[g], cid, fs, 4);
+                       a.P[g], cid, fs, force, 4);
       __syncthreads();
     }
     if (!r.ok)
@@ -1058,14 +1058,14 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
       for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
     FastResult r{};
     r.ok = false;
-    if (t.tile_max && t.exact_select == 0 && n > OCT_ITEMS && (n + 15) / 16 <= 4 * SEL_BLOCK) {
+    if (t.tile_max && t.exact_select != 1 && n > OCT_ITEMS && (n + 15) / 16 <= 4 * SEL_BLOCK) {
       // the producer wrote the max of every 16-item tile: only the tiles
       // reaching the cut are read for candidates
       uint32_t sv[FS_PER];
 #pragma unroll
       for (int u = 0; u < FS_PER; ++u) sv[u] = sc[fs_sample_item(n, u)];
       r = tiled_select(RowTiles{sc}, t.tile_max + ((size_t)g * H + h) * t.tile_stride, sv, n, t.k,
-                       id, fs, ts);
+                       id, fs, t.exact_select == 2, ts);
       __syncthreads();
     }
     if (!r.ok) r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
@@ -1253,13 +1253,13 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
       v4i acc = {0, 0, 0, 0};
       if (U1) {
         uint32_t av[4][4] = {};
-        if (i_in < nloc) load_code4(a.keyrec + ((size_t)g * a.T + s_tok[i_in]) * 256, kb, av);
+        if (i_in < nloc) load_code4(a.keyrec + ((size_t)g * a.rec_rows + s_tok[i_in]) * 256, kb, av);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(av[kc], b[kc], acc);
       } else {
         uint32_t hi[4][4] = {}, lo[4][4] = {};
         if (i_in < nloc) {
-          const uint8_t* rec = a.keyrec + ((size_t)g * a.T + s_tok[i_in]) * 256;
+          const uint8_t* rec = a.keyrec + ((size_t)g * a.rec_rows + s_tok[i_in]) * 256;
           load_code4(rec, kb, hi);
           const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
           const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
@@ -1414,7 +1414,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
     const int i = wave + ATTN_WAVES * lane;
     if (i < m) tk = (int)(0xfffffu - (uint32_t)(s_key[i] & 0xfffffu));
   }
-  const AttnLoads<TOP_KPW> L = attend_load<TOP_KPW>(a.kv8 + (size_t)g * a.T * 512, tk);
+  const AttnLoads<TOP_KPW> L = attend_load<TOP_KPW>(a.kv8 + (size_t)g * a.kv_rows * 512, tk);
   // the output list, best first (member keys are distinct)
   int* out = a.top + j * TOPK;
   if ((int)threadIdx.x < m) {

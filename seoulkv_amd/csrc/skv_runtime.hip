@@ -46,6 +46,8 @@ struct Arena {
   }
 };
 
+constexpr int APPEND_CHUNK = 1024;  // tokens per host-append staging round
+
 struct Handle {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -58,6 +60,10 @@ struct Handle {
   StepArgs a{};
   StepWork w{};
   DenseArgs dn{};  // dense FP8 decode over every key (comparison path)
+  // cache append: tokens after the prefill context extend the local window
+  int context0 = 0, append_capacity = 0;
+  uint16_t* append_stage = nullptr;  // [2][G][APPEND_CHUNK][256] bf16 (host appends)
+  int n_centroids = 0, np_max = 0;
   bool dense_ran = false;
   bool bound = false, ran = false;
   size_t lds_per_block = 0;
@@ -75,6 +81,29 @@ struct Handle {
   hipGraphExec_t graph_exec = nullptr;
   std::string error, meta;
 };
+
+std::string json_escape(const std::string& s);
+
+// The handle's JSON metadata (context and local window as of the last append).
+void build_meta(Handle* h) {
+  const StepArgs& a = h->a;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, h->device) != hipSuccess) memset(&prop, 0, sizeof prop);
+  char buf[1024];
+  snprintf(buf, sizeof buf,
+           "{\"device\": \"%s\", \"arch\": \"%s\", \"context\": %d, \"sink\": %d, \"local\": %d, "
+           "\"n_centroids\": %d, \"nprobe\": [%d, %d, %d, %d], \"pool_buffer\": %d, "
+           "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
+           "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
+           "\"kernels_per_step\": %d, \"lds_per_block\": %zu, \"pool_lds_items\": %d, "
+           "\"prefill_context\": %d, \"appended\": %d, \"append_capacity\": %d}",
+           json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), a.T, a.sink,
+           a.local, h->n_centroids, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min,
+           a.pool_capacity, h->np_max, h->static_bytes, h->work_bytes, N_STEP_KERNELS,
+           h->lds_per_block, h->w.top_u1.lds_items, h->context0, a.T - h->context0,
+           h->append_capacity);
+  h->meta = buf;
+}
 
 // Drop the captured step (launch options changed).
 void drop_graph(Handle* h) {
@@ -151,15 +180,29 @@ __global__ void k_init_keyrec(const uint16_t* k, const float* kscale, int T, uin
   }
 }
 
-// FP8 [V || K] records: one thread per (group, token, dim).
-__global__ void k_init_kv8(const uint16_t* k, const uint16_t* v, int T, uint8_t* kv8) {
-  const size_t n = (size_t)G * T * D;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+// FP8 [V || K] records of n tokens: k, v [G][n][256] bf16 (rows of the
+// group g that are src_stride tokens apart) -> kv8 rows row0 .. row0+n-1 of
+// each group (rows records per group).  One thread per (group, token, 4 dims).
+__global__ void k_pack_kv8(const uint16_t* k, const uint16_t* v, int n, size_t src_stride,
+                           int row0, int rows, uint8_t* kv8) {
+  const size_t total = (size_t)G * n * (D / 4);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
-    const size_t gt = i / D;
-    const int d = (int)(i % D);
-    kv8[gt * 512 + d] = (uint8_t)f32_to_fp8_e4m3(bf16_f32(v[i]));
-    kv8[gt * 512 + 256 + d] = (uint8_t)f32_to_fp8_e4m3(bf16_f32(k[i]));
+    const int c = (int)(i % (D / 4));
+    const size_t gt = i / (D / 4);
+    const int g = (int)(gt / n), t = (int)(gt % n);
+    const size_t src = ((size_t)g * src_stride + t) * D + 4 * c;
+    const uint2 kw = *reinterpret_cast<const uint2*>(k + src);
+    const uint2 vw = *reinterpret_cast<const uint2*>(v + src);
+    auto pack = [](uint2 w) {
+      return f32_to_fp8_e4m3(bf16_f32(w.x & 0xffffu)) |
+             (f32_to_fp8_e4m3(bf16_f32(w.x >> 16)) << 8) |
+             (f32_to_fp8_e4m3(bf16_f32(w.y & 0xffffu)) << 16) |
+             (f32_to_fp8_e4m3(bf16_f32(w.y >> 16)) << 24);
+    };
+    uint8_t* rec = kv8 + ((size_t)g * rows + row0 + t) * 512;
+    *reinterpret_cast<uint32_t*>(rec + 4 * c) = pack(vw);
+    *reinterpret_cast<uint32_t*>(rec + 256 + 4 * c) = pack(kw);
   }
 }
 
@@ -251,6 +294,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     return fail(nullptr, SKV_EINVAL, "n_centroids %d must be a multiple of 32 in [32, 65536]", nc);
   if (ix->sink < 0 || ix->local < 0 || ix->sink + ix->local >= T)
     return fail(nullptr, SKV_EINVAL, "sink/local %d/%d do not fit context %d", ix->sink, ix->local, T);
+  if (ix->append_capacity < 0 || ix->append_capacity > (1 << 20) - T)
+    return fail(nullptr, SKV_EINVAL, "append capacity %d: context plus capacity above 2^20",
+                ix->append_capacity);
+  const int cap_app = ix->append_capacity;
   const int R = T - ix->sink - ix->local;
 
   // ---- host-side validation and the spill-2 mate table
@@ -322,6 +369,12 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
 
   StepArgs& a = h->a;
   a.T = T;
+  a.rec_rows = T;
+  a.kv_rows = T + cap_app;
+  h->context0 = T;
+  h->append_capacity = cap_app;
+  h->n_centroids = nc;
+  h->np_max = np_max;
   a.sink = ix->sink;
   a.local = ix->local;
   a.nc = nc;
@@ -343,7 +396,9 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   // per range
   a.pool_range = std::max(128, (nc / 64 + 31) / 32 * 32);
   a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
+  const int max_slices = (a.sink + a.local + cap_app + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
   h->dn.T = T;
+  h->dn.rows = T + cap_app;
   dense_shape(T, h->dn.iters, h->dn.nb);
   if (h->dn.nb > DN_TARGET_BLOCKS) {  // the merge kernel holds at most this many partials
     fail(h, SKV_EINVAL, "dense decode shape: %d blocks per group", h->dn.nb);
@@ -364,7 +419,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.post_mate = (int*)ar.take((size_t)G * np_max * 4);
     a.post_p2 = (uint8_t*)ar.take((size_t)G * np_max * 64);
     a.keyrec = (uint8_t*)ar.take((size_t)G * T * 256);
-    a.kv8 = (uint8_t*)ar.take((size_t)G * T * 512);
+    a.kv8 = (uint8_t*)ar.take((size_t)G * (T + cap_app) * 512);
   };
   plan_static(s);
   h->static_bytes = s.used;
@@ -396,7 +451,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
     a.s2_tmax = (uint16_t*)ar.take((size_t)G * H * (a.cap / 16) * 2);
-    a.dense_part = (float*)ar.take((size_t)G * H * std::max(a.dense_slices, 1) * (D + 2) * 4);
+    a.dense_part = (float*)ar.take((size_t)G * H * std::max(max_slices, 1) * (D + 2) * 4);
     a.selbm = (uint32_t*)ar.take((size_t)G * (nc / 32) * 4);  // cleared by k_front
     a.u1_tok = (int*)ar.take((size_t)G * U1_MAX * 4);
     a.s4 = (uint16_t*)ar.take((size_t)G * H * U1_MAX * 2);
@@ -407,8 +462,11 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.out = (uint16_t*)ar.take(16 * D * 2);
     a.bm_u1 = (uint64_t*)ar.take((size_t)G * H * words1 * 8);
     a.bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
-    h->dn.part = (float*)ar.take((size_t)G * h->dn.nb * H * (D + 2) * 4);
+    h->dn.part = (float*)ar.take((size_t)G * DN_TARGET_BLOCKS * H * (D + 2) * 4);  // any T
     h->dn.out = (uint16_t*)ar.take(16 * D * 2);
+    h->append_stage =
+        cap_app ? (uint16_t*)ar.take((size_t)2 * G * std::min(cap_app, APPEND_CHUNK) * D * 2)
+                : nullptr;
   };
   plan_work(wk);
   h->work_bytes = wk.used;
@@ -492,7 +550,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
                          sbits, (float*)a.kscale);
       hipLaunchKernelGGL(k_init_keyrec, dim3(8192), dim3(256), 0, h->stream, dk, a.kscale, T,
                          (uint8_t*)a.keyrec);
-      hipLaunchKernelGGL(k_init_kv8, dim3(8192), dim3(256), 0, h->stream, dk, dv, T, (uint8_t*)a.kv8);
+      hipLaunchKernelGGL(k_pack_kv8, dim3(8192), dim3(256), 0, h->stream, dk, dv, T, (size_t)T, 0,
+                         a.kv_rows, (uint8_t*)a.kv8);
       hipLaunchKernelGGL(k_init_postp2, dim3(4096), dim3(256), 0, h->stream, a.post_tok, a.keyrec, T,
                          np_max, dnp, (uint8_t*)a.post_p2);
       ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(h->stream) == hipSuccess;
@@ -533,19 +592,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     return bail(SKV_EHIP);
   }
 
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) != hipSuccess) memset(&prop, 0, sizeof prop);
-  char buf[1024];
-  snprintf(buf, sizeof buf,
-           "{\"device\": \"%s\", \"arch\": \"%s\", \"context\": %d, \"sink\": %d, \"local\": %d, "
-           "\"n_centroids\": %d, \"nprobe\": [%d, %d, %d, %d], \"pool_buffer\": %d, "
-           "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
-           "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
-           "\"kernels_per_step\": %d, \"lds_per_block\": %zu, \"pool_lds_items\": %d}",
-           json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), T, a.sink, a.local,
-           nc, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min, a.pool_capacity, np_max,
-           h->static_bytes, h->work_bytes, N_STEP_KERNELS, h->lds_per_block, w.top_u1.lds_items);
-  h->meta = buf;
+  build_meta(h);
   *handle_out = h;
   return SKV_OK;
 }
@@ -664,6 +711,62 @@ int skv_dense_decode(void* handle) {
   HIPCHK(h, hipGetLastError());
   h->dense_ran = true;
   return SKV_OK;
+}
+
+// Cache append: FP8 records of n new tokens at rows T .. T+n-1, then the
+// context and the local window grow by n (the index, the key codec and the
+// retrieval region are the prefill's).  k, v: [G][n][256] BF16, device
+// pointers when on_device, else host memory staged APPEND_CHUNK tokens at a
+// time.  Work already enqueued keeps the shape it was launched with.
+static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n, bool on_device) {
+  if (!h) return SKV_ESTATE;
+  if (!k || !v) return fail(h, SKV_EINVAL, "NULL K/V");
+  if (on_device && (((uintptr_t)k | (uintptr_t)v) & 7))
+    return fail(h, SKV_EINVAL, "device K/V must be 8-byte aligned");
+  StepArgs& a = h->a;
+  if (n < 1 || n > h->context0 + h->append_capacity - a.T)
+    return fail(h, SKV_EINVAL, "append of %d tokens: %d of the capacity %d left", n,
+                h->context0 + h->append_capacity - a.T, h->append_capacity);
+  HIPCHK(h, hipSetDevice(h->device));
+  if (on_device) {
+    hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * n * (D / 4) + 255) / 256)), dim3(256),
+                       0, h->stream, k, v, n, (size_t)n, a.T, a.kv_rows, (uint8_t*)a.kv8);
+    HIPCHK(h, hipGetLastError());
+  } else {
+    const int chunk = std::min(h->append_capacity, APPEND_CHUNK);
+    uint16_t* sk = h->append_stage;
+    uint16_t* sv = sk + (size_t)G * chunk * D;
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+      const int c = std::min(chunk, n - t0);
+      for (int g = 0; g < G; ++g) {  // pageable source: the copy returns once it is staged
+        HIPCHK(h, hipMemcpyAsync(sk + (size_t)g * c * D, k + ((size_t)g * n + t0) * D,
+                                 (size_t)c * D * 2, hipMemcpyHostToDevice, h->stream));
+        HIPCHK(h, hipMemcpyAsync(sv + (size_t)g * c * D, v + ((size_t)g * n + t0) * D,
+                                 (size_t)c * D * 2, hipMemcpyHostToDevice, h->stream));
+      }
+      hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * c * (D / 4) + 255) / 256)),
+                         dim3(256), 0, h->stream, sk, sv, c, (size_t)c, a.T + t0, a.kv_rows,
+                         (uint8_t*)a.kv8);
+      HIPCHK(h, hipGetLastError());
+    }
+  }
+  a.T += n;
+  a.local += n;
+  a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
+  h->dn.T = a.T;
+  dense_shape(a.T, h->dn.iters, h->dn.nb);
+  drop_graph(h);  // the step's launch shapes changed
+  build_meta(h);
+  return SKV_OK;
+}
+
+int skv_append(void* handle, const uint16_t* k_bf16, const uint16_t* v_bf16, int n) {
+  return append_tokens(static_cast<Handle*>(handle), k_bf16, v_bf16, n, false);
+}
+
+int skv_append_device(void* handle, const void* k_dev, const void* v_dev, int n) {
+  return append_tokens(static_cast<Handle*>(handle), static_cast<const uint16_t*>(k_dev),
+                       static_cast<const uint16_t*>(v_dev), n, true);
 }
 
 int skv_dense_output_device(void* handle, void** dev_ptr) {
@@ -865,11 +968,12 @@ int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t c
       return SKV_OK;
     }
     case SKV_STAGE_KEYREC: {
-      if (cap < (int64_t)a.T * 256) return fail(h, SKV_EINVAL, "stage buffer too small");
-      return copy_rows(a.keyrec + (size_t)group * a.T * 256, 0, 1, (int64_t)a.T * 256, 1);
+      if (cap < (int64_t)a.rec_rows * 256) return fail(h, SKV_EINVAL, "stage buffer too small");
+      return copy_rows(a.keyrec + (size_t)group * a.rec_rows * 256, 0, 1,
+                       (int64_t)a.rec_rows * 256, 1);
     }
     case SKV_STAGE_KV8:
-      return copy_rows(a.kv8 + (size_t)group * a.T * 512, 0, 1, (int64_t)a.T * 512, 1);
+      return copy_rows(a.kv8 + (size_t)group * a.kv_rows * 512, 0, 1, (int64_t)a.T * 512, 1);
     case SKV_STAGE_KSCALE:
       return copy_rows(a.kscale + group * D, 0, 4, D, 1);
     default:

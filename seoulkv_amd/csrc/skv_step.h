@@ -54,7 +54,9 @@ enum {
 
 struct StepArgs {
   // shapes
-  int T, sink, local, nc, np_max, cap;
+  int T, sink, local, nc, np_max, cap;  // T, local: current (grow with appended tokens)
+  int rec_rows;             // key records per group (the prefill context)
+  int kv_rows;              // FP8 records per group (prefill context + append capacity)
   int P[G];
   float lam[G];
   int pool_min, pool_capacity, debug;
@@ -75,8 +77,8 @@ struct StepArgs {
   const int* post_tok;      // [G][np_max]
   const int* post_mate;     // [G][np_max] (-1: no mate)
   const uint8_t* post_p2;   // [G][np_max][64]
-  const uint8_t* keyrec;    // [G][T][256]: p2 | r2 | r4 planes
-  const uint8_t* kv8;       // [G][T][512]: fp8 V | fp8 K
+  const uint8_t* keyrec;    // [G][rec_rows][256]: p2 | r2 | r4 planes
+  const uint8_t* kv8;       // [G][kv_rows][512]: fp8 V | fp8 K (rows < T valid)
   // per-step workspace
   QOperand* qop;            // [G][QV_COUNT]
   uint16_t* lower;          // [G][H][nc] ordered BF16

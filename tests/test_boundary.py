@@ -134,6 +134,8 @@ def test_api_host_validation():
     with pytest.raises(RuntimeError):
         runner.debug_snapshot()
     assert runner.metadata()["initialized"] is False
+    with pytest.raises(RuntimeError):
+        runner.append(k[:, :1], v[:, :1])  # append needs an initialised instance
     runner.close()
     runner.close()  # idempotent
     with pytest.raises(RuntimeError):
@@ -144,6 +146,10 @@ def test_config_and_index_validation():
     with pytest.raises((TypeError, ValueError)):
         SeoulKV4Config(stage15_capacity=100)
     assert SeoulKV4Config().stage15_capacity == 13056
+    assert SeoulKV4Config().append_capacity == 0  # the reference's static cache
+    for bad in (-1, 1.5, True, (1 << 20) + 1):
+        with pytest.raises(ValueError):
+            SeoulKV4Config(append_capacity=bad)
     k, v, _ = __import__("seoulkv_amd.synthetic", fromlist=["make_cache"]).make_cache(8192, 256)
     with pytest.raises(ValueError):
         SeoulKV4Index.build(k[:, :5000], v[:, :5000])  # below the minimum context

@@ -310,3 +310,34 @@ def test_sparse_output_tracks_dense_decode(step):
     cos = [float(out[j] @ dense[j] / np.linalg.norm(out[j]) / np.linalg.norm(dense[j]))
            for j in range(16)]
     assert min(cos) > 0.99
+
+
+def test_grown_cache_attends_appended_tokens(step):
+    """A cache grown by n appended tokens (context T0 + n, local L + n, the
+    prefill's codes and cells): the same top-100 as the prefill step, and
+    torch's SDPA over sink + [T0 - L, T0 + n) + top-100 -- every appended
+    token once, no retrieval token twice."""
+    _, _, _, q, traces, _ = step
+    cells, code8, scales, k8, v8 = oracle_inputs(**PARAMS)
+    n = 40
+    gen = torch.Generator().manual_seed(5)
+    kn = (torch.randn(4, n, 256, generator=gen) * 3).bfloat16()
+    vn = torch.randn(4, n, 256, generator=gen).bfloat16()
+    k8n, v8n = od.fp8_records(bits(kn), bits(vn))
+    k8g, v8g = np.concatenate([k8, k8n], 1), np.concatenate([v8, v8n], 1)
+    grown, out = od.decode_step(cells, code8, scales, k8g, v8g, bits(q).reshape(16, 256),
+                                sink=128, local=256 + n, context=8192 + n)
+    qf = q.reshape(16, 256).float()
+    for g in range(4):
+        np.testing.assert_array_equal(grown[g].top100, traces[g].top100)
+    for j in (0, 7, 13):
+        g, h = divmod(j, 4)
+        ids = od.attention_ids(8192 + n, 128, 256 + n, grown[g].top100[h])
+        assert set(range(8192, 8192 + n)) <= set(ids.tolist())
+        assert len(set(ids.tolist())) == len(ids) == 128 + 256 + n + 100
+        kk = torch.from_numpy(k8g[g][ids]).double()[None, None]
+        vv = torch.from_numpy(v8g[g][ids]).double()[None, None]
+        want = torch.nn.functional.scaled_dot_product_attention(
+            qf[j].double()[None, None, None], kk, vv
+        )[0, 0, 0].numpy()
+        assert np.allclose(out[j], want, rtol=1e-12, atol=1e-12)
