@@ -238,6 +238,13 @@ __device__ __forceinline__ void expand2(uint32_t w, uint32_t out[4]) {
 #pragma unroll
   for (int m = 0; m < 4; ++m) out[m] = spread2((w >> (8 * m)) & 0xffu);
 }
+// The same 16 codes in the byte-transposed order of the 2-bit operand images
+// (QV_RAW, QV_Q15): word j byte m = code 4m + j, i.e. bits 2j.. of every
+// byte; one shift and one mask per word.
+__device__ __forceinline__ void expand2t(uint32_t w, uint32_t out[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[j] = (w >> (2 * j)) & 0x03030303u;
+}
 // 8 little-endian 4-bit codes of w -> 2 words of 4 byte-codes each.
 __device__ __forceinline__ void expand4(uint32_t w, uint32_t out[2]) {
 #pragma unroll

@@ -67,12 +67,18 @@ __device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, Q
   if (h < H) prep_head(a, g, v, s, out, h, lane, qw);
   __syncthreads();
   // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
-  // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.
+  // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.  The
+  // 2-bit variants (QV_RAW, QV_Q15) transpose the 4 x 4 bytes of a lane's
+  // chunk, dim = .. + 4 byte + m, to match expand2t's A words (the MFMA pairs
+  // A and B bytes by position, so one permutation of both keeps every dot).
+  const bool tr = v != QV_QS;
   for (int w = threadIdx.x; w < 4 * WAVE * 4; w += blockDim.x) {
     const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
     const int col = l & 15, hh = col >> 2, limb = col & 3;
-    const int4 x4 = *reinterpret_cast<const int4*>(&s.X[hh][(l >> 4) * 64 + kc * 16 + 4 * m]);
-    const int xs[4] = {x4.x, x4.y, x4.z, x4.w};
+    const int* xrow = &s.X[hh][(l >> 4) * 64 + kc * 16];
+    int xs[4];
+#pragma unroll
+    for (int byte = 0; byte < 4; ++byte) xs[byte] = tr ? xrow[4 * byte + m] : xrow[4 * m + byte];
     uint32_t word = 0;
 #pragma unroll
     for (int byte = 0; byte < 4; ++byte) {
@@ -344,8 +350,8 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
     uint32_t eu[4], el[4], a4[4];
-    expand2(up[kc], eu);
-    expand2(lo[kc], el);
+    expand2t(up[kc], eu);
+    expand2t(lo[kc], el);
 #pragma unroll
     for (int m = 0; m < 4; ++m) a4[m] = (eu[m] << 2) | el[m];
     acc_c = mfma_i8(eu, b[kc], acc_c);
@@ -981,7 +987,7 @@ __global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         uint32_t av[4];
-        expand2(words[kc], av);
+        expand2t(words[kc], av);
         acc = mfma_i8(av, bq[kc], acc);
       }
       int64_t dot[4];
