@@ -265,33 +265,39 @@ __device__ __forceinline__ v4i mfma_i8(const uint32_t a[4], const uint32_t b[4],
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
 }
 
-// Reduce the limb columns of an MFMA accumulator to one exact dot per
-// (key, head).  Lane l holds rows 4*(l/16)+r, column l%16 = 4*head + limb.
-// After the call, lanes with (l % 4) == 0 hold in out[r] the sum
-// L0 + 256 L1 + 65536 L2 for head (l%16)/4 and key row 4*(l/16) + r.
-__device__ __forceinline__ void combine_limbs(v4i acc, int64_t out[4]) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int v0 = acc[r];
-    const int v1 = __builtin_amdgcn_update_dpp(0, v0, 0x101, 0xf, 0xf, true);  // row_shl:1
-    const int v2 = __builtin_amdgcn_update_dpp(0, v0, 0x102, 0xf, 0xf, true);  // row_shl:2
-    out[r] = (int64_t)v0 + ((int64_t)v1 << 8) + ((int64_t)v2 << 16);
-  }
-}
-
-// After combine_limbs: the quad's first lane holds rows 4 (l/16) + r of its
-// column's head in out[r]; returns, in every lane, row 4 (l/16) + (l % 4) of
-// that head (the quad's 4 rows spread over its 4 lanes).
-__device__ __forceinline__ int64_t quad_spread(const int64_t out[4]) {
+// The 16 x 16 int32 tile of an int8 MFMA whose columns are (head, limb)
+// pairs (column 4 head + limb, limb 3 zero): returns, in lane l, the exact
+// dot of row 4 (l / 16) + (l % 4) for head (l % 16) / 4, the sum of its
+// limbs << 8 limb.  Lane = limb and register = row within a quad, so a 4 x 4
+// transpose of the quad (two exchange rounds: lanes q, q ^ 2 swap the
+// off-diagonal 2 x 2 blocks, then lanes q, q ^ 1 the off-diagonal entries of
+// each block) gives each lane the limbs of its own row.
+__device__ __forceinline__ int64_t limb_rows(v4i acc) {
   const int q = threadIdx.x & 3;
-  int64_t d = 0;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)out[r], 0x00, 0xf, 0xf, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(out[r] >> 32), 0x00, 0xf, 0xf, false);
-    if (r == q) d = (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);  // quad_perm [0,0,0,0]
+  int x0 = acc[0], x1 = acc[1], x2 = acc[2], x3 = acc[3];
+  const bool top = q < 2;
+  int s0 = top ? x2 : x0, s1 = top ? x3 : x1;
+  int r0 = __builtin_amdgcn_update_dpp(0, s0, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  int r1 = __builtin_amdgcn_update_dpp(0, s1, 0x4E, 0xf, 0xf, false);
+  if (top) {
+    x2 = r0;
+    x3 = r1;
+  } else {
+    x0 = r0;
+    x1 = r1;
   }
-  return d;
+  const bool even = (q & 1) == 0;
+  s0 = even ? x1 : x0;
+  s1 = even ? x3 : x2;
+  r0 = __builtin_amdgcn_update_dpp(0, s0, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+  r1 = __builtin_amdgcn_update_dpp(0, s1, 0xB1, 0xf, 0xf, false);
+  if (even) {
+    x1 = r0;
+  } else {
+    x0 = r0;
+    x2 = r1;
+  }
+  return (int64_t)x0 + ((int64_t)x1 << 8) + ((int64_t)x2 << 16);
 }
 
 }  // namespace skv

@@ -357,12 +357,9 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
     acc_c = mfma_i8(eu, b[kc], acc_c);
     acc_f = mfma_i8(a4, b[kc], acc_f);
   }
-  int64_t dc[4], df[4];
-  combine_limbs(acc_c, dc);
-  combine_limbs(acc_f, df);
   // lane (kb, h, q) converts centroid 4kb + q of the tile for head h
   const int h = (lane & 15) >> 2, q = lane & 3;
-  const int64_t dcq = quad_spread(dc), dfq = quad_spread(df);
+  const int64_t dcq = limb_rows(acc_c), dfq = limb_rows(acc_f);
   const int64_t S = sq.sum[h];
   const int fx = sq.fx[h];
   const float res = q == 0 ? t.rs.x : q == 1 ? t.rs.y : q == 2 ? t.rs.z : t.rs.w;
@@ -990,11 +987,9 @@ __global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
         expand2t(words[kc], av);
         acc = mfma_i8(av, bq[kc], acc);
       }
-      int64_t dot[4];
-      combine_limbs(acc, dot);  // rows 4kb + r of head h, in the quad's first lane
       // lane (kb, h, q) scores row 4kb + q of head h: every lane converts one
       const int q = lane & 3;
-      const int64_t dq = quad_spread(dot);
+      const int64_t dq = limb_rows(acc);
       const int ii = tile * 16 + 4 * kb + q;
       const uint32_t o = ii < n ? ordered16(bf16_rne(scaled_f32(2 * dq - 3 * S, fx))) : 0u;
       if (ii < n) s2[(size_t)h * a.cap + ii] = (uint16_t)o;
@@ -1284,10 +1279,7 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
         }
         // 8-bit dot = 16 x (code4 dot) + (residual-4 dot); lane (kb, h, q)
         // converts key 4kb + q of the tile for head h
-        int64_t dh[4], dl[4];
-        combine_limbs(acc, dh);
-        combine_limbs(acc_lo, dl);
-        const int64_t dhq = quad_spread(dh), dlq = quad_spread(dl);
+        const int64_t dhq = limb_rows(acc), dlq = limb_rows(acc_lo);
         const int h = (lane & 15) >> 2;
         const int i = tile * 16 + 4 * kb + (lane & 3), o = base + i;
         if (i < nloc && o < cap_out)
@@ -1295,10 +1287,8 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
               bf16_rne(scaled_f32(2 * (16 * dhq + dlq) - 255 * q->sum[h], q->fx[h])));
         continue;
       }
-      int64_t dot[4];
-      combine_limbs(acc, dot);
       // lane (kb, h, q) converts key 4kb + q of the tile for head h
-      const int64_t dq = quad_spread(dot);
+      const int64_t dq = limb_rows(acc);
       const int h = (lane & 15) >> 2;
       const int i = tile * 16 + 4 * kb + (lane & 3), o = base + i;
       if (i < nloc && o < cap_out)
