@@ -346,17 +346,18 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
   const int nc = a.nc, kb = lane >> 4;
   const uint32_t up[4] = {t.wu.x, t.wu.y, t.wu.z, t.wu.w};
   const uint32_t lo[4] = {t.wl.x, t.wl.y, t.wl.z, t.wl.w};
-  v4i acc_c = {0, 0, 0, 0}, acc_f = {0, 0, 0, 0};
+  // the 4-bit code is 4 upper + lower, so its dot is 4 (upper dot) + (lower
+  // dot), exact in each int32 limb column (|sum| <= 256 * 128 * 15)
+  v4i acc_c = {0, 0, 0, 0}, acc_l = {0, 0, 0, 0};
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
-    uint32_t eu[4], el[4], a4[4];
+    uint32_t eu[4], el[4];
     expand2t(up[kc], eu);
     expand2t(lo[kc], el);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) a4[m] = (eu[m] << 2) | el[m];
     acc_c = mfma_i8(eu, b[kc], acc_c);
-    acc_f = mfma_i8(a4, b[kc], acc_f);
+    acc_l = mfma_i8(el, b[kc], acc_l);
   }
+  const v4i acc_f = acc_c * 4 + acc_l;
   // lane (kb, h, q) converts centroid 4kb + q of the tile for head h
   const int h = (lane & 15) >> 2, q = lane & 3;
   const int64_t dcq = limb_rows(acc_c), dfq = limb_rows(acc_f);
