@@ -203,7 +203,9 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     stream = torch.cuda.Stream(dev)
-    config = SeoulKV4Config(stage15_capacity=None, debug=True, append_capacity=APPEND_TOKENS)
+    # token IDs stay below 2^20: at T = 2^20 (config 4) there is no room to append
+    n_append = min(APPEND_TOKENS, (1 << 20) - p.context)
+    config = SeoulKV4Config(stage15_capacity=None, debug=True, append_capacity=n_append)
     with torch.cuda.stream(stream):
         attn = SeoulKV4(device=dev, k=k, v=v, index=index, config=config)
         t0 = time.time()
@@ -261,26 +263,36 @@ def main() -> int:
         # cache append (after every measurement above: it grows the local
         # window): single-token host appends, one device append, then the
         # step over the grown window
-        half = APPEND_TOKENS // 2
-        kn, vn = k[:, -APPEND_TOKENS:].clone(), v[:, -APPEND_TOKENS:].clone()
-        attn.synchronize()
-        t = time.perf_counter()
-        for i in range(half):
-            attn.append(kn[:, i:i + 1], vn[:, i:i + 1])
-        attn.synchronize()
-        app_host_us = (time.perf_counter() - t) / half * 1e6
-        kd, vd = kn[:, half:].to(dev), vn[:, half:].to(dev)
-        t = time.perf_counter()
-        attn.append(kd, vd)
-        app_dev_us = (time.perf_counter() - t) * 1e6
-        start.record(stream)
-        for _ in range(args.steps):
-            attn._run_bound()
-        end.record(stream)
-        end.synchronize()
-        grown_us = start.elapsed_time(end) / args.steps * 1e3
-        log(f"append: {app_host_us:.1f} µs per 1-token host append, {app_dev_us:.1f} µs for "
-            f"{APPEND_TOKENS - half} tokens from device; step after {APPEND_TOKENS}: {grown_us:.1f} µs")
+        append = None
+        if n_append >= 2:
+            half = n_append // 2
+            kn, vn = k[:, -n_append:].clone(), v[:, -n_append:].clone()
+            attn.synchronize()
+            t = time.perf_counter()
+            for i in range(half):
+                attn.append(kn[:, i:i + 1], vn[:, i:i + 1])
+            attn.synchronize()
+            app_host_us = (time.perf_counter() - t) / half * 1e6
+            kd, vd = kn[:, half:].to(dev), vn[:, half:].to(dev)
+            t = time.perf_counter()
+            attn.append(kd, vd)
+            app_dev_us = (time.perf_counter() - t) * 1e6
+            start.record(stream)
+            for _ in range(args.steps):
+                attn._run_bound()
+            end.record(stream)
+            end.synchronize()
+            grown_us = start.elapsed_time(end) / args.steps * 1e3
+            log(f"append: {app_host_us:.1f} µs per 1-token host append, {app_dev_us:.1f} µs for "
+                f"{n_append - half} tokens from device; step after {n_append}: {grown_us:.1f} µs")
+            append = {
+                "host_1token_us": round(app_host_us, 1),
+                "device_tokens": n_append - half,
+                "device_us": round(app_dev_us, 1),
+                "step_us_after": round(grown_us, 2),
+                "appended": n_append,
+                "note": "wall time incl. host sync; the step attends the grown local window",
+            }
 
     nbytes = kernel_bytes(status, p, p.n_centroids)
     total_bytes = sum(nbytes.values())
@@ -361,14 +373,7 @@ def main() -> int:
             "max_abs_vs_oracle": dense_err,
             "sparse_over_dense": round(ms_per_step / dn_ms, 3),
         },
-        "append": {
-            "host_1token_us": round(app_host_us, 1),
-            "device_tokens": APPEND_TOKENS - half,
-            "device_us": round(app_dev_us, 1),
-            "step_us_after": round(grown_us, 2),
-            "appended": APPEND_TOKENS,
-            "note": "wall time incl. host sync; the step attends the grown local window",
-        },
+        "append": append,
         "profiled_steps": n_prof,
         "stage_sizes": {k_: status[k_] for k_ in ("survivors", "selected", "pool", "u1", "u2")},
         "cpu_baseline": cpu,
