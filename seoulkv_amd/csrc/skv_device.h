@@ -229,30 +229,21 @@ __device__ __forceinline__ int block_excl_scan(int v, int* scratch, int* total) 
 }
 
 // ------------------------------------------------------- code expansion
-// Spread the four 2-bit codes of byte t into four bytes (values 0..3).
-__device__ __forceinline__ uint32_t spread2(uint32_t t) {
-  return (t | (t << 6) | (t << 12) | (t << 18)) & 0x03030303u;
-}
-// 16 little-endian 2-bit codes of w -> 4 words of 4 byte-codes each.
-__device__ __forceinline__ void expand2(uint32_t w, uint32_t out[4]) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) out[m] = spread2((w >> (8 * m)) & 0xffu);
-}
-// The same 16 codes in the byte-transposed order of the 2-bit operand images
-// (QV_RAW, QV_Q15): word j byte m = code 4m + j, i.e. bits 2j.. of every
-// byte; one shift and one mask per word.
+// 16 little-endian 2-bit codes of w in the byte-transposed order of the
+// query images: word j byte m = code 4m + j, i.e. bits 2j.. of every byte;
+// one shift and one mask per word.
 __device__ __forceinline__ void expand2t(uint32_t w, uint32_t out[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) out[j] = (w >> (2 * j)) & 0x03030303u;
 }
-// 8 little-endian 4-bit codes of w -> 2 words of 4 byte-codes each.
-__device__ __forceinline__ void expand4(uint32_t w, uint32_t out[2]) {
+// 16 little-endian 4-bit codes (8 in w0, 8 in w1) in the same order: word j
+// = nibbles j, 4 + j of w0 and j, 4 + j of w1 (codes j, 4 + j, 8 + j,
+// 12 + j); one byte permute gathers the two masked halves.
+__device__ __forceinline__ void expand4t(uint32_t w0, uint32_t w1, uint32_t out[4]) {
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    uint32_t v = (w >> (16 * m)) & 0xffffu;
-    uint32_t x = v & 0x0f0fu;          // nibbles 0, 2
-    uint32_t y = (v >> 4) & 0x0f0fu;   // nibbles 1, 3
-    out[m] = (x & 0xffu) | ((y & 0xffu) << 8) | ((x >> 8) << 16) | ((y >> 8) << 24);
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t a = (w0 >> (4 * j)) & 0x000f000fu, b = (w1 >> (4 * j)) & 0x000f000fu;
+    out[j] = __builtin_amdgcn_perm(b, a, 0x06040200u);  // a.b0, a.b2, b.b0, b.b2
   }
 }
 

@@ -67,18 +67,17 @@ __device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, Q
   if (h < H) prep_head(a, g, v, s, out, h, lane, qw);
   __syncthreads();
   // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
-  // col = l%16, dim = (l/16)*64 + kc*16 + 4m + byte; limb 3 is zero.  The
-  // 2-bit variants (QV_RAW, QV_Q15) transpose the 4 x 4 bytes of a lane's
-  // chunk, dim = .. + 4 byte + m, to match expand2t's A words (the MFMA pairs
-  // A and B bytes by position, so one permutation of both keeps every dot).
-  const bool tr = v != QV_QS;
+  // col = l%16, dim = (l/16)*64 + kc*16 + 4 byte + m (the 4 x 4 bytes of a
+  // lane's 16-dim chunk transposed, to match the A words of expand2t and
+  // expand4t: the MFMA pairs A and B bytes by position, so one permutation
+  // of both keeps every dot); limb 3 is zero.
   for (int w = threadIdx.x; w < 4 * WAVE * 4; w += blockDim.x) {
     const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
     const int col = l & 15, hh = col >> 2, limb = col & 3;
     const int* xrow = &s.X[hh][(l >> 4) * 64 + kc * 16];
     int xs[4];
 #pragma unroll
-    for (int byte = 0; byte < 4; ++byte) xs[byte] = tr ? xrow[4 * byte + m] : xrow[4 * m + byte];
+    for (int byte = 0; byte < 4; ++byte) xs[byte] = xrow[4 * byte + m];
     uint32_t word = 0;
 #pragma unroll
     for (int byte = 0; byte < 4; ++byte) {
@@ -1129,8 +1128,8 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
     uint32_t ep[4], er[4];
-    expand2(pw[kc], ep);
-    expand2(rw[kc], er);
+    expand2t(pw[kc], ep);
+    expand2t(rw[kc], er);
 #pragma unroll
     for (int m = 0; m < 4; ++m) out[kc][m] = (ep[m] << 2) | er[m];
   }
@@ -1267,10 +1266,7 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
           const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
           const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
-          for (int kc = 0; kc < 4; ++kc) {
-            expand4(rw[2 * kc], &lo[kc][0]);
-            expand4(rw[2 * kc + 1], &lo[kc][2]);
-          }
+          for (int kc = 0; kc < 4; ++kc) expand4t(rw[2 * kc], rw[2 * kc + 1], lo[kc]);
         }
         v4i acc_lo = {0, 0, 0, 0};
 #pragma unroll
