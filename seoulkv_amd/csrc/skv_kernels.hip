@@ -257,17 +257,26 @@ __device__ __forceinline__ void stash_wave(AttnScratch& s, float m, float l, con
 __device__ __forceinline__ void merge_waves(const AttnScratch& s, int d, float& M, float& L,
                                             float& O) {
   constexpr int NW = SEL_BLOCK / WAVE;
-  M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) M = fmaxf(M, s.m[w]);
-  L = 0.f;
-  O = 0.f;
+  // every LDS read issued before the first use (no per-wave branch); a wave
+  // without keys has m = -inf, l = o = 0 and weight exp(-inf) = 0
+  float mw[NW], lw[NW], ow[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    if (s.m[w] == -INFINITY) continue;
-    const float sc = __expf(s.m[w] - M);
-    L += s.l[w] * sc;
-    O += s.o[w][d] * sc;
+    mw[w] = s.m[w];
+    lw[w] = s.l[w];
+    ow[w] = s.o[w][d];
+  }
+  M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) M = fmaxf(M, mw[w]);
+  L = 0.f;
+  O = 0.f;
+  if (M == -INFINITY) return;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float sc = __expf(mw[w] - M);
+    L += lw[w] * sc;
+    O += ow[w] * sc;
   }
 }
 
