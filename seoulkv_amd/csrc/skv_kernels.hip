@@ -1156,7 +1156,7 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
 // of 512 threads per group over at most 100 words.
 constexpr int us_block(int stage) { return stage == 4 ? 1024 : 512; }
 constexpr int US_GRID_U1 = 64;  // blocks per group over the pool
-constexpr int US_GRID_U2 = 16;  // blocks per group over U1 (<= 100 words)
+constexpr int US_GRID_U2 = 32;  // blocks per group over U1 (<= 100 words; spans of >= US_CHUNK)
 
 template <int STAGE>
 __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
