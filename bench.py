@@ -33,6 +33,7 @@ from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 G_KV = 4  # KV heads of the layer
 APPEND_TOKENS = 128  # tokens appended after the measured steps (cache-append check)
+N_COLD = 10  # independent instances the cold-cache steps rotate over
 METRIC = "µs/layer decode step at T=128K (1 GPU); achieved HBM GB/s; top-100 ID match"
 
 
@@ -43,13 +44,16 @@ def log(msg: str) -> None:
 def kernel_bytes(status: dict, p, nc: int) -> dict:
     """Algorithmic HBM bytes of each kernel for one step (all 4 KV groups),
     from the live stage sizes.  Reads of each input once plus the outputs the
-    next stage needs."""
+    next stage needs.  Member bitmaps are (n + 63) / 64 words of 8 B per
+    (group, head) over a group's n items."""
     G, H = 4, 4
     sel = sum(status["selected"])
     scanned = sum(status["scanned"])
     pool = sum(status["pool"])
     u1 = sum(status["u1"])
     u2 = sum(status["u2"])
+    bm_pool = H * sum((n + 63) // 64 * 8 for n in status["pool"])  # top-1600 members
+    bm_u1 = H * sum((n + 63) // 64 * 8 for n in status["u1"])      # top-256 members
     return {
         # Q + key scales in (per block, from L2); both centroid planes, scale,
         # residual norm in; lower/upper bounds and fine scores out; three
@@ -68,19 +72,44 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         # posting indices and their 64 B prefix rows in; 2-bit scores out
         "score2": pool * (4 + 64 + H * 2),
         # pool scores in; member bitmaps out
-        "top1600": pool * H * 2 + G * H * pool // 8,
+        "top1600": pool * H * 2 + bm_pool,
         # member bitmaps + pool tokens in; U1 tokens, their 128 B (prefix |
         # residual-2) key rows in; U1 tokens and 4-bit scores out
-        "union_score4": G * H * pool // 8 + u1 * (4 + 4 + 128 + H * 2),
-        "top256": u1 * (4 + H * 2) + G * H * u1 // 8,
+        "union_score4": bm_pool + u1 * (4 + 4 + 128 + H * 2),
+        "top256": u1 * (4 + H * 2) + bm_u1,
         # member bitmaps + U1 tokens in; full 256 B key records in; U2 tokens
         # and 8-bit scores out
-        "union_score8": G * H * u1 // 8 + u2 * (4 + 4 + 256 + H * 2),
+        "union_score8": bm_u1 + u2 * (4 + 4 + 256 + H * 2),
         # U2 scores + tokens in, top-100 IDs out; the 100 FP8 [V||K] records of
         # each head, the sink/local slice partials in; BF16 output out
         "top100_sdpa": u2 * (4 + H * 2) + 16 * 100 * 4 + 16 * 100 * 512
         + 16 * ((p.sink + p.local + 255) // 256) * 258 * 4 + 16 * 256 * 2,
     }
+
+
+def kv_gather_bytes(top_ids, p) -> int:
+    """FP8 [V || K] record bytes the sparse SDPA gathers in one step: each KV
+    group's sink and local records once (read for its 4 query heads) plus the
+    distinct top-100 tokens of its heads (a token chosen by several heads of
+    a group is one record)."""
+    rec = 512
+    total = 0
+    for g in range(4):
+        ids = np.unique(np.asarray(top_ids[g]).ravel())
+        ids = ids[ids >= 0]
+        total += (p.sink + p.local + len(ids)) * rec
+    return int(total)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
@@ -117,7 +146,14 @@ def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
         t = time.perf_counter()
         od.dense_decode(kf, vf, qf)
         dt.append(time.perf_counter() - t)
-    dense_fp8 = od.dense_decode(k8, v8, qf)  # the GPU dense path's reference
+    # the same dense decode over the FP8-cast records (like-for-like bytes with
+    # the GPU's dense FP8 path, whose reference output it also is)
+    d8 = []
+    dense_fp8 = None
+    for _ in range(3):
+        t = time.perf_counter()
+        dense_fp8 = od.dense_decode(k8, v8, qf)
+        d8.append(time.perf_counter() - t)
     threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
     return {
         "value": statistics.median(times) * 1e6,
@@ -125,12 +161,22 @@ def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
         "cores": int(threads),
         "kind": "port",
         "sample": (
-            f"{len(times)} full sparse decode steps of the {len(times) and 'same'} config-2 "
-            "workload (numpy oracle: query prep, coarse, fine, pool, 2/4/8-bit scoring, "
-            "top-k, FP8 SDPA), median; prefill untimed"
+            f"{len(times)} full sparse decode steps of the same {args_config()} workload "
+            "(numpy oracle: query prep, coarse, fine, pool, 2/4/8-bit scoring, top-k, FP8 "
+            "SDPA), median; prefill untimed; `cores` = BLAS threads the oracle ran on"
         ),
+        "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model(),
         "dense_fp32_us": statistics.median(dt) * 1e6,
+        "dense_fp8_cast_us": statistics.median(d8) * 1e6,
     }, match, out, dense_fp8
+
+
+_CONFIG = {"name": "cfg2"}
+
+
+def args_config() -> str:
+    return _CONFIG["name"]
 
 
 def calibrate_copy(mib: int) -> int:
@@ -176,6 +222,7 @@ def main() -> int:
                     help="only copy MIB MiB device-to-device 5 times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    _CONFIG["name"] = args.config
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(
@@ -229,6 +276,34 @@ def main() -> int:
         torch.cuda.synchronize()
         ms_per_step = start.elapsed_time(end) / args.steps
         log(f"device time {ms_per_step * 1e3:.1f} µs/step over {args.steps} steps")
+
+        # cold cache: steps rotate over N_COLD instances of the same cache, each
+        # with its own device copy of the index, key rows and FP8 records, so
+        # the ~30-40 MB a step touches was last read N_COLD - 1 steps (over
+        # 300 MB) earlier and is no longer in the L2s or the 256 MB MALL, as
+        # for a decoder that visits every other layer between two steps of
+        # this one
+        cold = [attn]
+        cold_cfg = SeoulKV4Config(stage15_capacity=None)
+        for _ in range(N_COLD - 1):
+            inst = SeoulKV4(device=dev, k=k, v=v, index=index, config=cold_cfg)
+            inst.run(q)
+            cold.append(inst)
+        for inst in cold:
+            inst._run_bound()
+        torch.cuda.synchronize()
+        n_cold = max(N_COLD, (args.steps // N_COLD) * N_COLD)
+        start.record(stream)
+        for i in range(n_cold):
+            cold[i % N_COLD]._run_bound()
+        end.record(stream)
+        end.synchronize()
+        cold_ms = start.elapsed_time(end) / n_cold
+        for inst in cold[1:]:
+            inst.close()
+        del cold
+        log(f"cold-cache device time {cold_ms * 1e3:.1f} µs/step over {n_cold} steps "
+            f"({N_COLD} instances)")
 
         # host-inclusive: 8 KiB H2D query bind + enqueue per step
         t = time.perf_counter()
@@ -294,6 +369,8 @@ def main() -> int:
                 "note": "wall time incl. host sync; the step attends the grown local window",
             }
 
+    gather_bytes = kv_gather_bytes(top_gpu, p)
+    gather_us = alone_ms["top100_sdpa"] * 1e3
     nbytes = kernel_bytes(status, p, p.n_centroids)
     total_bytes = sum(nbytes.values())
     dominant = max(alone_ms, key=alone_ms.get)
@@ -348,6 +425,8 @@ def main() -> int:
         },
         "step_hbm_bytes": int(total_bytes),
         "step_hbm_GBps": round(total_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "value_cold": round(cold_ms * 1e3, 2),
+        "cold_instances": N_COLD,
         "top100_match": match,
         "host_inclusive_us": round(host_us, 2),
         "roofline": {
@@ -362,6 +441,17 @@ def main() -> int:
             "bytes_per_launch": int(nbytes.get(dominant, 0)),
         },
         "kernels": per_kernel,
+        "kv_gather": {
+            "bytes": gather_bytes,
+            "kernel": "top100_sdpa",
+            "us": round(gather_us, 2),
+            "GB/s": round(gather_bytes / (gather_us * 1e-6) / 1e9, 1),
+            "frac": round(gather_bytes / (gather_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "unique sink/local + top-100 FP8 records of each KV group; the "
+                    "sink/local part is gathered by extra blocks of the select launch "
+                    "while the centroid selections run, the top-100 part by k_top100 "
+                    "after its selection; time = k_top100 alone",
+        },
         "dense_fp8": {
             "us": round(dn_ms * 1e3, 2),
             "kernel_us": round(dn_kernel_ms * 1e3, 2),

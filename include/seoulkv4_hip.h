@@ -7,9 +7,9 @@
  *   src/seoulkv4/_runtime.py:189  enqueue(state)
  *   src/seoulkv4/_runtime.py:197  metadata(state)
  * plus the device reads done by the public API:
- *   src/seoulkv4/api.py:112       synchronize()
+ *   src/seoulkv4/api.py:104       synchronize()
  *   src/seoulkv4/result.py:30     DecodeResult.to_torch()
- *   src/seoulkv4/api.py:127       debug_snapshot()
+ *   src/seoulkv4/api.py:119       debug_snapshot()
  *
  * Plain pointers and sizes only.  Host arrays are read during the call and not
  * retained.  Every function returns 0 on success or a SKV_E* code; after a
@@ -83,14 +83,21 @@ int skv_create(const skv_index_desc *index, const uint16_t *k_bf16,
  * (query head j belongs to KV head j/4) to the device, asynchronously. */
 int skv_bind_query(void *handle, const uint16_t *q_bf16);
 
-/* Device-resident variant: q_dev is a device pointer to [16][256] BF16. */
-int skv_bind_query_device(void *handle, const void *q_dev);
+/* Device-resident variant: q_dev is a device pointer to [16][256] BF16,
+ * written by work on producer_stream (a hipStream_t; NULL = the legacy default
+ * stream).  The 8 KiB copy is enqueued on producer_stream after the handle's
+ * steps enqueued so far (they read the query buffer), and the handle's stream
+ * waits for it, so the next skv_enqueue sees this query.  q_dev must stay valid
+ * until producer_stream reaches the copy (stream-ordered lifetime, as for a
+ * tensor used on its own stream).  Pass the handle's own stream to copy there
+ * without events. */
+int skv_bind_query_device(void *handle, const void *q_dev, void *producer_stream);
 
 /* Reference enqueue (_runtime.py:189-194): launches every stage of one decode
  * step on the handle's stream.  No host synchronisation, no readback. */
 int skv_enqueue(void *handle);
 
-/* Reference synchronize (api.py:112-115).  Waits for the stream and, if
+/* Reference synchronize (api.py:104-107).  Waits for the stream and, if
  * status is non-NULL, stores the per-group device status words [4][8]:
  * 0 pool size, 1 error code (0, 4 pool above capacity, 5 pool below the
  * minimum, 7 pool kernel wait abandoned), 2 selected clusters, 3 coarse survivors, 4 |U1|, 5 |U2|,
@@ -104,7 +111,7 @@ int skv_output_device(void *handle, void **dev_ptr);
 /* Reference DecodeResult.to_torch (result.py:30-38): sync + copy [16][256]. */
 int skv_read_output(void *handle, uint16_t *host_out);
 
-/* Reference debug_snapshot (api.py:127-134): sync + copy final token IDs
+/* Reference debug_snapshot (api.py:119-126): sync + copy final token IDs
  * [4 groups][4 heads][100], best first. */
 int skv_debug_ids(void *handle, uint32_t *host_out);
 
@@ -175,7 +182,9 @@ int skv_profile(void *handle, int enable);
  * a cut estimated from a 4096-item sample and falls back to the full
  * selection when the sample misses; both give identical results.  exact = 1
  * always runs the full selection; exact = 2 (tests) makes every sampled cut
- * miss so the fallback runs; 0 restores the default.  Status word 7 of each group (see skv_sync)
+ * miss so the fallback runs; exact = 3 (tests) runs the full selections with
+ * the token top-k scores never held in LDS, so their in-memory radix passes
+ * run at every pool size; 0 restores the default.  Status word 7 of each group (see skv_sync)
  * records, one bit per stage (1 thresh, 2 fine select, 4 top-1600, 8 top-256,
  * 16 top-100), which selections of the last step took the full path. */
 int skv_select_mode(void *handle, int exact);
@@ -203,7 +212,7 @@ const char *skv_kernel_name(int i);
 /* Reference metadata (_runtime.py:197-454), as a JSON text. */
 const char *skv_metadata(void *handle);
 
-/* Releases every device buffer of the handle (reference close, api.py:136). */
+/* Releases every device buffer of the handle (reference close, api.py:128-137). */
 void skv_destroy(void *handle);
 
 /* Text of the last error of this handle (or of the last failed create when

@@ -78,7 +78,7 @@ def load_library() -> ctypes.CDLL:
     sig = {
         "skv_create": (i32, [ctypes.POINTER(IndexDesc), vp, vp, i32, vp, ctypes.POINTER(vp)]),
         "skv_bind_query": (i32, [vp, vp]),
-        "skv_bind_query_device": (i32, [vp, vp]),
+        "skv_bind_query_device": (i32, [vp, vp, vp]),
         "skv_enqueue": (i32, [vp]),
         "skv_sync": (i32, [vp, vp]),
         "skv_output_device": (i32, [vp, ctypes.POINTER(vp)]),
@@ -132,17 +132,19 @@ def _np(t: torch.Tensor, dtype) -> np.ndarray:
 
 def index_desc(index, *, pool_min: int, pool_capacity: int | None, debug: bool,
                append_capacity: int = 0):
-    """``skv_index_desc`` of a :class:`SeoulKV4Index`.  Returns ``(desc, keep)``;
-    the numpy arrays in ``keep`` back the descriptor's pointers and must
-    outlive every call that reads it."""
-    cells = index.cells
-    zones = index.zones
+    """``skv_index_desc`` of an index: this package's :class:`SeoulKV4Index`
+    (``cells`` / ``zones``) or the reference's (``_cells`` / ``_zones``,
+    reference ``index.py:41-56``; both hold the same cell dictionaries).
+    Returns ``(desc, keep)``; the numpy arrays in ``keep`` back the
+    descriptor's pointers and must outlive every call that reads it."""
+    cells = index.cells if hasattr(index, "cells") else index._cells
+    zones = index.zones if hasattr(index, "zones") else index._zones
     keep = []
     desc = IndexDesc()
-    desc.context = zones.context
-    desc.sink = zones.sink
-    desc.local = zones.local
-    desc.n_centroids = len(cells[0]["centroids"])
+    desc.context = int(zones.context)
+    desc.sink = int(zones.sink)
+    desc.local = int(zones.local)
+    desc.n_centroids = int(cells[0]["offsets"].numel()) - 1
     desc.pool_min = int(pool_min)
     desc.pool_capacity = int(pool_capacity or 0)
     desc.debug = int(bool(debug))
@@ -206,11 +208,20 @@ class Runtime:
         self._check(self.lib.skv_bind_query(self.handle, _ptr(self._qbuf)), "bind_query")
 
     def bind_query_device(self, q_dev: torch.Tensor) -> None:
-        """Device-resident Q [16, 256] BF16 on this device."""
+        """Device-resident Q [16, 256] BF16 on this device, written by work on
+        PyTorch's current stream: the library copies it on that stream (after
+        the writes and after this instance's earlier steps), and its own
+        stream waits for the copy.  A temporary (``.contiguous()``) may be
+        freed on return: the copy is ordered on its stream."""
         if q_dev.device.type != "cuda" or q_dev.dtype != torch.bfloat16 or q_dev.numel() != 16 * D:
             raise ValueError("expected a device BF16 Q with 16 x 256 elements")
+        if q_dev.device.index is not None and q_dev.device.index != self.device:
+            raise ValueError(f"Q is on {q_dev.device}, the instance on cuda:{self.device}")
         q_dev = q_dev.contiguous()
-        self._check(self.lib.skv_bind_query_device(self.handle, q_dev.data_ptr()), "bind_query")
+        producer = torch.cuda.current_stream(q_dev.device).cuda_stream
+        self._check(self.lib.skv_bind_query_device(self.handle, q_dev.data_ptr(),
+                                                   ctypes.c_void_p(producer or None)),
+                    "bind_query")
 
     def time_kernel(self, kernel: int, reps: int = 50) -> float:
         """Mean milliseconds of step kernel ``kernel`` launched ``reps`` times

@@ -207,25 +207,46 @@ __device__ __forceinline__ int wave_max(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
-// Exclusive block scan of one int per thread; returns the exclusive prefix
-// and stores the block total in *total.  scratch: >= blockDim/64 + 1 ints.
-__device__ __forceinline__ int block_excl_scan(int v, int* scratch, int* total) {
+// Unsigned inclusive wave scan (sums modulo 2^32, the same DPP pattern).
+__device__ __forceinline__ unsigned wave_incl_scan_u(unsigned v) {
+  v +=(unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+  v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+  return v;
+}
+
+// Exclusive block scan of one value per thread; returns the exclusive prefix
+// and stores the block total in *total.  scratch: >= blockDim/64 + 1 words.
+// T = int, or unsigned for packed fields whose sums may pass 2^31.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan_t(T v, T* scratch, T* total) {
   const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
   const int nw = (blockDim.x + WAVE - 1) / WAVE;
-  int inc = wave_incl_scan(v);
+  auto scan = [](T x) -> T {
+    if constexpr (sizeof(T) == 4 && T(-1) > T(0)) return wave_incl_scan_u(x);
+    else return wave_incl_scan(x);
+  };
+  T inc = scan(v);
   if (lane == WAVE - 1) scratch[wave] = inc;
   __syncthreads();
   if (wave == 0) {
-    int w = lane < nw ? scratch[lane] : 0;
-    int winc = wave_incl_scan(w);
+    T w = lane < nw ? scratch[lane] : T(0);
+    T winc = scan(w);
     if (lane < nw) scratch[lane] = winc - w;
     if (lane == nw - 1) scratch[nw] = winc;
   }
   __syncthreads();
-  int res = inc - v + scratch[wave];
+  T res = inc - v + scratch[wave];
   *total = scratch[nw];
   __syncthreads();
   return res;
+}
+
+__device__ __forceinline__ int block_excl_scan(int v, int* scratch, int* total) {
+  return block_excl_scan_t<int>(v, scratch, total);
 }
 
 // ------------------------------------------------------- code expansion

@@ -646,6 +646,13 @@ __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint
 constexpr int PL_BLOCK = 1024;  // pool: one posting per thread and page, one block per CU
 constexpr int PL_WAVES = PL_BLOCK / WAVE;
 constexpr int PL_RANGE_MAX = PL_BLOCK;  // centroids per pool block: one per thread
+// The range scan packs (postings << PL_SEL_BITS) | selected into one unsigned
+// word: a range selects at most PL_RANGE_MAX clusters, and its postings are
+// fewer than 2^(32 - PL_SEL_BITS) = 2^21 (a group holds < 2^21 postings:
+// spill 2 over at most 2^20 tokens, checked by skv_create).
+constexpr int PL_SEL_BITS = 11;
+constexpr unsigned PL_SEL_MASK = (1u << PL_SEL_BITS) - 1u;
+static_assert(PL_RANGE_MAX <= (int)PL_SEL_MASK, "a range's selected count fits its scan field");
 constexpr int S2_BLOCK = 256;  // score2 threads per block
 constexpr int S2_GRID = 320;   // score2 blocks per group
 constexpr int S2_TILES = 2;    // 16-item tiles per wave and pass (loads issued together)
@@ -738,18 +745,19 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     if (lane == 0 && alive) atomicAdd(&s_surv, alive);
   }
   // the range's selected clusters in order and their posting offsets: one
-  // scan of (postings << 10 | selected) over the range's centroids
+  // scan of (postings << PL_SEL_BITS | selected) over the range's centroids
   const bool is_sel = t < ncr && ((s_bm[(c0 + t) >> 5] >> (t & 31)) & 1u);
-  const int size = is_sel ? s_off[t + 1] - s_off[t] : 0;
-  int tot;
-  const unsigned ex = (unsigned)block_excl_scan((size << 10) | (is_sel ? 1 : 0), s_scan, &tot);
-  const int nsel = (unsigned)tot & 1023u;
+  const unsigned size = is_sel ? (unsigned)(s_off[t + 1] - s_off[t]) : 0u;
+  unsigned tot;
+  const unsigned ex = block_excl_scan_t<unsigned>((size << PL_SEL_BITS) | (is_sel ? 1u : 0u),
+                                                  reinterpret_cast<unsigned*>(s_scan), &tot);
+  const int nsel = (int)(tot & PL_SEL_MASK);
   if (is_sel) {
-    const int r = ex & 1023u;
+    const int r = (int)(ex & PL_SEL_MASK);
     s_cl[r] = t;
-    s_cum[r] = (int)(ex >> 10);
+    s_cum[r] = (int)(ex >> PL_SEL_BITS);
   }
-  if (t == 0) s_cum[nsel] = (int)((unsigned)tot >> 10);
+  if (t == 0) s_cum[nsel] = (int)(tot >> PL_SEL_BITS);
   __syncthreads();
   const int S = s_cum[nsel];  // postings of the selected clusters
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;

@@ -54,6 +54,9 @@ struct Handle {
   bool own_stream = false;
   hipEvent_t q_copied = nullptr;
   uint16_t* q_host = nullptr;  // pinned staging for bind_query
+  // device-query binding on a producer stream: the handle's steps so far
+  // (readers of the query buffer) and the copy on the producer stream
+  hipEvent_t steps_done = nullptr, q_ready = nullptr;
   void* static_mem = nullptr;
   void* work_mem = nullptr;
   size_t static_bytes = 0, work_bytes = 0;
@@ -64,6 +67,7 @@ struct Handle {
   int context0 = 0, append_capacity = 0;
   uint16_t* append_stage = nullptr;  // [2][G][APPEND_CHUNK][256] bf16 (host appends)
   int n_centroids = 0, np_max = 0;
+  int top_u1_lds_items = 0, top_u2_lds_items = 0;  // LDS-resident sizes (select modes 0-2)
   bool dense_ran = false;
   bool bound = false, ran = false;
   size_t lds_per_block = 0;
@@ -272,6 +276,8 @@ void skv_destroy(void* handle) {
   if (!h) return;
   if (h->stream) (void)hipStreamSynchronize(h->stream);
   if (h->q_copied) (void)hipEventDestroy(h->q_copied);
+  if (h->steps_done) (void)hipEventDestroy(h->steps_done);
+  if (h->q_ready) (void)hipEventDestroy(h->q_ready);
   for (hipEvent_t e : h->prof_ev)
     if (e) (void)hipEventDestroy(e);
   drop_graph(h);
@@ -315,6 +321,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
       if (c.offsets[i + 1] < c.offsets[i])
         return fail(nullptr, SKV_EINVAL, "cell %d CSR offsets not monotone", g);
     np[g] = c.offsets[nc];
+    if (np[g] >= (1 << 21))  // the pool kernel's range scan holds posting counts in 21 bits
+      return fail(nullptr, SKV_EINVAL, "cell %d holds %d postings (at most 2^21 - 1)", g, np[g]);
     np_max = std::max(np_max, np[g]);
     std::vector<int> first_post(T, -1), first_cluster(T, -1), seen(T, 0);
     std::vector<int>& m = mates[g];
@@ -577,6 +585,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
                       std::min(lds_items, a.cap), 0, FS_TOP1600, a.s2_tmax, a.cap / 16};
   w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, a.bm_u2, words2, a.status, ST_U1, U1_MAX,
                       0, FS_TOP256, nullptr, 0};
+  h->top_u1_lds_items = w.top_u1.lds_items;
+  h->top_u2_lds_items = w.top_u2.lds_items;
   // Dynamic LDS of the selection kernels: the sampled-cut scratch, or the
   // LDS-resident scores of the full selection, or the attention scratch of
   // the sink/local blocks, whichever is largest (they are never live together).
@@ -587,7 +597,9 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   w.top_u2_lds = std::max(topk_bytes, (size_t)w.top_u2.lds_items * 2);
 
   if (hipHostMalloc((void**)&h->q_host, 16 * D * 2, hipHostMallocDefault) != hipSuccess ||
-      hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&h->steps_done, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&h->q_ready, hipEventDisableTiming) != hipSuccess) {
     fail(h, SKV_EHIP, "pinned query staging failed");
     return bail(SKV_EHIP);
   }
@@ -609,11 +621,25 @@ int skv_bind_query(void* handle, const uint16_t* q) {
   return SKV_OK;
 }
 
-int skv_bind_query_device(void* handle, const void* q_dev) {
+int skv_bind_query_device(void* handle, const void* q_dev, void* producer_stream) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
   if (!q_dev) return fail(h, SKV_EINVAL, "NULL device query");
-  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, q_dev, 16 * D * 2, hipMemcpyDeviceToDevice, h->stream));
+  const hipStream_t ps = static_cast<hipStream_t>(producer_stream);
+  if (ps == h->stream) {
+    HIPCHK(h, hipMemcpyAsync((void*)h->a.q, q_dev, 16 * D * 2, hipMemcpyDeviceToDevice, h->stream));
+  } else {
+    // The copy is ordered on the producer's stream (NULL: the legacy default
+    // stream), after the work that wrote q_dev and after the handle's steps
+    // enqueued so far (they read the query buffer); the handle's stream then
+    // waits for the copy.  q_dev stays the caller's until the producer
+    // stream reaches the copy (stream-ordered lifetime).
+    HIPCHK(h, hipEventRecord(h->steps_done, h->stream));
+    HIPCHK(h, hipStreamWaitEvent(ps, h->steps_done, 0));
+    HIPCHK(h, hipMemcpyAsync((void*)h->a.q, q_dev, 16 * D * 2, hipMemcpyDeviceToDevice, ps));
+    HIPCHK(h, hipEventRecord(h->q_ready, ps));
+    HIPCHK(h, hipStreamWaitEvent(h->stream, h->q_ready, 0));
+  }
   h->bound = true;
   return SKV_OK;
 }
@@ -818,11 +844,15 @@ int skv_select_mode(void* handle, int exact) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
   HIPCHK(h, hipStreamSynchronize(h->stream));
-  if (exact < 0 || exact > 2) return fail(h, SKV_EINVAL, "select mode %d not in 0..2", exact);
-  const int e = exact;
+  if (exact < 0 || exact > 3) return fail(h, SKV_EINVAL, "select mode %d not in 0..3", exact);
+  // mode 3: the full selections, with the token top-k kernels' scores never
+  // held in LDS (their in-memory radix passes run at every size)
+  const int e = exact == 3 ? 1 : exact;
   h->a.exact_select = e;
   h->w.top_u1.exact_select = e;
   h->w.top_u2.exact_select = e;
+  h->w.top_u1.lds_items = exact == 3 ? 0 : h->top_u1_lds_items;
+  h->w.top_u2.lds_items = exact == 3 ? 0 : h->top_u2_lds_items;
   drop_graph(h);  // the kernels take the options by value
   return SKV_OK;
 }

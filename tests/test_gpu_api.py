@@ -6,6 +6,9 @@ caller uses."""
 
 from __future__ import annotations
 
+import functools
+import types
+
 import numpy as np
 import pytest
 import torch
@@ -119,54 +122,116 @@ def test_device_query_binding_matches_host_binding():
         rt.close()
 
 
-def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048):
-    """Every funnel stage bit-exact against the oracle on a BASELINE-sized
-    cache (seeded synthetic inputs), output within the attention tolerance."""
+def test_device_query_produced_on_another_stream():
+    """A query written by a PyTorch kernel on a side stream, late: the copy is
+    ordered after that kernel (and after the instance's earlier step, which
+    still reads the previous query), so both steps see their own query."""
+    index, k, v, qs = case(**P0)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    try:
+        outs, ids = [], []
+        for q in qs:
+            rt.bind_query(q)
+            rt.enqueue()
+            rt.synchronize()
+            outs.append(rt.read_output())
+            ids.append(rt.debug_ids())
+        base = qs[1].reshape(16, 256).to("cuda:0")
+        side = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        print("[gpu] device query from a side stream", flush=True)
+        rt.bind_query(qs[0])
+        rt.enqueue()  # step on q0, still running while q1 is bound
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(20_000_000)  # the producer's write lands late
+            q1 = base * 1
+            rt.bind_query_device(q1)
+        del q1  # freed on its stream after the copy
+        rt.synchronize()
+        assert torch.equal(rt.read_output(), outs[0])
+        assert torch.equal(rt.debug_ids(), ids[0])
+        rt.enqueue()
+        rt.synchronize()
+        assert torch.equal(rt.read_output(), outs[1])
+        assert torch.equal(rt.debug_ids(), ids[1])
+    finally:
+        torch.cuda.synchronize()
+        rt.close()
+
+
+@functools.lru_cache(maxsize=2)
+def _full_size_inputs(name, clustered, n_queries):
+    """(profile, k, v, queries, index at the profile's nprobe, oracle inputs)."""
     from seoulkv_amd.index import SeoulKV4Index
     from seoulkv_amd.synthetic import make_profile
 
-    print(f"[gpu] {name} P={nprobe} clustered={clustered}: inputs", flush=True)
-    prof, k, v, qs = make_profile(name, clustered=clustered)
-    index = SeoulKV4Index.build(k, v, sink=prof.sink, local=prof.local,
-                                nprobe=nprobe or prof.nprobe, n_centroids=prof.n_centroids)
-    print(f"[gpu] {name}: oracle", flush=True)
+    prof, k, v, qs = make_profile(name, clustered=clustered, n_queries=n_queries)
+    index = SeoulKV4Index.build(k, v, sink=prof.sink, local=prof.local, nprobe=prof.nprobe,
+                                n_centroids=prof.n_centroids)
     kb, vb = bits(k), bits(v)
     code8, scales = od.key_codec(kb)
     k8, v8 = od.fp8_records(kb, vb)
+    return prof, k, v, qs, index, (code8, scales, k8, v8)
+
+
+def _with_nprobe(index, nprobe):
+    """The same index cells probed with another nprobe (the clustering does
+    not depend on it; SeoulKV4Index.load(path, nprobe=...) does the same)."""
+    cells = tuple(dict(c, p=nprobe) for c in index.cells)
+    return types.SimpleNamespace(cells=cells, zones=index.zones)
+
+
+def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048, queries=(0,),
+                      n_queries=1):
+    """Every funnel stage bit-exact against the oracle on a BASELINE-sized
+    cache (seeded synthetic inputs), output within the attention tolerance."""
+    print(f"[gpu] {name} P={nprobe} clustered={clustered}: inputs", flush=True)
+    prof, k, v, qs, index, (code8, scales, k8, v8) = _full_size_inputs(name, clustered,
+                                                                        n_queries)
+    if nprobe is not None and nprobe != prof.nprobe:
+        index = _with_nprobe(index, nprobe)
     cells = [od.GroupCell.from_cell(c) for c in index.cells]
-    traces, ref = od.decode_step(cells, code8, scales, k8, v8, bits(qs[0]).reshape(16, 256),
-                                 sink=prof.sink, local=prof.local)
-    print(f"[gpu] {name}: device step", flush=True)
     rt = _hip.Runtime(0, k, v, index, pool_min=pool_min, pool_capacity=None, debug=True)
     try:
-        rt.bind_query(qs[0])
-        rt.enqueue()
-        status = rt.synchronize()
-        assert status["err"] == [0, 0, 0, 0]
-        for g, tr in enumerate(traces):
-            np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected)
-            np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool)
-            np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1)
-            np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2)
-            np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
-        _check_output(rt.read_output(), ref)
+        for qi in queries:
+            print(f"[gpu] {name}: oracle q{qi}", flush=True)
+            traces, ref = od.decode_step(cells, code8, scales, k8, v8,
+                                         bits(qs[qi]).reshape(16, 256),
+                                         sink=prof.sink, local=prof.local)
+            print(f"[gpu] {name}: device step q{qi}", flush=True)
+            rt.bind_query(qs[qi])
+            rt.enqueue()
+            status = rt.synchronize()
+            assert status["err"] == [0, 0, 0, 0]
+            for g, tr in enumerate(traces):
+                assert status["pool"][g] == len(tr.pool)
+                np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected)
+                np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool)
+                np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1)
+                np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2)
+                np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
+            _check_output(rt.read_output(), ref)
     finally:
         rt.close()
 
 
 @pytest.mark.slow
 def test_full_size_parity_config2():
-    """T = 131072, nc = 8192, P = 384."""
-    _full_size_parity("cfg2")
+    """T = 131072, nc = 8192, P = 384; three queries."""
+    _full_size_parity("cfg2", queries=(0, 1, 2), n_queries=3)
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("nprobe,clustered", [(16, True), (64, True), (256, True), (512, True),
-                                              (128, False), (384, False)])
+@pytest.mark.parametrize("nprobe,clustered", [(16, True), (64, True), (128, True), (256, True),
+                                              (512, True), (16, False), (64, False),
+                                              (128, False), (256, False), (384, False),
+                                              (512, False)])
 def test_full_size_parity_config3_nprobe_sweep(nprobe, clustered):
-    """config-2 shapes over the nprobe sweep, with
-    clustered and i.i.d. keys (the i.i.d. keys give the largest pools)."""
-    _full_size_parity("cfg2", nprobe=nprobe, clustered=clustered, pool_min=0)
+    """config-2 shapes over the whole nprobe sweep
+    (16, 64, 128, 256, 384, 512), clustered and i.i.d. keys (the i.i.d. keys
+    give the largest pools; P = 384 clustered is configuration 2)."""
+    _full_size_parity("cfg2", nprobe=nprobe, clustered=clustered, pool_min=0,
+                      n_queries=3 if clustered else 1)
 
 
 @pytest.mark.slow

@@ -146,3 +146,27 @@ def test_append_with_graph_mode():
         check_step(rt, q, [kn], [vn], "graph after append")
     finally:
         rt.close()
+
+
+def test_host_append_over_several_staging_chunks():
+    """A host append of 2100 tokens is staged in 1024-token rounds (three
+    rounds here): every record lands at its row and the step over the grown
+    cache equals the oracle's."""
+    index, k, v, qs = case(**P)
+    q = qs[0]
+    n = 2100
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True,
+                      append_capacity=2500)
+    try:
+        kn, vn = new_tokens(q, n, seed=21)
+        print(f"[gpu] host append of {n} tokens", flush=True)
+        rt.append(kn, vn)
+        check_step(rt, q, [kn], [vn], "multi-chunk append")
+        kb, vb = bits(kn), bits(vn)
+        for g in range(4):
+            rec = rt.read_stage("kv8", g).reshape(-1, 512)
+            assert rec.shape[0] == P["context"] + n
+            np.testing.assert_array_equal(rec[P["context"]:, 256:], fp8_bytes(kb[g]))
+            np.testing.assert_array_equal(rec[P["context"]:, :256], fp8_bytes(vb[g]))
+    finally:
+        rt.close()

@@ -131,12 +131,14 @@ def test_step_parity(runtimes, name, qi):
         assert cosine(got[j], out[j]) >= 0.999, f"head {j} cosine"
 
 
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", [1, 2, 3])
 @pytest.mark.parametrize("name", ["t8192_clustered", "t16384_nc1024_p256"])
 def test_selection_paths_agree(runtimes, name, mode):
-    """Every selection through the full path (mode 1) and through a sampled
-    cut forced to miss, i.e. the fallback (mode 2), equals the oracle; the
-    status bits record which selections fell back."""
+    """Every selection through the full path (mode 1), through a sampled cut
+    forced to miss, i.e. the fallback (mode 2), and through the full path
+    with the token top-k kernels' in-memory radix passes (mode 3: the path a
+    pool beyond the LDS capacity takes) equals the oracle; the status bits
+    record which selections fell back."""
     p = CASES[name]
     rt = runtime_for(runtimes, name)
     _, _, _, qs = case(**p)
@@ -156,7 +158,7 @@ def test_selection_paths_agree(runtimes, name, mode):
         np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2)
         np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
     bits = status["full_select"]
-    if mode == 1:
+    if mode in (1, 3):
         assert bits == [0, 0, 0, 0]  # the full path ran directly: nothing missed
     else:
         assert all(b == 31 for b in bits), bits  # every stage missed and fell back

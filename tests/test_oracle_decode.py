@@ -341,3 +341,27 @@ def test_grown_cache_attends_appended_tokens(step):
             qf[j].double()[None, None, None], kk, vv
         )[0, 0, 0].numpy()
         assert np.allclose(out[j], want, rtol=1e-12, atol=1e-12)
+
+
+def test_dense_decode_matches_torch_sdpa():
+    """``dense_decode`` (the CPU dense baseline and the dense FP8 path's
+    reference) against torch's scaled_dot_product_attention in float64, GQA
+    4:1 (query head j reads KV head j // 4), scale 1/sqrt(256)."""
+    import torch
+
+    g = torch.Generator().manual_seed(11)
+    T = 3000
+    k = torch.randn(4, T, 256, generator=g, dtype=torch.float32)
+    v = torch.randn(4, T, 256, generator=g, dtype=torch.float32)
+    q = torch.randn(16, 256, generator=g, dtype=torch.float32) * 0.5
+    got = od.dense_decode(k.numpy(), v.numpy(), q.numpy())
+    kk = k.double().repeat_interleave(4, dim=0)  # [16, T, 256]
+    vv = v.double().repeat_interleave(4, dim=0)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.double()[:, None, :], kk, vv, scale=1.0 / 16.0)[:, 0, :].numpy()
+    np.testing.assert_allclose(got, ref, rtol=0, atol=2e-6)
+    # a planted mistake (the GQA map j % 4) is caught
+    bad = np.stack([
+        (lambda lg: (np.exp(lg - lg.max()) / np.exp(lg - lg.max()).sum()) @ v.numpy()[j % 4])(
+            k.numpy()[j % 4] @ q.numpy()[j] / 16.0) for j in range(16)])
+    assert np.abs(bad - ref).max() > 1e-2
