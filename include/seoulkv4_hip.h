@@ -140,6 +140,22 @@ int skv_dense_decode(void *handle);
 int skv_dense_output_device(void *handle, void **dev_ptr);
 int skv_read_dense_output(void *handle, uint16_t *host_out);
 
+/* Allocation-free dense FP8 decode.  No counterpart in the reference: this
+ * entry point is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops or harnesses that forbid hipMalloc).  It
+ * computes what skv_dense_decode computes, from caller buffers on the current
+ * device: kv8 = [4][rows][512] FP8 e4m3fn [V (256 B) || K (256 B)] records,
+ * of which rows 0 .. T-1 of each KV head are attended; q_dev = [16][256] BF16;
+ * out_dev = [16][256] BF16.  stream: hipStream_t (NULL = default stream).
+ * It calls no allocator: the per-block partials live in a file-scope device
+ * array of 1 MiB (4 x 64 x 4 x 258 FP32) that each GPU holds until the
+ * process ends, its address looked up on the first call on a device.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (other
+ * streams, other threads) race.  Requires 1 <= T <= 2^20 and rows >= T, else
+ * SKV_EINVAL; errors are read with skv_last_error(NULL). */
+int skv_dense_decode_static(const void *kv8, int rows, int T, const void *q_dev,
+                            void *out_dev, void *stream);
+
 /* Mean milliseconds per launch over `reps` back-to-back launches of
  * mean_ms[0] the dense partial kernel, mean_ms[1] its merge kernel and
  * mean_ms[2] both (one dense decode).  Needs one skv_dense_decode first. */

@@ -92,6 +92,7 @@ def load_library() -> ctypes.CDLL:
         "skv_append": (i32, [vp, vp, vp, i32]),
         "skv_append_device": (i32, [vp, vp, vp, i32]),
         "skv_dense_decode": (i32, [vp]),
+        "skv_dense_decode_static": (i32, [vp, i32, i32, vp, vp, vp]),
         "skv_dense_output_device": (i32, [vp, ctypes.POINTER(vp)]),
         "skv_read_dense_output": (i32, [vp, vp]),
         "skv_time_dense": (i32, [vp, i32, vp]),
@@ -117,6 +118,31 @@ def declared_symbols() -> list[str]:
 
     text = HEADER.read_text()
     return sorted(set(re.findall(r"\b(skv_[a-z_]+)\s*\(", text)))
+
+
+def dense_decode_static(kv8: torch.Tensor, context: int, q: torch.Tensor,
+                        out: torch.Tensor) -> None:
+    """Allocation-free dense FP8 decode (``skv_dense_decode_static``) on
+    PyTorch's current stream: ``kv8`` uint8 [4, rows, 512] FP8 [V || K]
+    records on the device, rows ``0 .. context-1`` attended; ``q`` BF16
+    [16, 256] and ``out`` BF16 [16, 256] on the same device.  Raises on a
+    rejected size."""
+    if kv8.dtype != torch.uint8 or kv8.dim() != 3 or kv8.shape[0] != G or kv8.shape[2] != 512:
+        raise ValueError("expected uint8 records [4, rows, 512]")
+    for name, t in (("q", q), ("out", out)):
+        if t.dtype != torch.bfloat16 or t.numel() != 16 * D or not t.is_contiguous():
+            raise ValueError(f"expected a contiguous BF16 {name} with 16 x 256 elements")
+    if not (kv8.is_contiguous() and kv8.device == q.device == out.device):
+        raise ValueError("records, query and output must be contiguous on one device")
+    lib = load_library()
+    with torch.cuda.device(kv8.device):
+        stream = torch.cuda.current_stream(kv8.device).cuda_stream
+        code = lib.skv_dense_decode_static(kv8.data_ptr(), int(kv8.shape[1]), int(context),
+                                           q.data_ptr(), out.data_ptr(),
+                                           ctypes.c_void_p(stream or None))
+    if code != 0:
+        msg = lib.skv_last_error(None).decode()
+        raise RuntimeError(f"skv_dense_decode_static failed ({ERRORS.get(code, code)}): {msg}")
 
 
 def _ptr(a: np.ndarray) -> int:

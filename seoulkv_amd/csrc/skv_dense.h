@@ -39,4 +39,8 @@ inline void dense_shape(int T, int& iters, int& nb) {
 // k = 0: the per-block partials; k = 1: the merge into the output.
 void launch_dense(const DenseArgs& a, hipStream_t st, int k);
 
+// Records the error text of a call without a handle (read back through
+// skv_last_error(NULL)) and returns code.
+int note_call_error(int code, const char* fmt, ...);
+
 }  // namespace skv

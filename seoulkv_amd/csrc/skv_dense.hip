@@ -11,6 +11,9 @@
 // online-softmax state per row; rows, waves and blocks are merged by the
 // usual max/sum rescaling.  k_dense_merge folds the per-block partials of
 // each query head into the BF16 output.
+#include <mutex>
+
+#include "../../include/seoulkv4_hip.h"
 #include "skv_dense.h"
 #include "skv_device.h"
 
@@ -337,4 +340,71 @@ void launch_dense(const DenseArgs& a, hipStream_t st, int k) {
     hipLaunchKernelGGL(k_dense_merge, dim3(G * H, DN_MERGE_SLICES), dim3(256), 0, st, a);
 }
 
+// ------------------------------------------------ allocation-free dense decode
+// The partials of skv_dense_decode_static: one file-scope device array per
+// GPU, [G][DN_TARGET_BLOCKS][H][D + 2] FP32 (1 MiB), enough for every context
+// up to 2^20 keys (dense_shape never uses more than DN_TARGET_BLOCKS blocks
+// per group).  Host code never names it in a launch: the device address comes
+// from hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t DN_SCRATCH_FLOATS = (size_t)G * DN_TARGET_BLOCKS * H * (D + 2);
+static __device__ __align__(256) float scratch[DN_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int DN_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[DN_MAX_DEVICES] = {};
+
+// The calling thread's current device's copy of `scratch` (looked up on the
+// first call on that device); NULL with *err set on failure.
+float* device_scratch(int* device, hipError_t* err) {
+  *err = hipGetDevice(device);
+  if (*err != hipSuccess) return nullptr;
+  if (*device < 0 || *device >= DN_MAX_DEVICES) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[*device]) {
+    void* ptr = nullptr;
+    *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    g_scratch_ptr[*device] = static_cast<float*>(ptr);
+  }
+  return g_scratch_ptr[*device];
+}
+
+}  // namespace
+
 }  // namespace skv
+
+extern "C" int skv_dense_decode_static(const void* kv8, int rows, int T, const void* q_dev,
+                                       void* out_dev, void* stream) {
+  using namespace skv;
+  if (!kv8 || !q_dev || !out_dev) return note_call_error(SKV_EINVAL, "NULL records, query or output");
+  if (T < 1 || T > (1 << 20))
+    return note_call_error(SKV_EINVAL, "context %d outside [1, 2^20] (the static partials hold "
+                           "%d blocks per group)", T, DN_TARGET_BLOCKS);
+  if (rows < T) return note_call_error(SKV_EINVAL, "rows %d < context %d", rows, T);
+  int device = 0;
+  hipError_t e = hipSuccess;
+  float* part = device_scratch(&device, &e);
+  if (!part)
+    return note_call_error(SKV_EHIP, "device scratch lookup failed: %s", hipGetErrorString(e));
+  DenseArgs a{};
+  a.kv8 = static_cast<const uint8_t*>(kv8);
+  a.q = static_cast<const uint16_t*>(q_dev);
+  a.T = T;
+  a.rows = rows;
+  dense_shape(T, a.iters, a.nb);
+  if (a.nb > DN_TARGET_BLOCKS)  // never for T <= 2^20
+    return note_call_error(SKV_EINVAL, "context %d needs %d partials per group", T, a.nb);
+  a.part = part;
+  a.out = static_cast<uint16_t*>(out_dev);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  launch_dense(a, st, 0);
+  launch_dense(a, st, 1);
+  e = hipGetLastError();
+  if (e != hipSuccess) return note_call_error(SKV_EHIP, "dense launch failed: %s", hipGetErrorString(e));
+  return SKV_OK;
+}

@@ -262,6 +262,16 @@ std::string json_escape(const std::string& s) {
 
 }  // namespace
 
+int skv::note_call_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_create_error = buf;
+  return code;
+}
+
 extern "C" {
 
 const char* skv_version(void) { return "seoulkv4-hip gfx950 1"; }

@@ -155,3 +155,21 @@ def test_config_and_index_validation():
         SeoulKV4Index.build(k[:, :5000], v[:, :5000])  # below the minimum context
     with pytest.raises(ValueError):
         SeoulKV4Index.build(k.float(), v)
+
+
+def test_static_dense_decode_rejects_sizes_before_any_device_work():
+    """``skv_dense_decode_static`` checks its sizes on the host first: a
+    context outside [1, 2^20] or fewer rows than keys is SKV_EINVAL with a
+    message, before any HIP call (so this runs without a GPU)."""
+    import ctypes
+
+    from seoulkv_amd import _hip
+
+    lib = _hip.load_library()
+    dummy = ctypes.c_void_p(16)  # never dereferenced: the size checks come first
+    for rows, T, what in ((100, 0, "context 0"), (1 << 21, (1 << 20) + 1, "context"),
+                          (10, 11, "rows 10 < context 11")):
+        code = lib.skv_dense_decode_static(dummy, rows, T, dummy, dummy, None)
+        assert code == 1
+        assert what in lib.skv_last_error(None).decode()
+    assert lib.skv_dense_decode_static(None, 8, 8, dummy, dummy, None) == 1
