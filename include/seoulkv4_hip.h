@@ -108,6 +108,12 @@ int skv_sync(void *handle, int32_t *status);
  * overwritten by the next skv_enqueue). */
 int skv_output_device(void *handle, void **dev_ptr);
 
+/* Device pointer of the same output in the reference's per-KV-head layout
+ * (DecodeResult.device_tensors, result.py:25-28): [4][1][32][4][256] BF16,
+ * query head 4g + h at [g][0][h][h], every other row zero.  Written by each
+ * skv_enqueue with the compact output; valid until skv_destroy. */
+int skv_output_tiles_device(void *handle, void **dev_ptr);
+
 /* Reference DecodeResult.to_torch (result.py:30-38): sync + copy [16][256]. */
 int skv_read_output(void *handle, uint16_t *host_out);
 

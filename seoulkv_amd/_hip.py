@@ -82,6 +82,7 @@ def load_library() -> ctypes.CDLL:
         "skv_enqueue": (i32, [vp]),
         "skv_sync": (i32, [vp, vp]),
         "skv_output_device": (i32, [vp, ctypes.POINTER(vp)]),
+        "skv_output_tiles_device": (i32, [vp, ctypes.POINTER(vp)]),
         "skv_read_output": (i32, [vp, vp]),
         "skv_debug_ids": (i32, [vp, vp]),
         "skv_read_stage": (i32, [vp, i32, i32, vp, i64, ctypes.POINTER(i64)]),
@@ -283,6 +284,12 @@ class Runtime:
     def output_device_ptr(self) -> int:
         p = ctypes.c_void_p()
         self._check(self.lib.skv_output_device(self.handle, ctypes.byref(p)), "output")
+        return int(p.value)
+
+    def output_tiles_device_ptr(self) -> int:
+        """Device [4][1][32][4][256] BF16 output in the reference's layout."""
+        p = ctypes.c_void_p()
+        self._check(self.lib.skv_output_tiles_device(self.handle, ctypes.byref(p)), "output")
         return int(p.value)
 
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:

@@ -1469,7 +1469,9 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
       Lt += parts[r * (D + 2) + D + 1] * f;
       Ot += parts[r * (D + 2) + d] * f;
     }
-    a.out[j * D + d] = (uint16_t)bf16_rne(Ot / Lt);
+    const uint16_t ob = (uint16_t)bf16_rne(Ot / Lt);
+    a.out[j * D + d] = ob;
+    a.out_tiles[((size_t)(g * 32 + h) * H + h) * D + d] = ob;
   }
   SKV_TS(13, 15);
   SKV_TSE(9);

@@ -478,6 +478,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.top = (int*)ar.take(G * H * TOPK * 4);
     a.status = (int*)ar.take(G * ST_WORDS * 4);
     a.out = (uint16_t*)ar.take(16 * D * 2);
+    a.out_tiles = (uint16_t*)ar.take((size_t)G * 32 * H * D * 2);
     a.bm_u1 = (uint64_t*)ar.take((size_t)G * H * words1 * 8);
     a.bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
     h->dn.part = (float*)ar.take((size_t)G * DN_TARGET_BLOCKS * H * (D + 2) * 4);  // any T
@@ -904,6 +905,13 @@ int skv_output_device(void* handle, void** dev_ptr) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h || !dev_ptr) return SKV_EINVAL;
   *dev_ptr = h->a.out;
+  return SKV_OK;
+}
+
+int skv_output_tiles_device(void* handle, void** dev_ptr) {
+  Handle* h = static_cast<Handle*>(handle);
+  if (!h || !dev_ptr) return SKV_EINVAL;
+  *dev_ptr = h->a.out_tiles;
   return SKV_OK;
 }
 

@@ -108,6 +108,9 @@ struct StepArgs {
   int* top;                 // [G][H][TOPK]
   int* status;              // [G][ST_WORDS]
   uint16_t* out;            // [16][256] bf16
+  uint16_t* out_tiles;      // [G][32][H][D] bf16: query head 4g + h at [g][h][h] (the
+                            // reference's tile-padded per-KV-head layout); the other
+                            // rows stay zero (cleared once with the workspace)
 };
 
 struct TopkArgs {

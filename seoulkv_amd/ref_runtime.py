@@ -51,22 +51,19 @@ class GroupOutput:
 
     def to_torch(self) -> torch.Tensor:
         """CPU BF16 [1, 32, 4, 256]: head h of this KV head at [0, h, h]."""
-        out = self._runtime.read_output().reshape(16, _D)
-        padded = torch.zeros(self.shape, dtype=torch.bfloat16)
-        for h in range(_GROUP):
-            padded[0, h, h] = out[_GROUP * self.slot + h]
-        return padded
+        self._runtime.synchronize()
+        return self.device_view().cpu()
 
     def device_view(self) -> torch.Tensor:
-        """Device BF16 [4, 256] view of this KV head's rows of the output
-        buffer (valid until the next enqueue; no padding)."""
+        """Device BF16 [1, 32, 4, 256] view of this KV head's tile of the
+        library's padded output buffer (valid until the next enqueue)."""
         from seoulkv_amd.result import _DeviceArray
 
         raw = torch.as_tensor(
-            _DeviceArray(self._runtime.output_device_ptr(), (16, _D), "<i2"),
+            _DeviceArray(self._runtime.output_tiles_device_ptr(), (4,) + self.shape, "<i2"),
             device=f"cuda:{self._runtime.device}",
         ).view(torch.bfloat16)
-        return raw[_GROUP * self.slot : _GROUP * self.slot + _GROUP]
+        return raw[self.slot]
 
 
 class DebugIndices:

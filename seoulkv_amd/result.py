@@ -4,11 +4,10 @@ Mirrors ``DecodeResult`` (reference ``result.py:10-38``): valid until the
 owner's next ``run`` or ``close`` (generation check), ``to_torch`` waits and
 copies the output to a CPU BF16 [1, 1, 16, 256] tensor.
 
-``device_tensors`` returns one BF16 [1, 4, 256] device tensor per KV group
-(query head ``4 g + h`` is row ``h`` of group ``g``); they alias the
-library's output buffer.  The reference's per-group [1, 32, 4, 256] shape is
-a Tenstorrent tile padding with the result on the diagonal; this build keeps
-no padding.
+``device_tensors`` returns one BF16 [1, 32, 4, 256] device tensor per KV
+group in the reference's layout (``result.py:25-28``): query head ``4 g + h``
+at ``[0, h, h]``, every other row zero.  They alias a library buffer that
+each step writes along with the compact output.
 """
 
 from __future__ import annotations
@@ -48,15 +47,16 @@ class DecodeResult:
 
     @property
     def device_tensors(self) -> tuple:
-        """Per KV group BF16 [1, 4, 256] device views.  Call ``synchronize``
-        on the owner before reading them; do not retain across close."""
+        """Per KV group BF16 [1, 32, 4, 256] device views (query head 4g + h
+        at [0, h, h]).  Call ``synchronize`` on the owner before reading
+        them; do not retain across close."""
         owner = self._owner()
         state = owner._require_initialized()
-        ptr = state.output_device_ptr()
+        ptr = state.output_tiles_device_ptr()
         raw = torch.as_tensor(
-            _DeviceArray(ptr, (16, 256), "<i2"), device=f"cuda:{owner._device}"
+            _DeviceArray(ptr, (4, 1, 32, 4, 256), "<i2"), device=f"cuda:{owner._device}"
         ).view(torch.bfloat16)
-        return tuple(raw[4 * g : 4 * g + 4].unsqueeze(0) for g in range(4))
+        return tuple(raw[g] for g in range(4))
 
     def to_torch(self) -> torch.Tensor:
         """Synchronise and copy into a CPU BF16 [1, 1, 16, 256] tensor."""

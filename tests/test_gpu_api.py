@@ -46,9 +46,15 @@ def test_lifecycle_and_borrowed_results():
         traces, ref = oracle_step(P0, qs[0])
         _check_output(out0, ref)
         assert torch.equal(skv.debug_snapshot()["selected_ids"], _top100(traces))
-        views = r0.device_tensors
-        assert len(views) == 4 and all(t.shape == (1, 4, 256) for t in views)
-        assert torch.equal(torch.cat([t[0] for t in views]).cpu(), out0.reshape(16, 256))
+        views = r0.device_tensors  # the reference's [1, 32, 4, 256] per KV head
+        assert len(views) == 4 and all(t.shape == (1, 32, 4, 256) for t in views)
+        diag = torch.cat([torch.stack([t[0, h, h] for h in range(4)]) for t in views])
+        assert torch.equal(diag.cpu(), out0.reshape(16, 256))
+        for t in views:
+            off = t[0].clone()
+            for h in range(4):
+                off[h, h] = 0
+            assert not off.float().abs().sum().item()
         r1 = skv.run(qs[1])
         with pytest.raises(RuntimeError):
             r0.to_torch()  # borrowed output: superseded by the next run
