@@ -60,6 +60,45 @@ constexpr uint64_t CAND_HAS_ID = 1ull << 56;
 __device__ __forceinline__ uint32_t cand_ord(uint64_t c) { return (uint32_t)(c >> 40) & 0xffffu; }
 __device__ __forceinline__ int cand_pos(uint64_t c) { return (int)(c & 0xfffffu); }
 
+// Number of the n entries of a smaller than x; a is a 16-byte aligned LDS
+// array.  Four 16-byte reads are in flight per step (a dependent read per
+// entry would leave the loop bound by LDS latency).
+__device__ __forceinline__ int count_below(const uint32_t* a, int n, uint32_t x) {
+  const uint4* a4 = reinterpret_cast<const uint4*>(a);
+  const int n4 = n >> 2;
+  int r0 = 0, r1 = 0, r2 = 0, r3 = 0, j = 0;
+  auto c4 = [x](uint4 w) { return (int)(w.x < x) + (int)(w.y < x) + (int)(w.z < x) + (int)(w.w < x); };
+  for (; j + 4 <= n4; j += 4) {
+    const uint4 w0 = a4[j], w1 = a4[j + 1], w2 = a4[j + 2], w3 = a4[j + 3];
+    r0 += c4(w0);
+    r1 += c4(w1);
+    r2 += c4(w2);
+    r3 += c4(w3);
+  }
+  for (; j < n4; ++j) r0 += c4(a4[j]);
+  for (int i = 4 * n4; i < n; ++i) r1 += a[i] < x;
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Number of the n 64-bit entries of a (16-byte aligned LDS) larger than x.
+__device__ __forceinline__ int count_above64(const uint64_t* a, int n, uint64_t x) {
+  const uint4* a4 = reinterpret_cast<const uint4*>(a);
+  const int n2 = n >> 1;
+  int r0 = 0, r1 = 0, j = 0;
+  auto c2 = [x](uint4 w) {
+    const uint64_t lo = ((uint64_t)w.y << 32) | w.x, hi = ((uint64_t)w.w << 32) | w.z;
+    return (int)(lo > x) + (int)(hi > x);
+  };
+  for (; j + 4 <= n2; j += 4) {
+    const uint4 w0 = a4[j], w1 = a4[j + 1], w2 = a4[j + 2], w3 = a4[j + 3];
+    r0 += c2(w0) + c2(w1);
+    r1 += c2(w2) + c2(w3);
+  }
+  for (; j < n2; ++j) r0 += c2(a4[j]);
+  if (n & 1) r1 += a[n - 1] > x;
+  return r0 + r1;
+}
+
 struct FastResult {
   Selection sel;  // members: the candidates passing fs_member
   int ncand;      // candidates in FastScratch::cand
@@ -316,9 +355,7 @@ __device__ FastResult fs_finish(int k, IdFn id, FastScratch& s, uint32_t cut, in
     __syncthreads();
     if ((int)threadIdx.x < ties) {  // rank = number of smaller tied IDs
       const uint32_t x = s.tie[threadIdx.x];
-      int r = 0;
-      for (int j = 0; j < ties; ++j) r += s.tie[j] < x;
-      if (r == need - 1) s.sel[2] = (int)x;
+      if (count_below(s.tie, ties, x) == need - 1) s.sel[2] = (int)x;
     }
     __syncthreads();
     res.sel.idcut = (uint32_t)s.sel[2];
@@ -474,22 +511,35 @@ __device__ FastResult tiled_select(const TileSrc& src, const uint16_t* __restric
   for (int e = 0; e < 4; ++e)
     if ((hot >> e) & 1u) s.hist[at++] = (uint32_t)(t4 + e);
   __syncthreads();
+  SKV_TS(ts, 7);
   // ---- 3. candidates of the listed tiles (packed compares, one LDS append
-  // per set bit, as fast_select's pass)
+  // per set bit, as fast_select's pass).  The tiles of every round (at most
+  // TL_ROUNDS: the caller bounds the row to 4 x SEL_BLOCK tiles) are loaded
+  // before the first is scanned, so the rounds share one memory latency;
+  // the loads are branch-free (an unlisted slot reloads tile 0, unused).
+  constexpr int TL_ROUNDS = 4;
   const int lane = threadIdx.x & 63;
   const u16x2 cm1 = {(uint16_t)(cut - 1), (uint16_t)(cut - 1)};  // cut >= 1
   uint32_t mx = 0;
-  for (int base = 0; base < nhot; base += SEL_BLOCK) {  // block-uniform
-    const int i = base + (int)threadIdx.x;
-    const int tile = i < nhot ? (int)s.hist[i] : -1;
-    uint4 w[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-    if (tile >= 0) src.tile(tile, w);
+  int tl[TL_ROUNDS];
+  uint4 tw[TL_ROUNDS][2];
+#pragma unroll
+  for (int r = 0; r < TL_ROUNDS; ++r) {
+    const int i = r * SEL_BLOCK + (int)threadIdx.x;
+    tl[r] = i < nhot ? (int)s.hist[i] : -1;
+  }
+#pragma unroll
+  for (int r = 0; r < TL_ROUNDS; ++r) src.tile(max(tl[r], 0), tw[r]);
+#pragma unroll
+  for (int r = 0; r < TL_ROUNDS; ++r) {
+    if (r * SEL_BLOCK >= nhot) break;  // block-uniform
+    const int tile = tl[r];
     uint32_t mask = 0;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const uint32_t m = ge_cut2(w[r].x, cm1) | (ge_cut2(w[r].y, cm1) << 2) |
-                         (ge_cut2(w[r].z, cm1) << 4) | (ge_cut2(w[r].w, cm1) << 6);
-      mask |= ((m & 0x55u) | ((m >> 15) & 0xaau)) << (8 * r);
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t m = ge_cut2(tw[r][q].x, cm1) | (ge_cut2(tw[r][q].y, cm1) << 2) |
+                         (ge_cut2(tw[r][q].z, cm1) << 4) | (ge_cut2(tw[r][q].w, cm1) << 6);
+      mask |= ((m & 0x55u) | ((m >> 15) & 0xaau)) << (8 * q);
     }
     if (tile < 0) mask = 0;
     else if (n - 16 * tile < 16) mask &= (1u << (n - 16 * tile)) - 1u;
@@ -500,10 +550,10 @@ __device__ FastResult tiled_select(const TileSrc& src, const uint16_t* __restric
     wbase = __builtin_amdgcn_readlane(wbase, 63);
     int slot = wbase + inc - cnt;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {  // compile-time octet: no indexed arrays
-      uint32_t m8 = (mask >> (8 * r)) & 0xffu;
-      const u32x4 wv = {w[r].x, w[r].y, w[r].z, w[r].w};
-      const int pos0 = 16 * tile + 8 * r;
+    for (int q = 0; q < 2; ++q) {  // compile-time octet: no indexed arrays
+      uint32_t m8 = (mask >> (8 * q)) & 0xffu;
+      const u32x4 wv = {tw[r][q].x, tw[r][q].y, tw[r][q].z, tw[r][q].w};
+      const int pos0 = 16 * tile + 8 * q;
       while (m8) {
         const int e = __ffs(m8) - 1;
         m8 &= m8 - 1;
@@ -518,6 +568,7 @@ __device__ FastResult tiled_select(const TileSrc& src, const uint16_t* __restric
   mx = (uint32_t)wave_max((int)mx);
   if (lane == 0) atomicMax(&s.maxo, (int)mx);
   __syncthreads();
+  SKV_TS(ts, 8);
   return fs_finish<false>(k, id, s, cut, ts);
 }
 

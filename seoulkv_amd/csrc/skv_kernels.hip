@@ -482,13 +482,13 @@ __device__ void select_in_registers(const StepArgs& a, int g, int h, FastScratch
   const uint4 wu = load_oct(a.upper + row, nc);
   const uint4 wf = load_oct(a.fine_ord + row, nc);
   auto cid = [](int i) { return (uint32_t)i; };
-  const OctResult r1 = oct_select<true, true>(wl, a.P[g], cid, fs);
+  const OctResult r1 = oct_select<true, true>(wl, a.P[g], cid, fs, 2);
   const uint32_t thr = r1.sel.all ? 0u : r1.sel.v;
   if (t == 0) a.thr[g * H + h] = thr;
   SKV_TS(2, 6);
   // fine scores of the eligible centroids (upper >= thr), others excluded
   const uint4 wm = MaskedScores::pick4(wf, wu, thr);
-  const OctResult r2 = oct_select<false, true>(wm, a.P[g], cid, fs);
+  const OctResult r2 = oct_select<false, true>(wm, a.P[g], cid, fs, 4);
   // items 8t .. 8t+7 are byte t & 3 of bitmap word t >> 2: merge 4 lanes
   uint32_t m = r2.mine << (8 * (t & 3));
   m |= __shfl_xor(m, 1);
@@ -1056,8 +1056,8 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
   uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
   auto id = [tok](int i) { return (uint32_t)tok[i]; };
   if (t.exact_select == 0 && n <= OCT_ITEMS) {  // the scores fit in registers
-    const OctResult r =
-        oct_select<false, false>(load_oct(sc, n), t.k, id, *reinterpret_cast<FastScratch*>(dyn));
+    const OctResult r = oct_select<false, false>(load_oct(sc, n), t.k, id,
+                                                 *reinterpret_cast<FastScratch*>(dyn), ts);
     if (r.ok) {
       write_member_words(r.mine, n, bm);
       SKV_TS(ts, 15);
@@ -1330,7 +1330,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   const int g = blockIdx.x / H, h = blockIdx.x % H, j = g * H + h;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ SelectScratch s;
-  __shared__ uint64_t s_key[TOPK];
+  __shared__ __align__(16) uint64_t s_key[TOPK];
   __shared__ int s_cnt;
   __shared__ AttnScratch att;
   const int n = a.status[g * ST_WORDS + ST_U2];
@@ -1361,7 +1361,15 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
       t0 = reinterpret_cast<const uint4*>(tok)[2 * threadIdx.x];
       t1 = reinterpret_cast<const uint4*>(tok)[2 * threadIdx.x + 1];
     }
-    const OctResult r = oct_select<false, false>(w, TOPK, id, *reinterpret_cast<FastScratch*>(dyn));
+    // the octet's tokens in LDS for the tie ranking (ordered before their
+    // reads by the selection's first barrier)
+    __shared__ __align__(16) uint32_t s_tok[U2_MAX];
+    if (8 * (int)threadIdx.x < U2_MAX) {
+      reinterpret_cast<uint4*>(s_tok)[2 * threadIdx.x] = t0;
+      reinterpret_cast<uint4*>(s_tok)[2 * threadIdx.x + 1] = t1;
+    }
+    const OctResult r = oct_select<false, false>(
+        w, TOPK, [&](int i) { return s_tok[i]; }, *reinterpret_cast<FastScratch*>(dyn), 13);
     if (r.ok) {
       SKV_TS(13, 6);
       // members in list order (deterministic, so the attention sums are too)
@@ -1429,9 +1437,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   int* out = a.top + j * TOPK;
   if ((int)threadIdx.x < m) {
     const uint64_t key = s_key[threadIdx.x];
-    int rank = 0;
-    for (int jj = 0; jj < m; ++jj) rank += s_key[jj] > key;
-    out[rank] = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
+    out[count_above64(s_key, m, key)] = (int)(0xfffffu - (uint32_t)(key & 0xfffffu));
   } else if ((int)threadIdx.x < TOPK) {
     out[threadIdx.x] = -1;
   }

@@ -63,9 +63,7 @@ __device__ __forceinline__ uint64_t rank_ties(uint64_t eq, int ties, int need, P
   __syncthreads();
   if (t < ties) {  // rank = number of smaller tied IDs (IDs are distinct)
     const uint32_t x = s.tie[t];
-    int rk = 0;
-    for (int j = 0; j < ties; ++j) rk += s.tie[j] < x;
-    win[t] = rk < need;
+    win[t] = count_below(s.tie, ties, x) < need;
   }
   __syncthreads();
   uint64_t m = 0, rest = eq;
@@ -85,7 +83,8 @@ struct OctResult {
 };
 
 template <bool VALUE_ONLY, bool POS_IDS, typename IdFn>
-__device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s) {
+__device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s,
+                                                int ts = -1) {
   OctResult res;
   res.ok = true;
   res.mine = 0;
@@ -112,8 +111,10 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
     }
   }
   __syncthreads();
+  SKV_TS(ts, 1);
   fs_rank_bin(s, k);
   __syncthreads();
+  SKV_TS(ts, 2);
   const int b1 = s.sel[0];
   const int acc1 = s.sel[1];
   const int total = s.sel[2];
@@ -132,6 +133,7 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
   __syncthreads();
   fs_rank_digit(s, k, acc1);
   __syncthreads();
+  SKV_TS(ts, 3);
   const uint32_t v = ((uint32_t)b1 << 4) | (uint32_t)s.sel[0];
   const int above = s.sel[1];
   const int ties = s.sel[3];
