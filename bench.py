@@ -66,11 +66,11 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         "select": G * H * nc * 6 + G * nc // 8 + G * (p.sink + p.local) * 512
         + 16 * ((p.sink + p.local + 255) // 256) * 258 * 4,
         # upper bounds in, survivor masks out; CSR bounds of the selected
-        # lists, mate and token of each of their postings in; pool tokens and
-        # posting indices out
-        "pool": G * nc * (H * 2 + 1) + sel * 8 + scanned * (4 + 4) + pool * 8,
-        # posting indices and their 64 B prefix rows in; 2-bit scores out
-        "score2": pool * (4 + 64 + H * 2),
+        # lists, mate and token of each of their postings in; pool tokens
+        # out; the 64 B prefix row of each pool key in, its 2-bit scores and
+        # the 16-key tile maxima out
+        "pool": G * nc * (H * 2 + 1) + sel * 8 + scanned * (4 + 4) + pool * 4
+        + pool * (64 + H * 2) + H * pool // 16 * 2,
         # pool scores in; member bitmaps out
         "top1600": pool * H * 2 + bm_pool,
         # member bitmaps + pool tokens in; U1 tokens, their 128 B (prefix |

@@ -87,9 +87,9 @@ __device__ __forceinline__ uint32_t ordered16(uint32_t b) {
 }
 
 __device__ __forceinline__ uint32_t bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t nan = ((u >> 16) | 0x40u) & 0xffffu, r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? nan : r;  // a select, no branch
 }
 
 __device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
@@ -106,6 +106,24 @@ __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float f[4]) {
 __device__ __forceinline__ float scaled_f32(int64_t Dv, int e) {
   return __double2float_rn(ldexp((double)Dv, e));
 }
+
+// scaled_f32(2^m dq + off, e) for the dot dq = x0 + 2^8 x1 + 2^16 x2 of a
+// matrix core's limb sums (|x_i| < 2^24, |off| < 2^40) without 64-bit
+// integer arithmetic: every partial sum below is an exact double (a
+// multiple of 2^e under 2^53 of them), so the one rounding is the final
+// conversion, as in scaled_f32.
+struct LimbScale {
+  double p0, p1, p2, c;  // 2^(e+m), 2^(e+m+8), 2^(e+m+16), off 2^e
+  __device__ LimbScale(int e, int m, int64_t off) {
+    p0 = ldexp(1.0, e + m);
+    p1 = ldexp(1.0, e + m + 8);
+    p2 = ldexp(1.0, e + m + 16);
+    c = ldexp((double)off, e);
+  }
+  __device__ float operator()(int x0, int x1, int x2) const {
+    return __double2float_rn(__fma_rn((double)x2, p2, __fma_rn((double)x1, p1, __fma_rn((double)x0, p0, c))));
+  }
+};
 
 // RNE_f32(sqrt(N) * 2^fx) by integer arithmetic: the root of N << 2k
 // (largest k keeping it below 2^62) carries >= 26 significant bits, a sticky

@@ -11,8 +11,8 @@
 //               and the q15 / qs operands
 //   pool        survivor masks; postings owned under the spill-2 mate rule;
 //               selected list + pool tokens in encounter order (one pass,
-//               decoupled look-back over the centroid ranges)
-//   score2      2-bit scores of the pool
+//               decoupled look-back over the centroid ranges) and the 2-bit
+//               scores of the pool keys
 //   top1600     per head: top-1600 of the pool -> membership bitmap
 //   union_score4  U1 = union over heads in pool order + 4-bit scores of U1
 //   top256      per head: top-256 of U1 -> membership bitmap
@@ -643,7 +643,7 @@ __device__ __forceinline__ bool owned(const uint32_t* selbm, uint32_t mate, uint
   return mate > c || !((selbm[mate >> 5] >> (mate & 31)) & 1u);
 }
 
-constexpr int PL_BLOCK = 1024;  // pool: one posting per thread and page, one block per CU
+constexpr int PL_BLOCK = 1024;  // pool: one block per CU; waves 1.. hold a posting per thread and page
 constexpr int PL_WAVES = PL_BLOCK / WAVE;
 constexpr int PL_RANGE_MAX = PL_BLOCK;  // centroids per pool block: one per thread
 // The range scan packs (postings << PL_SEL_BITS) | selected into one unsigned
@@ -653,9 +653,9 @@ constexpr int PL_RANGE_MAX = PL_BLOCK;  // centroids per pool block: one per thr
 constexpr int PL_SEL_BITS = 11;
 constexpr unsigned PL_SEL_MASK = (1u << PL_SEL_BITS) - 1u;
 static_assert(PL_RANGE_MAX <= (int)PL_SEL_MASK, "a range's selected count fits its scan field");
-constexpr int S2_BLOCK = 256;  // score2 threads per block
-constexpr int S2_GRID = 320;   // score2 blocks per group
-constexpr int S2_TILES = 2;    // 16-item tiles per wave and pass (loads issued together)
+constexpr int PL_PAGE = PL_BLOCK - WAVE;     // postings per page (waves 1..)
+// 16-key tiles of s2 the first two pages' owned postings overlap (at most)
+constexpr int PL_TM_TILES = (2 * PL_PAGE + 15) / 16 + 1;
 
 // Range records for the look-back, one 64-bit word written and read whole:
 // state (bits 62..63) | launch epoch (57..61) | coarse survivors (40..56) |
@@ -675,6 +675,79 @@ __device__ __forceinline__ int lb_field(unsigned long long v, int shift, int bit
   return (int)((v >> shift) & ((1ull << bits) - 1));
 }
 
+// 2-bit pool scores (reference codegen/stage15.py:886-995):
+// s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) of a key from its 64-byte prefix row
+// (the posting-ordered copy), 16 keys per int8 matrix-core tile.  A wave
+// scores the 64 postings its lanes hold, 4 tiles: s2_rows loads tile u's
+// rows (lane (kb, row) reads bytes 16 kb .. 16 kb + 15 of the row of the
+// posting held by lane 16 u + row; j < 0: absent, zeros).  s2_score
+// multiplies the query image (rows: head x limb) by the keys (columns), so
+// lane l receives the 4 limb sums of key l % 16 for head l / 16 in its 4
+// accumulator registers (no exchange between lanes), and returns in sc[u]
+// that key's ordered score; ls is head l / 16's scale.
+__device__ __forceinline__ void s2_rows(const uint8_t* __restrict__ rows, int j, uint4 (&w)[4]) {
+  const int lane = threadIdx.x & 63, row = lane & 15, kb = lane >> 4;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int jj = __shfl(j, 16 * u + row);
+    w[u] = jj >= 0 ? *reinterpret_cast<const uint4*>(rows + (size_t)jj * 64 + kb * 16)
+                   : make_uint4(0, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void s2_score(const uint4 (&w)[4], const uint32_t (&bq)[4][4],
+                                         const LimbScale& ls, uint32_t (&sc)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      uint32_t av[4];
+      expand2t(words[kc], av);
+      acc = mfma_i8(bq[kc], av, acc);
+    }
+    sc[u] = ordered16(bf16_rne(ls(acc[0], acc[1], acc[2])));  // 2 dq - 3 sum(q15), 2^fx
+  }
+}
+
+// Stores the scores of s2_score for the owned postings: own = the wave's
+// ballot of owned postings (bit p: the posting lane p holds), wbase = the
+// segment rank of its first owned posting; rank r lands at pool position
+// base + r.  With tm, each score also raises tm[head][tile - t0], the LDS
+// maximum of its 16-key tile (pool position / 16).
+__device__ __forceinline__ void s2_emit(const uint32_t (&sc)[4], uint64_t own, int wbase, int base,
+                                        uint16_t* s2, int cap, uint32_t* tm, int t0) {
+  const int lane = threadIdx.x & 63, hq = lane >> 4;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int p = 16 * u + (lane & 15);
+    if ((own >> p) & 1ull) {
+      const int pos = base + wbase + __popcll(own & ((1ull << p) - 1ull));
+      if (pos < cap) s2[(size_t)hq * cap + pos] = (uint16_t)sc[u];
+      if (tm) atomicMax(&tm[hq * PL_TM_TILES + (pos >> 4) - t0], sc[u]);
+    }
+  }
+}
+
+// Maxima of the 16-key tiles of s2 ([H][tstride] words) that the pool
+// positions [A, A + L) overlap.  With tm (the LDS maxima of s2_emit,
+// tm[head][tile - A / 16]) a tile inside the segment gets its exact
+// maximum, and so does its last tile when the segment ends the pool
+// (end_exact: positions beyond hold no key); any other tile gets 0xffff.
+// Such a tile is shared with another block, which writes 0xffff to it as
+// well: an upper bound, all the top-1600's tile skip needs.
+__device__ void s2_tile_max(int A, int L, bool end_exact, const uint32_t* tm, uint16_t* tmax,
+                            int tstride) {
+  if (L <= 0) return;
+  const int t_lo = A >> 4, nt = ((A + L - 1) >> 4) - t_lo + 1;
+  for (int x = threadIdx.x; x < nt * H; x += blockDim.x) {
+    const int h = x / nt, i = x - h * nt, tile = t_lo + i, s0 = 16 * tile;
+    const bool exact = tm && s0 >= A && (s0 + 16 <= A + L || end_exact);
+    if (tile < tstride) tmax[(size_t)h * tstride + tile] = (uint16_t)(exact ? tm[h * PL_TM_TILES + i] : 0xffffu);
+  }
+}
+
 __device__ __forceinline__ unsigned long long lb_load(const unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -683,12 +756,14 @@ __device__ __forceinline__ void lb_store(unsigned long long* p, unsigned long lo
 }
 
 // The pool of one KV group in encounter order: selected clusters ascending,
-// CSR order within a cluster, each token kept at its first occurrence.
-// Block b = range b of pool_range centroids (a multiple of 32).  Each range
-// publishes its counts, then sums its predecessors' counts (decoupled
-// look-back: a predecessor that already published its inclusive prefix ends
-// the walk) and writes its owned postings at their pool positions, one
-// posting per thread.
+// CSR order within a cluster, each token kept at its first occurrence, and
+// the 2-bit scores of its keys.  Block b = range b of pool_range centroids
+// (a multiple of 32).  Each range publishes its counts, then sums its
+// predecessors' counts (decoupled look-back: a predecessor that already
+// published its inclusive prefix ends the walk) and writes its owned
+// postings at their pool positions, one posting per thread.  The prefix
+// rows of the range's postings are loaded before the look-back and scored
+// while wave 0 walks it, so the scores are ready with the positions.
 __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   SKV_TSB(0, 0);
   SKV_TS(5, 0);
@@ -698,6 +773,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   __shared__ int s_off[PL_RANGE_MAX + 1], s_cum[PL_RANGE_MAX + 1], s_cl[PL_RANGE_MAX];
   __shared__ int s_scan[PL_WAVES + 1], s_surv, s_scanned;
   __shared__ unsigned long long s_excl;
+  __shared__ uint32_t s_tm[H * PL_TM_TILES];  // tile maxima of the first two pages' keys
   // range b = block b: workgroups are dispatched in index order within each
   // XCD, so the lowest unfinished range always gets a slot and every wait
   // below ends.  The launch epoch tags this launch's records.
@@ -723,6 +799,12 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     upv[h] = a.upper[((size_t)g * H + h) * nc + cu];
     thv[h] = a.thr[g * H + h];
   }
+  // the 2-bit scorer's query operand (B image of 16 q15, its sum and scale)
+  const QOperand* q15 = &a.qop[g * QV_COUNT + QV_Q15];
+  uint32_t bq[4][4];
+  load_b(q15, bq);
+  // lane l's head l / 16: s2 = (2 dq - 3 sum q15) 2^(fx + 4)
+  const LimbScale ls(q15->fx[lane >> 4] + 4, 1, -3 * q15->sum[lane >> 4]);
 #pragma unroll
   for (int u = 0; u < BM_PER; ++u)
     if (t + u * PL_BLOCK < nbw) s_bm[t + u * PL_BLOCK] = bmw[u];
@@ -732,6 +814,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     s_surv = 0;
     s_scanned = 0;
   }
+  if (t < H * PL_TM_TILES) s_tm[t] = 0;
   // survivor head masks (upper_h >= thr_h) of the range's centroids
   uint32_t m = 0;
   if (t < ncr) {
@@ -779,27 +862,35 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     j = locate(i, cl);
     return owned(s_bm, (uint32_t)mate[j], (uint32_t)(c0 + cl));
   };
-  // ---- count: the first two pages stay in registers for the emit (their
-  // mate and token loads issued together); later pages are re-walked
-  const bool h0 = (int)threadIdx.x < S, h1 = (int)threadIdx.x + PL_BLOCK < S;
+  // ---- count: postings go to waves 1.. (PL_PAGE per page; wave 0 walks
+  // the look-back while they are scored).  The first two pages stay in
+  // registers for the emit (their mate, token and prefix-row loads issued
+  // together); later pages are re-walked.
+  const int pi = (int)threadIdx.x - WAVE;  // this thread's posting of a page (wave 0: none)
+  const bool h0 = pi >= 0 && pi < S, h1 = pi >= 0 && pi + PL_PAGE < S;
   int cl0 = 0, cl1 = 0;
-  const int j0 = h0 ? locate(threadIdx.x, cl0) : 0;
-  const int j1 = h1 ? locate(threadIdx.x + PL_BLOCK, cl1) : 0;
+  const int j0 = h0 ? locate(pi, cl0) : -1;
+  const int j1 = h1 ? locate(pi + PL_PAGE, cl1) : -1;
   const int m0 = h0 ? mate[j0] : -1, m1 = h1 ? mate[j1] : -1;
   const int t0 = h0 ? ptok[j0] : 0, t1 = h1 ? ptok[j1] : 0;
   const bool o0 = h0 && owned(s_bm, (uint32_t)m0, (uint32_t)(c0 + cl0));
   const bool o1 = h1 && owned(s_bm, (uint32_t)m1, (uint32_t)(c0 + cl1));
-  int owned_total;
-  const int ex0 = block_excl_scan(o0 ? 1 : 0, s_scan, &owned_total);
-  const int page0_total = owned_total;
-  int ex1 = 0, page1_total = 0;
-  if (S > PL_BLOCK) {  // block-uniform
-    ex1 = block_excl_scan(o1 ? 1 : 0, s_scan, &page1_total);
-    owned_total += page1_total;
-  }
-  for (int base = 2 * PL_BLOCK; base < S; base += PL_BLOCK) {
+  // prefix rows of the first two pages' owned postings, issued once the
+  // mates are in; the rows (64 B per key) are the kernel's bulk traffic and
+  // arrive during the scans and the look-back
+  const uint8_t* __restrict__ rows = a.post_p2 + (size_t)g * a.np_max * 64;
+  uint4 rw0[4], rw1[4];
+  if (wave > 0) s2_rows(rows, o0 ? j0 : -1, rw0);  // wave-uniform
+  if (wave > 0 && S > PL_PAGE) s2_rows(rows, o1 ? j1 : -1, rw1);
+  // one scan for both pages: page 1 in the high half (a page owns < 2^16)
+  int both;
+  const int exb = block_excl_scan((o1 ? 1 << 16 : 0) | (o0 ? 1 : 0), s_scan, &both);
+  const int ex0 = exb & 0xffff, ex1 = exb >> 16;
+  const int page0_total = both & 0xffff, page1_total = both >> 16;
+  int owned_total = page0_total + page1_total;
+  for (int base = 2 * PL_PAGE; base < S; base += PL_PAGE) {
     int j = 0;
-    const bool o = (int)(base + threadIdx.x) < S && posting(base + threadIdx.x, j);
+    const bool o = pi >= 0 && base + pi < S && posting(base + pi, j);
     int tot;
     (void)block_excl_scan(o ? 1 : 0, s_scan, &tot);
     owned_total += tot;
@@ -902,6 +993,10 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     sc = wave_sum(sc);
     if (lane == 0) atomicAdd(&s_scanned, sc);
   }
+  // 2-bit scores of the first two pages (waves 1.. while wave 0 looks back)
+  uint32_t sc0[4] = {0, 0, 0, 0}, sc1[4] = {0, 0, 0, 0};
+  if (wave > 0 && (wave - 1) * WAVE < S) s2_score(rw0, bq, ls, sc0);  // wave-uniform
+  if (wave > 0 && PL_PAGE + (wave - 1) * WAVE < S) s2_score(rw1, bq, ls, sc1);
   __syncthreads();
   SKV_TSB(0, 1);
   const unsigned long long excl = s_excl;
@@ -910,28 +1005,35 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   // ---- emit: the selected list and the owned postings at their positions
   for (int r = t; r < nsel; r += PL_BLOCK) a.sel[(size_t)g * nc + sel0 + r] = c0 + s_cl[r];
   int* pool = a.pool_tok + (size_t)g * a.cap;
-  int* pool_post = a.pool_post + (size_t)g * a.cap;
-  if (o0 && pos0 + ex0 < a.cap) {
-    pool[pos0 + ex0] = t0;
-    pool_post[pos0 + ex0] = j0;
-  }
-  if (o1 && pos0 + page0_total + ex1 < a.cap) {
-    pool[pos0 + page0_total + ex1] = t1;
-    pool_post[pos0 + page0_total + ex1] = j1;
-  }
-  int carry = page0_total + page1_total;
-  for (int base = 2 * PL_BLOCK; base < S; base += PL_BLOCK) {  // ranges over two pages
-    int j = 0;
-    const bool o = (int)(base + threadIdx.x) < S && posting(base + threadIdx.x, j);
+  uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
+  uint16_t* tmax = a.s2_tmax + (size_t)g * H * (a.cap / 16);
+  if (o0 && pos0 + ex0 < a.cap) pool[pos0 + ex0] = t0;
+  if (o1 && pos0 + page0_total + ex1 < a.cap) pool[pos0 + page0_total + ex1] = t1;
+  s2_emit(sc0, __ballot(o0), __builtin_amdgcn_readfirstlane(ex0), pos0, s2, a.cap, s_tm, pos0 >> 4);
+  if (S > PL_PAGE)
+    s2_emit(sc1, __ballot(o1), page0_total + __builtin_amdgcn_readfirstlane(ex1), pos0, s2, a.cap,
+            s_tm, pos0 >> 4);
+  const int p01 = page0_total + page1_total;
+  int carry = p01;
+  for (int base = 2 * PL_PAGE; base < S; base += PL_PAGE) {  // ranges over two pages
+    int j = -1;
+    const bool o = pi >= 0 && base + pi < S && posting(base + pi, j);
+    uint4 rw[4];
+    if (wave > 0) s2_rows(rows, o ? j : -1, rw);
     int tot;
     const int ex = block_excl_scan(o ? 1 : 0, s_scan, &tot);
     const int p = pos0 + carry + ex;
-    if (o && p < a.cap) {
-      pool[p] = ptok[j];
-      pool_post[p] = j;
-    }
+    if (o && p < a.cap) pool[p] = ptok[j];
+    uint32_t sc[4] = {0, 0, 0, 0};
+    if (wave > 0 && base + (wave - 1) * WAVE < S) s2_score(rw, bq, ls, sc);
+    s2_emit(sc, __ballot(o), __builtin_amdgcn_readfirstlane(ex), pos0 + carry, s2, a.cap, nullptr,
+            0);
+    s2_tile_max(pos0 + carry, tot, false, nullptr, tmax, a.cap / 16);  // bounds only
     carry += tot;
   }
+  // tile maxima of the first two pages' segment (from the LDS maxima)
+  __syncthreads();
+  s2_tile_max(pos0, p01, b == nb - 1 && S <= 2 * PL_PAGE, s_tm, tmax, a.cap / 16);
   // ---- the last range writes the group's totals
   if (b == nb - 1 && threadIdx.x == 0) {
     {
@@ -950,77 +1052,6 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     }
   }
   SKV_TSE(0);
-}
-
-// 2-bit pool scores s2 = bf16(16 RNE(sum q15 (2 p2 - 3))) from each pool
-// key's prefix plane (its row in the posting-ordered copy), 16 pool items per
-// matrix-core tile, tiles spread over the grid (grid-stride).
-__global__ __launch_bounds__(S2_BLOCK) void k_score2(StepArgs a) {
-  SKV_TSB(2, 0);
-  SKV_TS(14, 0);
-  const int g = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int n = a.status[g * ST_WORDS + ST_POOL];
-  const int ntiles = (n + 15) / 16;
-  constexpr int WPB = S2_BLOCK / WAVE;
-  const int w0 = blockIdx.x * WPB + (threadIdx.x >> 6), wstride = gridDim.x * WPB;
-  if (w0 >= ntiles) {
-    SKV_TSE(2);
-    return;
-  }
-  const QOperand* q = &a.qop[g * QV_COUNT + QV_Q15];
-  uint32_t bq[4][4];
-  load_b(q, bq);
-  const int row = lane & 15, kb = lane >> 4, h = (lane & 15) >> 2;
-  const int64_t S = q->sum[h];
-  const int fx = q->fx[h] + 4;
-  // the prefix rows in posting order: pool keys of one cluster list are
-  // consecutive there, so the 64-byte rows are read as whole lines
-  const int* __restrict__ ppost = a.pool_post + (size_t)g * a.cap;
-  const uint8_t* __restrict__ rows = a.post_p2 + (size_t)g * a.np_max * 64;
-  uint16_t* s2 = a.s2 + (size_t)g * H * a.cap;
-  // S2_TILES tiles per wave and pass, all index and row loads issued first
-  for (int t0 = w0; t0 < ntiles; t0 += wstride * S2_TILES) {
-    int jp[S2_TILES];
-#pragma unroll
-    for (int u = 0; u < S2_TILES; ++u) {
-      const int i = (t0 + u * wstride) * 16 + row;
-      jp[u] = i < n ? ppost[i] : -1;
-    }
-    uint4 wv[S2_TILES];
-#pragma unroll
-    for (int u = 0; u < S2_TILES; ++u)
-      wv[u] = jp[u] >= 0 ? *reinterpret_cast<const uint4*>(rows + (size_t)jp[u] * 64 + kb * 16)
-                         : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int u = 0; u < S2_TILES; ++u) {
-      const int tile = t0 + u * wstride;
-      if (tile >= ntiles) break;  // wave-uniform
-      const uint32_t words[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-      v4i acc = {0, 0, 0, 0};
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        uint32_t av[4];
-        expand2t(words[kc], av);
-        acc = mfma_i8(av, bq[kc], acc);
-      }
-      // lane (kb, h, q) scores row 4kb + q of head h: every lane converts one
-      const int q = lane & 3;
-      const int64_t dq = limb_rows(acc);
-      const int ii = tile * 16 + 4 * kb + q;
-      const uint32_t o = ii < n ? ordered16(bf16_rne(scaled_f32(2 * dq - 3 * S, fx))) : 0u;
-      if (ii < n) s2[(size_t)h * a.cap + ii] = (uint16_t)o;
-      // the tile's max for each head: over the quad, then the 4 row groups
-      uint32_t vmax = o;
-      vmax = max(vmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)vmax, 0xB1, 0xf, 0xf, false));
-      vmax = max(vmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)vmax, 0x4E, 0xf, 0xf, false));
-      vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 16));
-      vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, 32));
-      if (lane < 16 && q == 0) a.s2_tmax[((size_t)g * H + h) * (a.cap / 16) + tile] = (uint16_t)vmax;
-    }
-  }
-  SKV_TS(14, 15);
-  SKV_TSE(2);
 }
 
 // ============================================================ token top-k
@@ -1485,8 +1516,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
-    "front", "select", "pool", "score2", "top1600", "union_score4", "top256", "union_score8",
-    "top100_sdpa"};
+    "front", "select", "pool", "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
 
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
@@ -1510,21 +1540,18 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
                          bm_lds, st, a);
       break;
     case 3:
-      hipLaunchKernelGGL(k_score2, dim3(S2_GRID, G), dim3(S2_BLOCK), 0, st, a);
-      break;
-    case 4:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
       break;
-    case 5:
+    case 4:
       hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(us_block(4)), 0, st, a);
       break;
-    case 6:
+    case 5:
       hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
       break;
-    case 7:
+    case 6:
       hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(us_block(8)), 0, st, a);
       break;
-    case 8:
+    case 7:
       hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
       break;
     default:

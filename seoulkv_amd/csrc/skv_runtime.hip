@@ -466,7 +466,6 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.pool_flags = (unsigned long long*)ar.take((size_t)G * a.pool_blocks * 8);
     a.pool_epoch = (unsigned*)ar.take((size_t)G * 4);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
-    a.pool_post = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);
     a.s2_tmax = (uint16_t*)ar.take((size_t)G * H * (a.cap / 16) * 2);
     a.dense_part = (float*)ar.take((size_t)G * H * std::max(max_slices, 1) * (D + 2) * 4);

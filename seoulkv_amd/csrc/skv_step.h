@@ -9,8 +9,7 @@
 //                    _kernels/stage1_fine/seoulkv4_fine_native_select.py:35-73 (top-P union)
 //   k_pool           _kernels/stage1_coarse/seoulkv4_coarse_select.py:334-379 (survivor
 //                    masks); codegen/stage15.py:275-345 (mate-ownership dedup,
-//                    encounter-order pool)
-//   k_score2         codegen/stage15.py:886-995 (2-bit scores)
+//                    encounter-order pool); codegen/stage15.py:886-995 (2-bit scores)
 //   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
 //   k_union_score<4> codegen/stage15.py:1519-1597 (U1) +
 //                    _kernels/stage16/seoulkv4_stage16_matrix.py:21-60 (4-bit scores)
@@ -94,9 +93,9 @@ struct StepArgs {
   unsigned long long* pool_flags;  // [G][pool_blocks] look-back records (epoch-tagged)
   unsigned* pool_epoch;     // [G] launches of the pool kernel (tags the look-back records)
   int* pool_tok;            // [G][cap]
-  int* pool_post;           // [G][cap] posting index (into post_p2) of each pool key
   uint16_t* s2;             // [G][H][cap] ordered
-  uint16_t* s2_tmax;        // [G][H][cap/16] max of every 16-key tile of s2
+  uint16_t* s2_tmax;        // [G][H][cap/16] upper bound (exact max, or 0xffff for a
+                            // tile two pool blocks share) of every 16-key tile of s2
   uint64_t* bm_u1;          // [G][H][words_u1] top-1600 members
   uint64_t* bm_u2;          // [G][H][words_u2] top-256 members
   float* dense_part;        // [16][dense_slices][D + 2] sink/local partial (o, max, sum)
@@ -145,7 +144,7 @@ constexpr int DENSE_SLICE_KEYS = ATTN_WAVES * 16;
 // member-bitmap words the top-k kernel keeps in LDS beside its scratch
 constexpr int TOPK_LDS_WORDS = 2048;
 
-constexpr int N_STEP_KERNELS = 9;
+constexpr int N_STEP_KERNELS = 8;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 // Kernel k (0 .. N_STEP_KERNELS - 1, in step order) of one decode step.
