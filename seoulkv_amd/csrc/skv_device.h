@@ -69,8 +69,8 @@ enum { QV_RAW = 0, QV_Q15 = 1, QV_QS = 2, QV_COUNT = 3 };
 
 // Per (group, variant) query operand block, written by the query-prep kernel.
 struct QOperand {
-  // int8 MFMA B image: [chunk kc][lane][16 bytes]; lane l holds column l%16
-  // (head (l%16)/4, limb (l%16)%4, limb 3 = 0) for dims
+  // int8 matrix-core operand image: [chunk kc][lane][16 bytes]; lane l holds
+  // row l%16 (head (l%16)/4, limb (l%16)%4, limb 3 = 0) for dims
   // (l/16)*64 + kc*16 + [0,16).
   uint32_t bimg[4][WAVE][4];
   int64_t sum[H];   // S_h = sum_d X_h[d]
@@ -109,19 +109,18 @@ __device__ __forceinline__ float scaled_f32(int64_t Dv, int e) {
 
 // scaled_f32(2^m dq + off, e) for the dot dq = x0 + 2^8 x1 + 2^16 x2 of a
 // matrix core's limb sums (|x_i| < 2^24, |off| < 2^40) without 64-bit
-// integer arithmetic: every partial sum below is an exact double (a
-// multiple of 2^e under 2^53 of them), so the one rounding is the final
-// conversion, as in scaled_f32.
+// integer arithmetic: x2 2^(e+m+16) + x1 2^(e+m+8) + x0 2^(e+m) + off 2^e
+// in double FMAs, every partial sum exact (a multiple of 2^e under 2^53 of
+// them), so the one rounding is the final conversion, as in scaled_f32.
 struct LimbScale {
-  double p0, p1, p2, c;  // 2^(e+m), 2^(e+m+8), 2^(e+m+16), off 2^e
-  __device__ LimbScale(int e, int m, int64_t off) {
-    p0 = ldexp(1.0, e + m);
-    p1 = ldexp(1.0, e + m + 8);
-    p2 = ldexp(1.0, e + m + 16);
-    c = ldexp((double)off, e);
-  }
-  __device__ float operator()(int x0, int x1, int x2) const {
-    return __double2float_rn(__fma_rn((double)x2, p2, __fma_rn((double)x1, p1, __fma_rn((double)x0, p0, c))));
+  double p0, p1, p2;  // 2^(e+m), 2^(e+m+8), 2^(e+m+16)
+  __device__ LimbScale(int e, int m)
+      : p0(ldexp(1.0, e + m)), p1(ldexp(1.0, e + m + 8)), p2(ldexp(1.0, e + m + 16)) {}
+  // the offset term off 2^e
+  __device__ static double offset(int64_t off, int e) { return ldexp((double)off, e); }
+  __device__ float operator()(int x0, int x1, int x2, double c) const {
+    return __double2float_rn(
+        __fma_rn((double)x2, p2, __fma_rn((double)x1, p1, __fma_rn((double)x0, p0, c))));
   }
 };
 
@@ -288,46 +287,16 @@ __device__ __forceinline__ void expand4t(uint32_t w0, uint32_t w1, uint32_t out[
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// One 16-key x 16-column x 64-dim int8 matrix-core step.
+// One 16 x 16 x 64 int8 matrix-core step, C[m][n] += sum_k A[m][k] B[k][n]:
+// lane l supplies row (A) / column (B) l % 16 over k = 16 (l / 16) .. + 15
+// and receives C[4 (l / 16) + i][l % 16] in register i.  The scorers pass
+// the query image as A (rows: head x limb) and 16 keys as B, so lane l gets
+// the limb sums of key l % 16 for head l / 16.
 __device__ __forceinline__ v4i mfma_i8(const uint32_t a[4], const uint32_t b[4], v4i c) {
   v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
   v4i bv = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, c, 0, 0, 0);
 }
 
-// The 16 x 16 int32 tile of an int8 MFMA whose columns are (head, limb)
-// pairs (column 4 head + limb, limb 3 zero): returns, in lane l, the exact
-// dot of row 4 (l / 16) + (l % 4) for head (l % 16) / 4, the sum of its
-// limbs << 8 limb.  Lane = limb and register = row within a quad, so a 4 x 4
-// transpose of the quad (two exchange rounds: lanes q, q ^ 2 swap the
-// off-diagonal 2 x 2 blocks, then lanes q, q ^ 1 the off-diagonal entries of
-// each block) gives each lane the limbs of its own row.
-__device__ __forceinline__ int64_t limb_rows(v4i acc) {
-  const int q = threadIdx.x & 3;
-  int x0 = acc[0], x1 = acc[1], x2 = acc[2], x3 = acc[3];
-  const bool top = q < 2;
-  int s0 = top ? x2 : x0, s1 = top ? x3 : x1;
-  int r0 = __builtin_amdgcn_update_dpp(0, s0, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
-  int r1 = __builtin_amdgcn_update_dpp(0, s1, 0x4E, 0xf, 0xf, false);
-  if (top) {
-    x2 = r0;
-    x3 = r1;
-  } else {
-    x0 = r0;
-    x1 = r1;
-  }
-  const bool even = (q & 1) == 0;
-  s0 = even ? x1 : x0;
-  s1 = even ? x3 : x2;
-  r0 = __builtin_amdgcn_update_dpp(0, s0, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
-  r1 = __builtin_amdgcn_update_dpp(0, s1, 0xB1, 0xf, 0xf, false);
-  if (even) {
-    x1 = r0;
-  } else {
-    x0 = r0;
-    x2 = r1;
-  }
-  return (int64_t)x0 + ((int64_t)x1 << 8) + ((int64_t)x2 << 16);
-}
 
 }  // namespace skv

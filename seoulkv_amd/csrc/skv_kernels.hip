@@ -324,12 +324,24 @@ constexpr int FR_MAX_BLOCKS = 128;  // front blocks per group (each loops over i
 // group's per-step state (the q15 / qs operands of the later kernels are
 // formed by extra blocks of the selection launch).
 // Loads of one 16-centroid tile for one wave: the two planes (lane row
-// l % 16, dims (l / 16) * 16 ..) and the per-centroid factors of the lane's
-// output centroids c0 .. c0 + 3 (one 32-centroid block).
+// l % 16, dims (l / 16) * 16 ..), the residual norm of the lane's output
+// centroid l % 16 and the tile's 32-centroid block factors.
 struct FrTile {
   uint4 wu, wl;
-  float4 rs;
-  float sc4, gf;
+  float rs, sc4, gf;
+};
+
+// Per-lane conversion constants of the front (lane l converts head l / 16):
+// value = (2 dq - 3 S) 2^fx, fine = (2 dq - 15 S) 2^fx.
+struct FrConv {
+  LimbScale ls;
+  double cc, cf;
+  float norm;
+  __device__ FrConv(const QOperand& sq, int h)
+      : ls(sq.fx[h], 1),
+        cc(LimbScale::offset(-3 * sq.sum[h], sq.fx[h])),
+        cf(LimbScale::offset(-15 * sq.sum[h], sq.fx[h])),
+        norm(sq.norm[h]) {}
 };
 
 // Branch-free (a tile past the end reloads the last one, unused), so the
@@ -341,61 +353,58 @@ __device__ __forceinline__ FrTile fr_load(const StepArgs& a, int g, int tile, in
   const size_t rowoff = ((size_t)g * nc + tt * 16 + row) * 64 + kb * 16;
   t.wu = *reinterpret_cast<const uint4*>(a.cen_up + rowoff);
   t.wl = *reinterpret_cast<const uint4*>(a.cen_lo + rowoff);
-  const int c0 = tt * 16 + 4 * kb;
-  t.rs = *reinterpret_cast<const float4*>(a.resid + (size_t)g * nc + c0);
-  t.sc4 = a.scale4[(size_t)g * (nc / 32) + (c0 >> 5)];
-  t.gf = a.gfs[(size_t)g * (nc / 32) + (c0 >> 5)];
+  t.rs = a.resid[(size_t)g * nc + tt * 16 + row];
+  t.sc4 = a.scale4[(size_t)g * (nc / 32) + (tt >> 1)];
+  t.gf = a.gfs[(size_t)g * (nc / 32) + (tt >> 1)];
   return t;
 }
 
-// Coarse bounds and fine scores of one tile's 16 centroids x 4 heads.
+// Coarse bounds and fine scores of one tile's 16 centroids x 4 heads.  The
+// query image is the matrix core's row operand (head x limb) and the tile's
+// centroids its columns, so lane l holds the limb sums of centroid l % 16
+// for head l / 16 and converts them itself.
 __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int lane, const FrTile& t,
-                                         const uint32_t (&b)[4][4], const QOperand& sq) {
-  const int nc = a.nc, kb = lane >> 4;
+                                         const uint32_t (&b)[4][4], const FrConv& cv) {
+  const int nc = a.nc;
   const uint32_t up[4] = {t.wu.x, t.wu.y, t.wu.z, t.wu.w};
   const uint32_t lo[4] = {t.wl.x, t.wl.y, t.wl.z, t.wl.w};
   // the 4-bit code is 4 upper + lower, so its dot is 4 (upper dot) + (lower
-  // dot), exact in each int32 limb column (|sum| <= 256 * 128 * 15)
+  // dot), exact in each int32 limb (|sum| <= 256 * 128 * 15)
   v4i acc_c = {0, 0, 0, 0}, acc_l = {0, 0, 0, 0};
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc) {
     uint32_t eu[4], el[4];
     expand2t(up[kc], eu);
     expand2t(lo[kc], el);
-    acc_c = mfma_i8(eu, b[kc], acc_c);
-    acc_l = mfma_i8(el, b[kc], acc_l);
+    acc_c = mfma_i8(b[kc], eu, acc_c);
+    acc_l = mfma_i8(b[kc], el, acc_l);
   }
   const v4i acc_f = acc_c * 4 + acc_l;
-  // lane (kb, h, q) converts centroid 4kb + q of the tile for head h
-  const int h = (lane & 15) >> 2, q = lane & 3;
-  const int64_t dcq = limb_rows(acc_c), dfq = limb_rows(acc_f);
-  const int64_t S = sq.sum[h];
-  const int fx = sq.fx[h];
-  const float res = q == 0 ? t.rs.x : q == 1 ? t.rs.y : q == 2 ? t.rs.z : t.rs.w;
-  const float value = __fmul_rn(scaled_f32(2 * dcq - 3 * S, fx), t.sc4);
-  const float margin = __fmul_rn(sq.norm[h], res);
-  const size_t o = ((size_t)g * H + h) * nc + tile * 16 + 4 * kb + q;
+  const int h = lane >> 4, r = lane & 15;
+  const float value = __fmul_rn(cv.ls(acc_c[0], acc_c[1], acc_c[2], cv.cc), t.sc4);
+  const float margin = __fmul_rn(cv.norm, t.rs);
+  const size_t o = ((size_t)g * H + h) * nc + tile * 16 + r;
   const uint32_t lo16 = ordered16(bf16_rne(__fsub_rn(value, margin)));
   a.lower[o] = (uint16_t)lo16;
   a.upper[o] = (uint16_t)ordered16(bf16_rne(__fadd_rn(value, margin)));
-  const uint32_t fb = bf16_rne(__fmul_rn(scaled_f32(2 * dfq - 15 * S, fx), t.gf));
+  const uint32_t fb = bf16_rne(__fmul_rn(cv.ls(acc_f[0], acc_f[1], acc_f[2], cv.cf), t.gf));
   const uint32_t fo = ordered16(fb);
   a.fine_ord[o] = (uint16_t)fo;
   if (a.debug) a.fine_bits[o] = (uint16_t)fb;
   if (a.tmax_lo) {
-    // 8-centroid tile maxima: the quad's 4 rows, then rows 4kb.. and 4(kb+1)..
-    // (lanes l, l + 16); the fine-score maximum of the whole 16-centroid tile
+    // 8-centroid tile maxima: within each quad, then the two quads of each
+    // half row (half-row mirror); the fine-score maximum of the whole row
     uint32_t lmax = lo16, fmax = fo;
     lmax = max(lmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lmax, 0xB1, 0xf, 0xf, false));
     lmax = max(lmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lmax, 0x4E, 0xf, 0xf, false));
-    lmax = max(lmax, (uint32_t)__shfl_xor((int)lmax, 16));
-    if (q == 0 && (kb & 1) == 0)
-      a.tmax_lo[((size_t)g * H + h) * (nc / 8) + tile * 2 + (kb >> 1)] = (uint16_t)lmax;
+    lmax = max(lmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lmax, 0x141, 0xf, 0xf, false));
+    if ((r & 7) == 0)
+      a.tmax_lo[((size_t)g * H + h) * (nc / 8) + tile * 2 + (r >> 3)] = (uint16_t)lmax;
     fmax = max(fmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)fmax, 0xB1, 0xf, 0xf, false));
     fmax = max(fmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)fmax, 0x4E, 0xf, 0xf, false));
-    fmax = max(fmax, (uint32_t)__shfl_xor((int)fmax, 16));
-    fmax = max(fmax, (uint32_t)__shfl_xor((int)fmax, 32));
-    if (lane < 16 && q == 0) a.tmax_fi[((size_t)g * H + h) * (nc / 16) + tile] = (uint16_t)fmax;
+    fmax = max(fmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)fmax, 0x141, 0xf, 0xf, false));
+    fmax = max(fmax, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)fmax, 0x128, 0xf, 0xf, false));
+    if (r == 0) a.tmax_fi[((size_t)g * H + h) * (nc / 16) + tile] = (uint16_t)fmax;
   }
 }
 
@@ -428,13 +437,14 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
       const uint4 w = *reinterpret_cast<const uint4*>(&sq.bimg[kc][lane][0]);
       b[kc][0] = w.x; b[kc][1] = w.y; b[kc][2] = w.z; b[kc][3] = w.w;
     }
+    const FrConv cv(sq, lane >> 4);
     if (!LOOP) {
-      fr_score(a, g, tile, lane, cur, b, sq);
+      fr_score(a, g, tile, lane, cur, b, cv);
     } else {
       for (;;) {
         const int next = tile + step;
         const FrTile nxt = fr_load(a, g, next, lane);
-        fr_score(a, g, tile, lane, cur, b, sq);
+        fr_score(a, g, tile, lane, cur, b, cv);
         if (next >= ntiles) break;
         cur = nxt;
         tile = next;
@@ -696,7 +706,7 @@ __device__ __forceinline__ void s2_rows(const uint8_t* __restrict__ rows, int j,
 }
 
 __device__ __forceinline__ void s2_score(const uint4 (&w)[4], const uint32_t (&bq)[4][4],
-                                         const LimbScale& ls, uint32_t (&sc)[4]) {
+                                         const LimbScale& ls, double c, uint32_t (&sc)[4]) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
@@ -707,7 +717,7 @@ __device__ __forceinline__ void s2_score(const uint4 (&w)[4], const uint32_t (&b
       expand2t(words[kc], av);
       acc = mfma_i8(bq[kc], av, acc);
     }
-    sc[u] = ordered16(bf16_rne(ls(acc[0], acc[1], acc[2])));  // 2 dq - 3 sum(q15), 2^fx
+    sc[u] = ordered16(bf16_rne(ls(acc[0], acc[1], acc[2], c)));  // (2 dq - 3 sum q15) 2^fx
   }
 }
 
@@ -804,7 +814,8 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   uint32_t bq[4][4];
   load_b(q15, bq);
   // lane l's head l / 16: s2 = (2 dq - 3 sum q15) 2^(fx + 4)
-  const LimbScale ls(q15->fx[lane >> 4] + 4, 1, -3 * q15->sum[lane >> 4]);
+  const LimbScale ls(q15->fx[lane >> 4] + 4, 1);
+  const double lc = LimbScale::offset(-3 * q15->sum[lane >> 4], q15->fx[lane >> 4] + 4);
 #pragma unroll
   for (int u = 0; u < BM_PER; ++u)
     if (t + u * PL_BLOCK < nbw) s_bm[t + u * PL_BLOCK] = bmw[u];
@@ -995,8 +1006,8 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   }
   // 2-bit scores of the first two pages (waves 1.. while wave 0 looks back)
   uint32_t sc0[4] = {0, 0, 0, 0}, sc1[4] = {0, 0, 0, 0};
-  if (wave > 0 && (wave - 1) * WAVE < S) s2_score(rw0, bq, ls, sc0);  // wave-uniform
-  if (wave > 0 && PL_PAGE + (wave - 1) * WAVE < S) s2_score(rw1, bq, ls, sc1);
+  if (wave > 0 && (wave - 1) * WAVE < S) s2_score(rw0, bq, ls, lc, sc0);  // wave-uniform
+  if (wave > 0 && PL_PAGE + (wave - 1) * WAVE < S) s2_score(rw1, bq, ls, lc, sc1);
   __syncthreads();
   SKV_TSB(0, 1);
   const unsigned long long excl = s_excl;
@@ -1025,7 +1036,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
     const int p = pos0 + carry + ex;
     if (o && p < a.cap) pool[p] = ptok[j];
     uint32_t sc[4] = {0, 0, 0, 0};
-    if (wave > 0 && base + (wave - 1) * WAVE < S) s2_score(rw, bq, ls, sc);
+    if (wave > 0 && base + (wave - 1) * WAVE < S) s2_score(rw, bq, ls, lc, sc);
     s2_emit(sc, __ballot(o), __builtin_amdgcn_readfirstlane(ex), pos0 + carry, s2, a.cap, nullptr,
             0);
     s2_tile_max(pos0 + carry, tot, false, nullptr, tmax, a.cap / 16);  // bounds only
@@ -1267,6 +1278,11 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
   uint32_t b[4][4];
   load_b(q, b);
   const int row = lane & 15, kb = lane >> 4;
+  // lane l converts key l % 16 of a tile for head l / 16:
+  // 4-bit (2 dq - 15 S) 2^(fx + 4), 8-bit (2 dq - 255 S) 2^fx
+  const int hq = lane >> 4;
+  const LimbScale ls(q->fx[hq] + (U1 ? 4 : 0), 1);
+  const double lc = LimbScale::offset((U1 ? -15 : -255) * q->sum[hq], q->fx[hq] + (U1 ? 4 : 0));
   for (int c0 = w_lo; c0 < w_hi; c0 += US_CHUNK) {
     const int nw = min(US_CHUNK, w_hi - c0);
     const bool first = c0 == w_lo;
@@ -1304,7 +1320,7 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
         uint32_t av[4][4] = {};
         if (i_in < nloc) load_code4(a.keyrec + ((size_t)g * a.rec_rows + s_tok[i_in]) * 256, kb, av);
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(av[kc], b[kc], acc);
+        for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(b[kc], av[kc], acc);
       } else {
         uint32_t hi[4][4] = {}, lo[4][4] = {};
         if (i_in < nloc) {
@@ -1319,26 +1335,17 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
         v4i acc_lo = {0, 0, 0, 0};
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
-          acc = mfma_i8(hi[kc], b[kc], acc);
-          acc_lo = mfma_i8(lo[kc], b[kc], acc_lo);
+          acc = mfma_i8(b[kc], hi[kc], acc);
+          acc_lo = mfma_i8(b[kc], lo[kc], acc_lo);
         }
-        // 8-bit dot = 16 x (code4 dot) + (residual-4 dot); lane (kb, h, q)
-        // converts key 4kb + q of the tile for head h
-        const int64_t dhq = limb_rows(acc), dlq = limb_rows(acc_lo);
-        const int h = (lane & 15) >> 2;
-        const int i = tile * 16 + 4 * kb + (lane & 3), o = base + i;
-        if (i < nloc && o < cap_out)
-          s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
-              bf16_rne(scaled_f32(2 * (16 * dhq + dlq) - 255 * q->sum[h], q->fx[h])));
-        continue;
+        // 8-bit dot = 16 x (code4 dot) + (residual-4 dot), limb by limb
+        // (|16 hi + lo| < 2^23 per limb)
+        acc = acc * 16 + acc_lo;
       }
-      // lane (kb, h, q) converts key 4kb + q of the tile for head h
-      const int64_t dq = limb_rows(acc);
-      const int h = (lane & 15) >> 2;
-      const int i = tile * 16 + 4 * kb + (lane & 3), o = base + i;
+      const int i = tile * 16 + row, o = base + i;
       if (i < nloc && o < cap_out)
-        s_out[((size_t)g * H + h) * cap_out + o] = (uint16_t)ordered16(
-            bf16_rne(scaled_f32(2 * dq - 15 * q->sum[h], q->fx[h] + 4)));
+        s_out[((size_t)g * H + hq) * cap_out + o] =
+            (uint16_t)ordered16(bf16_rne(ls(acc[0], acc[1], acc[2], lc)));
     }
     base += nloc;
     __syncthreads();
