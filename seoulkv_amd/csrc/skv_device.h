@@ -13,45 +13,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace skv {
+#include "skv_trace.h"
 
-// Phase timestamps for development builds (-DSKV_TRACE): thread 0 of block
-// (0, 0) stores the 100 MHz real-time counter at point i of kernel slot k;
-// skv_trace_read copies the table out.  Compiled out otherwise.
-#ifdef SKV_TRACE
-extern __device__ unsigned long long g_skv_trace[32][16];
-#define SKV_TS(k, i)                                                           \
-  do {                                                                         \
-    if ((k) >= 0 && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)   \
-      g_skv_trace[(k)][(i)] = __builtin_amdgcn_s_memrealtime();                \
-  } while (0)
-// SKV_TSB(k, i): every block's thread 0 records point i of kernel slot k
-// (first 4096 blocks, x-major over (blockIdx.x, blockIdx.y)); SKV_TSE(k):
-// point 3 = the latest time any wave of the block reached it.
-extern __device__ unsigned long long g_skv_trace_blk[12][4096][4];
-#define SKV_TSB(k, i)                                                          \
-  do {                                                                         \
-    const unsigned _b = blockIdx.x + blockIdx.y * gridDim.x;                   \
-    if (threadIdx.x == 0 && _b < 4096)                                         \
-      g_skv_trace_blk[(k)][_b][(i)] = __builtin_amdgcn_s_memrealtime();        \
-  } while (0)
-#define SKV_TSE(k)                                                             \
-  do {                                                                         \
-    const unsigned _b = blockIdx.x + blockIdx.y * gridDim.x;                   \
-    if ((threadIdx.x & 63) == 0 && _b < 4096)                                  \
-      atomicMax(&g_skv_trace_blk[(k)][_b][3], __builtin_amdgcn_s_memrealtime()); \
-  } while (0)
-#else
-#define SKV_TS(k, i) \
-  do {               \
-  } while (0)
-#define SKV_TSB(k, i) \
-  do {                \
-  } while (0)
-#define SKV_TSE(k) \
-  do {             \
-  } while (0)
-#endif
+namespace skv {
 
 constexpr int G = 4;          // KV heads (index cells)
 constexpr int H = 4;          // query heads per KV head

@@ -34,7 +34,7 @@
 
 namespace skv {
 
-#ifdef SKV_TRACE
+#ifdef SKV_TRACE  // the tables of skv_trace.h
 __device__ unsigned long long g_skv_trace[32][16];
 __device__ unsigned long long g_skv_trace_blk[12][4096][4];
 #endif
@@ -978,14 +978,9 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
       s_excl = excl;
       // every range has published, so every block has read the epoch
       if (b == nb - 1) a.pool_epoch[g] = epoch + 1;
-#ifdef SKV_TRACE
-      {
-        const unsigned _bb = blockIdx.x + blockIdx.y * gridDim.x;
-        if (_bb < 4096) g_skv_trace_blk[10][_bb][0] = (unsigned long long)spins;
-        if (_bb < 4096) g_skv_trace_blk[10][_bb][1] = (unsigned long long)b;
-        if (_bb < 4096) g_skv_trace_blk[10][_bb][2] = (unsigned long long)S;
-      }
-#endif
+      SKV_TSV(10, 0, spins);
+      SKV_TSV(10, 1, b);
+      SKV_TSV(10, 2, S);
     }
   } else if (b == nb - 1) {  // the last range: postings of all selected lists
     // 16 centroids per thread and pass, their 17 CSR offsets loaded together

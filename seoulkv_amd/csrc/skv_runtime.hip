@@ -47,13 +47,18 @@ struct Arena {
 };
 
 constexpr int APPEND_CHUNK = 1024;  // tokens per host-append staging round
+constexpr int Q_RING = 8;           // query staging slots (host run-ahead, in steps)
 
 struct Handle {
   int device = 0;
   hipStream_t stream = nullptr;
   bool own_stream = false;
-  hipEvent_t q_copied = nullptr;
-  uint16_t* q_host = nullptr;  // pinned staging for bind_query
+  // pinned staging ring of skv_bind_query: slot i is reused once its
+  // previous upload (event q_copied[i]) has left it, so the host can run up
+  // to Q_RING steps ahead of the device
+  hipEvent_t q_copied[Q_RING] = {};
+  uint16_t* q_host = nullptr;  // [Q_RING][16][D]
+  unsigned q_next = 0;
   // device-query binding on a producer stream: the handle's steps so far
   // (readers of the query buffer) and the copy on the producer stream
   hipEvent_t steps_done = nullptr, q_ready = nullptr;
@@ -285,7 +290,8 @@ void skv_destroy(void* handle) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return;
   if (h->stream) (void)hipStreamSynchronize(h->stream);
-  if (h->q_copied) (void)hipEventDestroy(h->q_copied);
+  for (hipEvent_t e : h->q_copied)
+    if (e) (void)hipEventDestroy(e);
   if (h->steps_done) (void)hipEventDestroy(h->steps_done);
   if (h->q_ready) (void)hipEventDestroy(h->q_ready);
   for (hipEvent_t e : h->prof_ev)
@@ -606,8 +612,11 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   w.top_u1_lds = std::max(topk_bytes, (size_t)w.top_u1.lds_items * 2);
   w.top_u2_lds = std::max(topk_bytes, (size_t)w.top_u2.lds_items * 2);
 
-  if (hipHostMalloc((void**)&h->q_host, 16 * D * 2, hipHostMallocDefault) != hipSuccess ||
-      hipEventCreateWithFlags(&h->q_copied, hipEventDisableTiming) != hipSuccess ||
+  bool ring_ok = hipHostMalloc((void**)&h->q_host, (size_t)Q_RING * 16 * D * 2,
+                               hipHostMallocDefault) == hipSuccess;
+  for (int i = 0; i < Q_RING && ring_ok; ++i)
+    ring_ok = hipEventCreateWithFlags(&h->q_copied[i], hipEventDisableTiming) == hipSuccess;
+  if (!ring_ok ||
       hipEventCreateWithFlags(&h->steps_done, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&h->q_ready, hipEventDisableTiming) != hipSuccess) {
     fail(h, SKV_EHIP, "pinned query staging failed");
@@ -623,10 +632,15 @@ int skv_bind_query(void* handle, const uint16_t* q) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
   if (!q) return fail(h, SKV_EINVAL, "NULL query");
-  HIPCHK(h, hipEventSynchronize(h->q_copied));  // previous upload has left the staging buffer
-  memcpy(h->q_host, q, 16 * D * 2);
-  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, h->q_host, 16 * D * 2, hipMemcpyHostToDevice, h->stream));
-  HIPCHK(h, hipEventRecord(h->q_copied, h->stream));
+  // the next ring slot; it waits only if its upload of Q_RING binds ago
+  // has not run yet (the host is Q_RING steps ahead)
+  const unsigned slot = h->q_next % Q_RING;
+  uint16_t* stage = h->q_host + (size_t)slot * 16 * D;
+  HIPCHK(h, hipEventSynchronize(h->q_copied[slot]));
+  memcpy(stage, q, 16 * D * 2);
+  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, stage, 16 * D * 2, hipMemcpyHostToDevice, h->stream));
+  HIPCHK(h, hipEventRecord(h->q_copied[slot], h->stream));
+  ++h->q_next;
   h->bound = true;
   return SKV_OK;
 }

@@ -11,13 +11,21 @@ It writes ``tests/golden/index_cells.npz``: per case the generator parameters,
 the full small arrays of the encoded cell and SHA-256 digests of the large
 ones.  Tests regenerate the same keys and compare ``seoulkv_amd``'s builder
 against these vectors; they never import the reference.
+
+It also writes ``tests/golden/ref_index_v4.npz.xz``: the bytes of a whole
+four-cell index archive written by the reference's own ``SeoulKV4Index.dump``
+(``index.py:74-76`` -> ``_codecs/index.py:220-230``), xz-compressed for the
+repository, so that loading an archive the reference wrote is tested, not
+only this package's own writer.  ``--archive-only`` rewrites just that file.
 """
 
 from __future__ import annotations
 
 import hashlib
 import json
+import lzma
 import sys
+import tempfile
 from pathlib import Path
 
 import numpy as np
@@ -55,12 +63,41 @@ def ivf_keys(n: int, seed: int) -> torch.Tensor:
     return x / x.norm(dim=-1, keepdim=True)
 
 
-def main(reference_src: str) -> None:
+# the archive case: (context, components, sink, local, p, seed); four heads
+ARCHIVE = (1024, 32, 64, 128, 32, 0)
+
+
+def write_archive(build_stage1_cell, ref_index_cls) -> None:
+    """Four cells built by the reference builder exactly as its
+    ``SeoulKV4Index.build`` does (``index.py:146-157``; its 6400-token
+    minimum context is a build-time profile check, not an archive property),
+    dumped by the reference's own writer."""
+    context, comps, sink, local, p, seed = ARCHIVE
+    k, _, _ = make_cache(context, comps, clustered=True, sink=sink, local=local)
+    cells = [
+        build_stage1_cell(k[head], p=p, lam=0.0625, seed=seed, r0=sink, r1=context - local)
+        for head in range(4)
+    ]
+    with tempfile.TemporaryDirectory() as tmp:
+        raw = Path(tmp) / "ref_index_v4.npz"
+        ref_index_cls(cells, {"nprobe_source": "explicit (build)"}).dump(raw)
+        data = raw.read_bytes()
+    path = HERE / "ref_index_v4.npz.xz"
+    path.write_bytes(lzma.compress(data, preset=9))
+    print("wrote", path, len(data), "archive bytes,", path.stat().st_size, "compressed")
+
+
+def main(reference_src: str, archive_only: bool = False) -> None:
     # the reference checkout is read-only input: no bytecode caches there
     sys.dont_write_bytecode = True
     sys.path.insert(0, reference_src)
     from seoulkv4._clustering import _refined_hierarchical_ivf  # reference IVF
     from seoulkv4._index_build import build_stage1_cell  # the reference builder
+    from seoulkv4.index import SeoulKV4Index as RefIndex  # the reference writer
+
+    write_archive(build_stage1_cell, RefIndex)
+    if archive_only:
+        return
 
     arrays, meta = {}, []
     for name, context, comps, clustered, sink, local, p, seed, head in CASES:
@@ -102,4 +139,5 @@ def main(reference_src: str) -> None:
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    main(args[0] if args else "/root/reference/src", archive_only="--archive-only" in sys.argv)
