@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from seoulkv_amd import SeoulKV4, SeoulKV4Config, SeoulKV4Index  # noqa: E402
+from seoulkv_amd.index import build_cell, list_agreement, posting_cosine  # noqa: E402
 from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -209,6 +210,53 @@ def measured_traffic(kernel: str):
     return None
 
 
+def index_build(args) -> int:
+    """Index build time on the host CPU and on the GPU for one config, and how
+    far the GPU-built cells agree with the CPU-built ones (the build starts
+    both from the same seeds; a difference is a floating-point rounding
+    change of an assignment).  Cells are built one at a time exactly as
+    ``SeoulKV4Index.build`` builds them (one log line per cell).  One JSON
+    line."""
+    p, k, v, _ = make_profile(args.config, n_queries=1)
+    r0, r1 = p.sink, p.context - p.local
+    log(f"{args.config}: T={p.context}, nc={p.n_centroids}")
+
+    def build(device: str):
+        cells, t0 = [], time.time()
+        for head in range(4):
+            cells.append(build_cell(k[head], p=p.nprobe, lam=0.0625, seed=0, r0=r0, r1=r1,
+                                    nc=p.n_centroids, device=torch.device(device)))
+            if device != "cpu":
+                torch.cuda.synchronize()
+            log(f"{device} build: cell {head} done at {time.time() - t0:.1f} s")
+        return SeoulKV4Index(cells, {"nprobe_source": "explicit (build)"}), time.time() - t0
+
+    SeoulKV4Index.build(k[:, :8192].contiguous(), v[:, :8192].contiguous(), sink=p.sink,
+                        local=p.local, nprobe=64, n_centroids=512, build_device="cuda:0")
+    torch.cuda.synchronize()  # warm the GPU build path (kernels, allocator)
+    gpu, gpu_s = build("cuda:0")
+    cpu, cpu_s = build("cpu")
+    log(f"GPU build {gpu_s:.1f} s, CPU build {cpu_s:.1f} s ({torch.get_num_threads()} threads)")
+    agree, identical, quality = [], [], {"cpu": [], "gpu": []}
+    for h, (c, g) in enumerate(zip(cpu.cells, gpu.cells)):
+        agree.append(round(list_agreement(c, g), 6))
+        quality["cpu"].append(round(posting_cosine(c, k[h]), 5))
+        quality["gpu"].append(round(posting_cosine(g, k[h]), 5))
+        identical.append(bool(torch.equal(c["offsets"], g["offsets"])
+                              and torch.equal(c["values"], g["values"])))
+    print(json.dumps({
+        "metric": "index build seconds (4 KV heads, one cell at a time)",
+        "config": {"workload": args.config, "context": p.context,
+                   "n_centroids": p.n_centroids, "nprobe": p.nprobe},
+        "cpu_s": round(cpu_s, 2), "gpu_s": round(gpu_s, 2),
+        "cpu_threads": torch.get_num_threads(), "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "list_agreement": agree, "csr_identical": identical,
+        "posting_cosine": quality,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,6 +269,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--index-build", action="store_true",
+                    help="only time SeoulKV4Index.build on the CPU and the GPU for --config "
+                         "and compare the two indexes")
     args = ap.parse_args()
     _CONFIG["name"] = args.config
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -238,6 +289,8 @@ def main() -> int:
         return 1
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.index_build:
+        return index_build(args)
 
     t0 = time.time()
     p, k, v, qs = make_profile(args.config, n_queries=1)

@@ -10,7 +10,15 @@ The clustering depends on torch's RNG stream and on the exact sequence of
 floating-point operations, so the sequence of torch calls below is kept the
 same as the reference's: the same generators and seeds, the same score-chunk
 sizes and the same reductions.  Any change here changes which centroid a key
-lands in.
+lands in.  Each block cites the reference lines it restates.
+
+One deliberate difference: the leaf seeds of the batched local solves are
+drawn from a CPU generator on every build device and then moved (the
+reference draws them from a generator on the build device,
+``_clustering.py:125,177``).  The CPU build, the one the golden vectors pin,
+is unchanged; a GPU build then starts from the same seeds as the CPU build,
+so the two indexes differ only where floating-point rounding on the GPU
+changes an assignment.
 """
 
 from __future__ import annotations
@@ -22,17 +30,20 @@ SCORE_BUDGET = 16 * 2**20  # FP32 score elements per slab (64 MiB)
 
 
 def score_rows(n_centroids: int) -> int:
+    # reference _clustering.py:9-10 (_score_rows)
     return max(1, min(8192, SCORE_BUDGET // n_centroids))
 
 
 def withdraw(capacity: torch.Tensor, total: int) -> torch.Tensor:
-    """Take ``total`` units from donors in order, each at most its capacity."""
+    """Take ``total`` units from donors in order, each at most its capacity
+    (reference ``_clustering.py:13-15``, ``_withdraw``)."""
     remaining = (total - capacity.cumsum(0)).clamp_min(0)
     return torch.cat((remaining.new_tensor([total]), remaining[:-1])) - remaining
 
 
 def spherical_kmeans(x: torch.Tensor, k: int, iters: int, seed: int) -> torch.Tensor:
-    """Lloyd iterations on the unit sphere (cosine assignment)."""
+    """Lloyd iterations on the unit sphere (cosine assignment; reference
+    ``_clustering.py:18-32``, ``_kmeans``)."""
     n = x.shape[0]
     gen = torch.Generator().manual_seed(seed)
     cent = x[torch.randperm(n, generator=gen)[:k].to(x.device)].clone()
@@ -49,7 +60,8 @@ def spherical_kmeans(x: torch.Tensor, k: int, iters: int, seed: int) -> torch.Te
 
 
 def midrise(x: torch.Tensor, bits: int) -> torch.Tensor:
-    """Max-abs mid-rise quantiser with 2**bits levels per row."""
+    """Max-abs mid-rise quantiser with 2**bits levels per row (reference
+    ``_clustering.py:35-41``, ``_midrise``)."""
     a = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-9)
     levels = 2**bits
     step = 2 * a / levels
@@ -58,7 +70,8 @@ def midrise(x: torch.Tensor, bits: int) -> torch.Tensor:
 
 def allocate_leaves(counts: torch.Tensor, n_leaves: int) -> torch.Tensor:
     """Exactly ``n_leaves`` leaves over the coarse buckets, proportional to
-    occupancy, at least one per non-empty bucket (largest remainders first)."""
+    occupancy, at least one per non-empty bucket (largest remainders first;
+    reference ``_clustering.py:44-70``, ``_allocate_leaves``)."""
     raw = counts.float() * (n_leaves / max(float(counts.sum()), 1.0))
     alloc = torch.floor(raw).long()
     alloc = torch.where(counts > 0, alloc.clamp_min(1), torch.zeros_like(alloc))
@@ -86,7 +99,8 @@ def allocate_leaves(counts: torch.Tensor, n_leaves: int) -> torch.Tensor:
 
 
 def _solve_bucket_alone(x, size, nleaf, iters, seed):
-    """A bucket too large to pad into a batch gets its own k-means."""
+    """A bucket too large to pad into a batch gets its own k-means
+    (reference ``_clustering.py:149-153``)."""
     if size < nleaf:
         return x[torch.arange(nleaf, device=x.device) % size]
     return spherical_kmeans(x, nleaf, iters, seed)
@@ -106,15 +120,18 @@ def hierarchical_ivf(
 
     ``keys`` are unit-norm fp32 rows.  ``labels[i]`` holds key i's ``spill``
     best leaves; the CSR lists every key under each of them, ordered by key.
+    Reference ``_clustering.py:73-236`` (``_refined_hierarchical_ivf``).
     """
     n, d = keys.shape
     dev = keys.device
+    # coarse k-means and assignment (reference :93-99)
     k0 = min(max(2, coarse_clusters), n_leaves, n)
     c0 = spherical_kmeans(keys, k0, coarse_iters, seed)
     coarse = torch.empty(n, dtype=torch.long, device=dev)
     for start in range(0, n, 8192):
         coarse[start : start + 8192] = (keys[start : start + 8192] @ c0.t()).argmax(1)
 
+    # leaves per coarse bucket, topped up to `spill` per active bucket (:105-118)
     counts0 = torch.bincount(coarse, minlength=k0)
     leaves = allocate_leaves(counts0, n_leaves)
     active = counts0 > 0
@@ -129,16 +146,18 @@ def hierarchical_ivf(
         donors = spare.argsort(descending=True, stable=True)
         leaves += need
         leaves[donors] -= withdraw(spare[donors], deficit)
+    # bucket order and starts (:119-126); the seed generator is a CPU one on
+    # every device (see the module note)
     leaf_start = leaves.cumsum(0) - leaves
     order = torch.argsort(coarse, stable=True)
     coarse_start = counts0.cumsum(0) - counts0
     cent = torch.empty(n_leaves, d, dtype=keys.dtype, device=dev)
     labels = torch.empty(n, spill, dtype=torch.long, device=dev)
     batch_coarse = max(1, int(batch_coarse))
-    gen = torch.Generator(device=dev).manual_seed(seed + 0x48494552)
+    gen = torch.Generator().manual_seed(seed + 0x48494552)
     alone = 0
 
-    for b0 in range(0, k0, batch_coarse):
+    for b0 in range(0, k0, batch_coarse):  # batches of coarse buckets (:128-217)
         b1 = min(b0 + batch_coarse, k0)
         cb = counts0[b0:b1]
         lb = leaves[b0:b1]
@@ -148,6 +167,7 @@ def hierarchical_ivf(
         last = int(coarse_start[b1 - 1] + counts0[b1 - 1])
         max_n, max_l = int(cb.max()), int(lb.max())
         if len(cb) * max_n * max_l > SCORE_BUDGET or max_l > max_n:
+            # buckets solved one by one (:138-160)
             cursor = first
             for j, (size, nleaf, offset) in enumerate(
                 zip(cb.tolist(), lb.tolist(), leaf_start[b0:b1].tolist())
@@ -169,6 +189,7 @@ def hierarchical_ivf(
                 alone += 1
             continue
 
+        # the batch padded into one slab (:161-173)
         ids = order[first:last]
         local_bucket = coarse[ids] - b0
         local_start = cb.cumsum(0) - cb
@@ -183,9 +204,10 @@ def hierarchical_ivf(
         xb = torch.zeros(b1 - b0, max_n, d, dtype=keys.dtype, device=dev)
         xb[local_bucket, rank] = keys[ids]
         # Seed leaves with random real keys (padding rows sort last); a
-        # singleton bucket reuses its key for every extra leaf.
+        # singleton bucket reuses its key for every extra leaf (:174-185).
         seed_rows = (
-            torch.rand(b1 - b0, max_n, generator=gen, device=dev)
+            torch.rand(b1 - b0, max_n, generator=gen)
+            .to(dev)
             .masked_fill(~row_ok, torch.inf)
             .topk(max_l, dim=1, largest=False)
             .indices
@@ -193,7 +215,7 @@ def hierarchical_ivf(
         seed_rows = torch.where(col_ok & (cols_i >= cb[:, None]), seed_rows[:, :1], seed_rows)
         cf = xb.gather(1, seed_rows[..., None].expand(-1, -1, d)).clone()
 
-        for _ in range(local_iters):
+        for _ in range(local_iters):  # batched Lloyd steps (:187-199)
             score = torch.bmm(xb, cf.transpose(1, 2)).masked_fill(
                 ~col_ok[:, None, :], -torch.inf
             )
@@ -205,6 +227,7 @@ def hierarchical_ivf(
             cf = torch.where(cnt[..., None] > 0, sums / cnt[..., None].clamp_min(1), cf)
             cf = cf / cf.norm(dim=2, keepdim=True).clamp_min(EPS)
 
+        # final labels against the updated codebook, leaves written back (:201-217)
         score = torch.bmm(xb, cf.transpose(1, 2)).masked_fill(
             ~col_ok[:, None, :], -torch.inf
         )
@@ -218,6 +241,7 @@ def hierarchical_ivf(
         )
         cent[leaf_start[b0:b1][owner] + local_leaf] = cf[owner, local_leaf]
 
+    # CSR posting lists and build statistics (:219-236)
     flat = labels.reshape(-1)
     key_of = torch.arange(n, device=dev).unsqueeze(1).expand_as(labels).reshape(-1)
     list_order = torch.argsort(flat)

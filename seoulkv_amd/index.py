@@ -21,6 +21,7 @@ from collections.abc import Sequence
 from numbers import Real
 from pathlib import Path
 
+import numpy as np
 import torch
 
 from seoulkv_amd._clustering import hierarchical_ivf, midrise
@@ -98,6 +99,56 @@ def build_cell(k, *, p, lam, seed, r0, r1, nc, device=None, coarse_clusters=128,
     )
     validate_static_cell(cell)
     return cell
+
+
+def posting_pairs(cell) -> np.ndarray:
+    """[tokens][2]: the two posting lists (ascending) of each listed token of
+    a spill-2 cell, rows in token order, from its CSR (``offsets``,
+    ``values``).  Two builds of the same keys agree on a token when its row
+    matches."""
+    off = cell["offsets"].numpy().astype(np.int64)
+    vals = cell["values"].numpy().astype(np.int64)
+    lists = np.repeat(np.arange(len(off) - 1), np.diff(off))
+    order = np.lexsort((lists, vals))
+    return lists[order].reshape(-1, 2)
+
+
+
+def list_agreement(a, b) -> float:
+    """How far two builds of the same keys put tokens in the same posting
+    lists, whatever the lists' numbering: each list of ``b`` is matched to the
+    list of ``a`` holding most of its tokens, and the result is the fraction
+    of ``b``'s (token, list) memberships whose token is in the matched list
+    (1.0: the same partition).  A leaf allocation that differs by one leaf
+    renumbers every later list, which a per-ID comparison would count as a
+    total mismatch."""
+    pa, pb = posting_pairs(a), posting_pairs(b)
+    if pa.shape != pb.shape:
+        raise ValueError("the cells list different token sets")
+    na = int(pa.max()) + 1
+    # every token joins its 2 lists in b with its 2 lists in a: 4 (b, a) pairs
+    pairs = (pb[:, :, None].astype(np.int64) * na + pa[:, None, :]).reshape(-1)
+    keys, counts = np.unique(pairs, return_counts=True)
+    best = np.zeros(int(pb.max()) + 1, dtype=np.int64)
+    np.maximum.at(best, keys // na, counts)
+    return float(best.sum()) / pb.size
+
+
+
+def posting_cosine(cell, k) -> float:
+    """Clustering quality of a cell over its KV head's keys ``k`` [T][256]:
+    the mean, over the retrieval tokens, of the cosine between a token's
+    normalised key and the nearer of its two lists' centroids (the stored
+    BF16 centroids).  Two builds of the same keys that differ only in which
+    near-tied assignments they took score the same to ~1e-3."""
+    r0, r1 = int(cell["r0"]), int(cell["r1"])
+    x = k[r0:r1].float()
+    x = x / x.norm(dim=-1, keepdim=True).clamp_min(1e-9)
+    c = cell["centroids"].float()
+    c = c / c.norm(dim=-1, keepdim=True).clamp_min(1e-9)
+    pairs = torch.from_numpy(posting_pairs(cell))
+    cos = torch.stack([(x * c[pairs[:, j]]).sum(-1) for j in range(2)]).amax(0)
+    return float(cos.mean())
 
 
 class SeoulKV4Index:
