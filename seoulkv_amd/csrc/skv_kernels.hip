@@ -781,7 +781,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
   extern __shared__ uint32_t s_bm[];
   __shared__ int s_off[PL_RANGE_MAX + 1], s_cum[PL_RANGE_MAX + 1], s_cl[PL_RANGE_MAX];
-  __shared__ int s_scan[PL_WAVES + 1], s_surv, s_scanned;
+  __shared__ int s_scan[PL_WAVES + 1], s_surv;
   __shared__ unsigned long long s_excl;
   __shared__ uint32_t s_tm[H * PL_TM_TILES];  // tile maxima of the first two pages' keys
   // range b = block b: workgroups are dispatched in index order within each
@@ -823,7 +823,6 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   if (t + PL_BLOCK <= ncr) s_off[t + PL_BLOCK] = off1;
   if (t == 0) {
     s_surv = 0;
-    s_scanned = 0;
   }
   if (t < H * PL_TM_TILES) s_tm[t] = 0;
   // survivor head masks (upper_h >= thr_h) of the range's centroids
@@ -854,6 +853,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   if (t == 0) s_cum[nsel] = (int)(tot >> PL_SEL_BITS);
   __syncthreads();
   const int S = s_cum[nsel];  // postings of the selected clusters
+  if (t == 0) a.pool_scan[g * a.pool_blocks + b] = S;  // summed by the U1 scorer (diagnostic)
   const int* __restrict__ mate = a.post_mate + (size_t)g * a.np_max;
   const int* __restrict__ ptok = a.post_tok + (size_t)g * a.np_max;
   // posting i of the range's selected lists -> posting index j (its cluster
@@ -982,22 +982,6 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
       SKV_TSV(10, 1, b);
       SKV_TSV(10, 2, S);
     }
-  } else if (b == nb - 1) {  // the last range: postings of all selected lists
-    // 16 centroids per thread and pass, their 17 CSR offsets loaded together
-    int sc = 0;
-    const int* off = a.csr_off + (size_t)g * (nc + 1);
-    for (int ch = (int)threadIdx.x - WAVE; ch < nc / 16; ch += PL_BLOCK - WAVE) {
-      const uint32_t m16 = (s_bm[ch >> 1] >> (16 * (ch & 1))) & 0xffffu;
-      if (!m16) continue;
-      int o[17];
-#pragma unroll
-      for (int q = 0; q < 17; ++q) o[q] = off[16 * ch + q];
-#pragma unroll
-      for (int q = 0; q < 16; ++q)
-        if ((m16 >> q) & 1u) sc += o[q + 1] - o[q];
-    }
-    sc = wave_sum(sc);
-    if (lane == 0) atomicAdd(&s_scanned, sc);
   }
   // 2-bit scores of the first two pages (waves 1.. while wave 0 looks back)
   uint32_t sc0[4] = {0, 0, 0, 0}, sc1[4] = {0, 0, 0, 0};
@@ -1043,7 +1027,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   // ---- the last range writes the group's totals
   if (b == nb - 1 && threadIdx.x == 0) {
     {
-      const int sv = surv0 + s_surv, sc = s_scanned;
+      const int sv = surv0 + s_surv;
       const int to = pos0 + owned_total, ts = sel0 + nsel;
       int err = a.status[g * ST_WORDS + ST_ERR];
       if (err == 0) {
@@ -1054,7 +1038,6 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
       a.status[g * ST_WORDS + ST_ERR] = err;
       a.status[g * ST_WORDS + ST_SEL] = ts;
       a.status[g * ST_WORDS + ST_SURV] = sv;
-      a.status[g * ST_WORDS + ST_SCANNED] = sc;
     }
   }
   SKV_TSE(0);
@@ -1222,6 +1205,13 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
   int* __restrict__ tok_out = (U1 ? a.u1_tok : a.u2_tok) + (size_t)g * cap_out;
   uint16_t* __restrict__ s_out = U1 ? a.s4 : a.s8;
   const int slot_out = U1 ? ST_U1 : ST_U2;
+  if (U1 && blockIdx.x == 0 && wave == 0) {  // diagnostic: postings the pool ranges walked
+    const int nb = (a.nc + a.pool_range - 1) / a.pool_range;
+    int sc = 0;
+    for (int i = lane; i < nb; i += WAVE) sc += a.pool_scan[g * a.pool_blocks + i];
+    sc = wave_sum(sc);
+    if (lane == 0) a.status[g * ST_WORDS + ST_SCANNED] = sc;
+  }
   if (n_in == 0) {
     if (blockIdx.x == 0 && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = 0;
     SKV_TSE((U1 ? 3 : 8));

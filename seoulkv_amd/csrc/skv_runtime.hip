@@ -470,6 +470,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.tmax_fi = nc > 8 * SEL_BLOCK ? (uint16_t*)ar.take((size_t)G * H * (nc / 16) * 2) : nullptr;
     a.sel = (int*)ar.take((size_t)G * nc * 4);
     a.pool_flags = (unsigned long long*)ar.take((size_t)G * a.pool_blocks * 8);
+    a.pool_scan = (int*)ar.take((size_t)G * a.pool_blocks * 4);
     a.pool_epoch = (unsigned*)ar.take((size_t)G * 4);
     a.pool_tok = (int*)ar.take((size_t)G * a.cap * 4);
     a.s2 = (uint16_t*)ar.take((size_t)G * H * a.cap * 2);

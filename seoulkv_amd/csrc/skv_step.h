@@ -36,7 +36,7 @@ enum {
   ST_SURV = 3,     // coarse survivors
   ST_U1 = 4,       // |U1|
   ST_U2 = 5,       // |U2|
-  ST_SCANNED = 6,  // postings scanned by the pool builder
+  ST_SCANNED = 6,  // postings of the selected lists (summed by the U1 scorer)
   ST_FULLSEL = 7,  // selections that ran the full pass (bit per stage, FS_*)
   ST_WORDS = 8
 };
@@ -91,6 +91,7 @@ struct StepArgs {
                             // (both written when nc > 8 x SEL_BLOCK, else NULL)
   int* sel;                 // [G][nc] selected clusters, ascending
   unsigned long long* pool_flags;  // [G][pool_blocks] look-back records (epoch-tagged)
+  int* pool_scan;           // [G][pool_blocks] postings of each pool range's selected lists
   unsigned* pool_epoch;     // [G] launches of the pool kernel (tags the look-back records)
   int* pool_tok;            // [G][cap]
   uint16_t* s2;             // [G][H][cap] ordered
