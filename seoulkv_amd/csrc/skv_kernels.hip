@@ -1060,6 +1060,12 @@ __device__ __forceinline__ void write_member_words(uint32_t mine, int n, uint64_
 }
 
 
+// Dynamic LDS of k_topk: the sampled-cut scratch and the member bitmap
+// (TOPK_LDS_WORDS words), or the LDS-resident scores of the full selection.
+size_t topk_dynamic_lds(int lds_items) {
+  return std::max(sizeof(FastScratch) + (size_t)TOPK_LDS_WORDS * 8, (size_t)lds_items * 2);
+}
+
 // Per (group, head): members = top-k by (ordered score, lowest token) of the
 // n items; writes the membership bitmap.  LDS-resident when n <= lds_items,
 // otherwise 8-bit radix passes over the full 40-bit keys in memory.
@@ -1549,6 +1555,37 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
     default:
       break;
   }
+}
+
+hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* static_bytes,
+                           size_t* dynamic_bytes) {
+  const void* fn = nullptr;
+  size_t dyn = 0;
+  switch (k) {
+    case 0: fn = reinterpret_cast<const void*>(&k_front<true>); break;
+    case 1: fn = reinterpret_cast<const void*>(&k_select); dyn = w.select_lds; break;
+    case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)(a.nc / 32) * 4; break;
+    case 3: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u1_lds; break;
+    case 4: fn = reinterpret_cast<const void*>(&k_union_score<4>); break;
+    case 5: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u2_lds; break;
+    case 6: fn = reinterpret_cast<const void*>(&k_union_score<8>); break;
+    case 7: fn = reinterpret_cast<const void*>(&k_top100); dyn = sizeof(FastScratch); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipFuncAttributes attr;
+  const hipError_t e = hipFuncGetAttributes(&attr, fn);
+  if (e != hipSuccess) return e;
+  size_t st = attr.sharedSizeBytes;
+  if (k == 0) {  // both front variants
+    hipFuncAttributes attr2;
+    const hipError_t e2 =
+        hipFuncGetAttributes(&attr2, reinterpret_cast<const void*>(&k_front<false>));
+    if (e2 != hipSuccess) return e2;
+    st = std::max(st, (size_t)attr2.sharedSizeBytes);
+  }
+  *static_bytes = st;
+  *dynamic_bytes = dyn;
+  return hipSuccess;
 }
 
 void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev) {

@@ -609,9 +609,22 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   // the sink/local blocks, whichever is largest (they are never live together).
   const size_t fs_bytes = sizeof(FastScratch);
   w.select_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES});
-  const size_t topk_bytes = fs_bytes + (size_t)TOPK_LDS_WORDS * 8;  // + member bitmap
-  w.top_u1_lds = std::max(topk_bytes, (size_t)w.top_u1.lds_items * 2);
-  w.top_u2_lds = std::max(topk_bytes, (size_t)w.top_u2.lds_items * 2);
+  w.top_u1_lds = topk_dynamic_lds(w.top_u1.lds_items);
+  w.top_u2_lds = topk_dynamic_lds(w.top_u2.lds_items);
+  // every launch must fit the block's LDS (static + dynamic): checked here,
+  // on the host, rather than left to a failed dispatch
+  for (int k = 0; k < N_STEP_KERNELS; ++k) {
+    size_t st = 0, dy = 0;
+    if (step_kernel_lds(a, w, k, &st, &dy) != hipSuccess) {
+      fail(h, SKV_EHIP, "cannot query kernel %s", kKernelNames[k]);
+      return bail(SKV_EHIP);
+    }
+    if (st + dy > h->lds_per_block) {
+      fail(h, SKV_EINVAL, "kernel %s needs %zu bytes of LDS per block, the device has %zu",
+           kKernelNames[k], st + dy, h->lds_per_block);
+      return bail(SKV_EINVAL);
+    }
+  }
 
   bool ring_ok = hipHostMalloc((void**)&h->q_host, (size_t)Q_RING * 16 * D * 2,
                                hipHostMallocDefault) == hipSuccess;

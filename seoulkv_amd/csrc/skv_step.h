@@ -148,8 +148,15 @@ constexpr int TOPK_LDS_WORDS = 2048;
 constexpr int N_STEP_KERNELS = 8;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
+// Dynamic LDS bytes of a top-k launch whose full selection holds lds_items
+// scores in LDS.
+size_t topk_dynamic_lds(int lds_items);
+
 // Kernel k (0 .. N_STEP_KERNELS - 1, in step order) of one decode step.
 void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k);
+// Static and dynamic LDS bytes per block of step kernel k as launched.
+hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* static_bytes,
+                           size_t* dynamic_bytes);
 void launch_step(const StepArgs& a, const StepWork& w, hipStream_t st, hipEvent_t* ev);
 
 }  // namespace skv
