@@ -416,9 +416,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   a.words_u2 = words2;
   a.pool_blocks = nc / 32;
   // at most 64 ranges per group (one pool block per CU over the 4 groups;
-  // one look-back poll reaches every predecessor), at least 128 centroids
-  // per range
-  a.pool_range = std::max(128, (nc / 64 + 31) / 32 * 32);
+  // one look-back poll reaches every predecessor), at least 32 centroids
+  // (one bitmap word) per range: small indexes still spread the pool's row
+  // fetch over ~64 CUs per group
+  a.pool_range = std::max(32, (nc / 64 + 31) / 32 * 32);
   a.dense_slices = (a.sink + a.local + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
   const int max_slices = (a.sink + a.local + cap_app + DENSE_SLICE_KEYS - 1) / DENSE_SLICE_KEYS;
   h->dn.T = T;
