@@ -81,8 +81,9 @@ int skv_create(const skv_index_desc *index, const uint16_t *k_bf16,
 
 /* Reference bind_query (_runtime.py:180-186): copies host Q [16][256] BF16
  * (query head j belongs to KV head j/4) to the device, asynchronously,
- * through a ring of 8 pinned staging slots: q_bf16 may be reused on return,
- * and the call blocks only when the host is 8 binds ahead of the device. */
+ * through a ring of 16 pinned staging slots: q_bf16 may be reused on return,
+ * and the call blocks only when the host is 9 or more binds ahead of the
+ * device. */
 int skv_bind_query(void *handle, const uint16_t *q_bf16);
 
 /* Device-resident variant: q_dev is a device pointer to [16][256] BF16,

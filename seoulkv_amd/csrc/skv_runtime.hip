@@ -47,16 +47,20 @@ struct Arena {
 };
 
 constexpr int APPEND_CHUNK = 1024;  // tokens per host-append staging round
-constexpr int Q_RING = 8;           // query staging slots (host run-ahead, in steps)
+constexpr int Q_RING = 16;          // query staging slots (host run-ahead, in steps)
+constexpr int Q_MARK = 8;           // uploads per completion event of the staging ring
 
 struct Handle {
   int device = 0;
   hipStream_t stream = nullptr;
   bool own_stream = false;
   // pinned staging ring of skv_bind_query: slot i is reused once its
-  // previous upload (event q_copied[i]) has left it, so the host can run up
-  // to Q_RING steps ahead of the device
-  hipEvent_t q_copied[Q_RING] = {};
+  // previous upload has left it, so the host runs up to Q_RING steps ahead
+  // of the device.  An event recorded on the stream costs the device about
+  // as much as the 8 KiB upload itself, so only the upload of every
+  // Q_MARK-th slot (slot % Q_MARK == Q_MARK - 1) records one: event
+  // q_marked[i / Q_MARK] covers slot i's upload and the uploads before it.
+  hipEvent_t q_marked[Q_RING / Q_MARK] = {};
   uint16_t* q_host = nullptr;  // [Q_RING][16][D]
   unsigned q_next = 0;
   // device-query binding on a producer stream: the handle's steps so far
@@ -290,7 +294,7 @@ void skv_destroy(void* handle) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return;
   if (h->stream) (void)hipStreamSynchronize(h->stream);
-  for (hipEvent_t e : h->q_copied)
+  for (hipEvent_t e : h->q_marked)
     if (e) (void)hipEventDestroy(e);
   if (h->steps_done) (void)hipEventDestroy(h->steps_done);
   if (h->q_ready) (void)hipEventDestroy(h->q_ready);
@@ -629,8 +633,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
 
   bool ring_ok = hipHostMalloc((void**)&h->q_host, (size_t)Q_RING * 16 * D * 2,
                                hipHostMallocDefault) == hipSuccess;
-  for (int i = 0; i < Q_RING && ring_ok; ++i)
-    ring_ok = hipEventCreateWithFlags(&h->q_copied[i], hipEventDisableTiming) == hipSuccess;
+  for (int i = 0; i < Q_RING / Q_MARK && ring_ok; ++i)
+    ring_ok = hipEventCreateWithFlags(&h->q_marked[i], hipEventDisableTiming) == hipSuccess;
   if (!ring_ok ||
       hipEventCreateWithFlags(&h->steps_done, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&h->q_ready, hipEventDisableTiming) != hipSuccess) {
@@ -647,14 +651,17 @@ int skv_bind_query(void* handle, const uint16_t* q) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
   if (!q) return fail(h, SKV_EINVAL, "NULL query");
-  // the next ring slot; it waits only if its upload of Q_RING binds ago
-  // has not run yet (the host is Q_RING steps ahead)
+  // The next ring slot.  Its previous upload (Q_RING binds ago) is covered
+  // by the event of its mark group, last recorded between Q_RING and
+  // Q_RING - Q_MARK + 1 binds ago (an event never recorded counts as done):
+  // the host waits only when it is Q_RING - Q_MARK + 1 or more steps ahead.
+  HIPCHK(h, hipSetDevice(h->device));
   const unsigned slot = h->q_next % Q_RING;
   uint16_t* stage = h->q_host + (size_t)slot * 16 * D;
-  HIPCHK(h, hipEventSynchronize(h->q_copied[slot]));
+  HIPCHK(h, hipEventSynchronize(h->q_marked[slot / Q_MARK]));
   memcpy(stage, q, 16 * D * 2);
   HIPCHK(h, hipMemcpyAsync((void*)h->a.q, stage, 16 * D * 2, hipMemcpyHostToDevice, h->stream));
-  HIPCHK(h, hipEventRecord(h->q_copied[slot], h->stream));
+  if (slot % Q_MARK == Q_MARK - 1) HIPCHK(h, hipEventRecord(h->q_marked[slot / Q_MARK], h->stream));
   ++h->q_next;
   h->bound = true;
   return SKV_OK;

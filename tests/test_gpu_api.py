@@ -15,6 +15,7 @@ import torch
 
 from oracle import decode as od
 from seoulkv_amd import SeoulKV4, SeoulKV4Config, SeoulKV4Index, _hip
+from seoulkv_amd.result import _DeviceArray
 from tests.helpers import bits, case, cosine, oracle_step
 
 pytestmark = pytest.mark.gpu
@@ -160,6 +161,44 @@ def test_device_query_produced_on_another_stream():
         rt.synchronize()
         assert torch.equal(rt.read_output(), outs[1])
         assert torch.equal(rt.debug_ids(), ids[1])
+    finally:
+        torch.cuda.synchronize()
+        rt.close()
+
+
+def test_host_runs_ahead_through_the_query_ring():
+    """Host binds while the device is held back: the host fills the pinned
+    staging ring, waits on its completion events and reuses slots; every
+    step, read from a copy ordered right after it on the stream, must equal
+    the synchronous step on its own query (5 queries in turn, so a reused
+    slot holding the wrong query would show)."""
+    index, k, v, qs = case(**P0, n_queries=5)
+    st = torch.cuda.Stream()
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=False,
+                      stream=st.cuda_stream)
+    try:
+        want = []
+        for q in qs:
+            rt.bind_query(q)
+            rt.enqueue()
+            rt.synchronize()
+            want.append(rt.read_output().view(torch.int16).reshape(16, 256))
+        out = torch.as_tensor(_DeviceArray(rt.output_device_ptr(), (16, 256), "<i2"),
+                              device="cuda:0")
+        n = 40
+        got = torch.zeros((n, 16, 256), dtype=torch.int16, device="cuda:0")
+        torch.cuda.synchronize()  # the fill (default stream) before the copies on st
+        print(f"[gpu] {n} host binds ahead of a held-back stream", flush=True)
+        with torch.cuda.stream(st):
+            torch.cuda._sleep(50_000_000)  # the device starts late
+            for i in range(n):
+                rt.bind_query(qs[i % 5])
+                rt.enqueue()
+                got[i].copy_(out)
+        st.synchronize()
+        got = got.cpu()
+        for i in range(n):
+            assert torch.equal(got[i], want[i % 5]), f"step {i}"
     finally:
         torch.cuda.synchronize()
         rt.close()
