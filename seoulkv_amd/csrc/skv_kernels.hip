@@ -40,64 +40,32 @@ __device__ unsigned long long g_skv_trace_blk[12][4096][4];
 #endif
 
 // ============================================================ query prep
-// Fixed-point operand of query variant v for KV group g, computed by one
-// 256-thread block: wave h owns head h, lane l dims 4l .. 4l+3.  Writes the
-// integers X, their sum, the scale exponent, ||q|| lambda (raw variant) and
-// the int8 limb B image to *out (LDS or global memory).
-// Sum of squares: X^2 < 2^44 is split into 22-bit halves so that both wave
-// sums stay below 2^30 (exact in int32).
-struct QPrepScratch {
-  int X[H][D];
-};
-
-__device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out, int h,
-                          int lane, uint2 qw);
+// Fixed-point operand of query variant v for KV group g, computed by the
+// first 4 waves of a block (wave h forms head h; lane l owns dims 4l ..
+// 4l+3): the integers X, their sum, the scale exponent, ||q|| lambda (raw
+// variant) and the int8 limb B image, written to *out (LDS or global
+// memory).  Sum of squares: X^2 < 2^44 is split into 22-bit halves so that
+// both wave sums stay below 2^30 (exact in int32).
+__device__ void prep_head(const StepArgs& a, int g, int v, QOperand* out, int h, int lane,
+                          uint2 qw);
 
 // This lane's 4 BF16 query elements of head h of group g (dims 4 lane ..).
 __device__ __forceinline__ uint2 load_qw(const StepArgs& a, int g, int h, int lane) {
   return *reinterpret_cast<const uint2*>(a.q + (g * H + h) * D + 4 * lane);
 }
 
-// Fixed-point operand of query variant v for KV group g (waves 0..3 form
-// one head each from qw, their lanes' query words, then the whole block
-// writes the B image).
-__device__ void prep_operand(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out,
-                             uint2 qw) {
+// Waves 0..3 form one head each from qw, their lanes' query words; the
+// operand is complete after the barrier.
+__device__ void prep_operand(const StepArgs& a, int g, int v, QOperand* out, uint2 qw) {
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
-  if (h < H) prep_head(a, g, v, s, out, h, lane, qw);
-  __syncthreads();
-  // B image: word (kc, lane l, m) = bytes limb (col%4) of X_{col/4}[dim],
-  // col = l%16, dim = (l/16)*64 + kc*16 + 4 byte + m (the 4 x 4 bytes of a
-  // lane's 16-dim chunk transposed, to match the A words of expand2t and
-  // expand4t: the MFMA pairs A and B bytes by position, so one permutation
-  // of both keeps every dot); limb 3 is zero.
-  for (int w = threadIdx.x; w < 4 * WAVE * 4; w += blockDim.x) {
-    const int kc = w >> 8, l = (w >> 2) & 63, m = w & 3;
-    const int col = l & 15, hh = col >> 2, limb = col & 3;
-    const int* xrow = &s.X[hh][(l >> 4) * 64 + kc * 16];
-    int xs[4];
-#pragma unroll
-    for (int byte = 0; byte < 4; ++byte) xs[byte] = xrow[4 * byte + m];
-    uint32_t word = 0;
-#pragma unroll
-    for (int byte = 0; byte < 4; ++byte) {
-      const int x = xs[byte];
-      const int l0 = (int)(int8_t)(x & 0xff);
-      const int x1 = (x - l0) >> 8;
-      const int l1 = (int)(int8_t)(x1 & 0xff);
-      const int l2 = (x1 - l1) >> 8;
-      const int limbv = limb == 0 ? l0 : limb == 1 ? l1 : limb == 2 ? l2 : 0;
-      word |= (uint32_t)(limbv & 0xff) << (8 * byte);
-    }
-    out->bimg[kc][l][m] = word;
-  }
+  if (h < H) prep_head(a, g, v, out, h, lane, qw);
   __syncthreads();
 }
 
 // One wave per head: the integers X, their sum, the scale exponent and
 // ||q|| lambda (raw variant) of query head 4g + h.
-__device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOperand* out, int h,
-                          int lane, uint2 qw) {
+__device__ void prep_head(const StepArgs& a, int g, int v, QOperand* out, int h, int lane,
+                          uint2 qw) {
   const uint32_t qb[4] = {qw.x & 0xffffu, qw.x >> 16, qw.y & 0xffffu, qw.y >> 16};
   uint32_t bits[4];
   if (v != QV_RAW) {
@@ -131,8 +99,27 @@ __device__ void prep_head(const StepArgs& a, int g, int v, QPrepScratch& s, QOpe
     sq_lo += (int)(x2 & 0x3fffffu);
     sq_hi += (int)(x2 >> 22);
   }
-  *reinterpret_cast<int4*>(&s.X[h][4 * lane]) = make_int4(X[0], X[1], X[2], X[3]);
   *reinterpret_cast<int4*>(&out->X[h][4 * lane]) = make_int4(X[0], X[1], X[2], X[3]);
+  // B image: word (kc, lane l, m) holds bytes limb (col % 4) of X_{col/4}[dim]
+  // for col = l % 16, dim = (l / 16) * 64 + kc * 16 + 4 byte + m (a lane's
+  // 16-dim chunk transposed 4 x 4, to match the A words of expand2t and
+  // expand4t: the MFMA pairs A and B bytes by position, so one permutation
+  // of both keeps every dot).  This lane's dims 4 lane + i are byte
+  // lane % 4 of words (kc = lane / 4 % 4, l = lane / 16 * 16 + 4h + limb,
+  // m = i); X = l0 + 2^8 l1 + 2^16 l2 in signed bytes (|X| < 2^22), limb 3 = 0.
+  uint8_t* img = reinterpret_cast<uint8_t*>(&out->bimg[(lane >> 2) & 3][(lane >> 4) * 16 + 4 * h][0]) +
+                 (lane & 3);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int l0 = (int)(int8_t)(X[i] & 0xff);
+    const int x1 = (X[i] - l0) >> 8;
+    const int l1 = (int)(int8_t)(x1 & 0xff);
+    const int l2 = (x1 - l1) >> 8;
+    img[0 * 16 + 4 * i] = (uint8_t)l0;  // word (kc, l + limb, m = i): 16 bytes per l
+    img[1 * 16 + 4 * i] = (uint8_t)l1;
+    img[2 * 16 + 4 * i] = (uint8_t)l2;
+    img[3 * 16 + 4 * i] = 0;
+  }
   sx = wave_sum(sx);
   sq_lo = wave_sum(sq_lo);
   sq_hi = wave_sum(sq_hi);
@@ -417,7 +404,6 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   SKV_TSB(4, 0);
   SKV_TS(0, 0);
   const int g = blockIdx.y, nc = a.nc;
-  __shared__ __align__(16) QPrepScratch sp;
   const int lane = threadIdx.x & 63;
   const int ntiles = nc / 16;
   const int step = FR_WAVES * (int)gridDim.x;
@@ -428,7 +414,7 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   __builtin_amdgcn_sched_barrier(0);  // keep the query load ahead of the tile's
   FrTile cur = fr_load(a, g, tile, lane);
   __shared__ __align__(16) QOperand sq;
-  prep_operand(a, g, QV_RAW, sp, &sq, qw);
+  prep_operand(a, g, QV_RAW, &sq, qw);
   SKV_TS(0, 1);
   if (tile < ntiles) {
     uint32_t b[4][4];
@@ -515,8 +501,12 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
   if ((int)blockIdx.x >= G * H + n_dense) {  // the q15 / qs operands of the later scorers
     const int i = blockIdx.x - G * H - n_dense, g = i / 2, v = QV_Q15 + i % 2;
     const int hq = min((int)(threadIdx.x >> 6), H - 1);
-    prep_operand(a, g, v, *reinterpret_cast<QPrepScratch*>(dyn), &a.qop[g * QV_COUNT + v],
-                 load_qw(a, g, hq, threadIdx.x & 63));
+    // formed in LDS (the image is written byte by byte), then copied out
+    QOperand& lq = *reinterpret_cast<QOperand*>(dyn);
+    prep_operand(a, g, v, &lq, load_qw(a, g, hq, threadIdx.x & 63));
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&lq);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + v]);
+    for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += blockDim.x) dst[i] = src[i];
     SKV_TSE(5);
     return;
   }

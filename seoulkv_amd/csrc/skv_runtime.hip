@@ -613,7 +613,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   // LDS-resident scores of the full selection, or the attention scratch of
   // the sink/local blocks, whichever is largest (they are never live together).
   const size_t fs_bytes = sizeof(FastScratch);
-  w.select_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES});
+  w.select_lds = std::max({fs_bytes, (size_t)nc * 2, ATTN_SCRATCH_BYTES, sizeof(QOperand)});
   w.top_u1_lds = topk_dynamic_lds(w.top_u1.lds_items);
   w.top_u2_lds = topk_dynamic_lds(w.top_u2.lds_items);
   // every launch must fit the block's LDS (static + dynamic): checked here,
