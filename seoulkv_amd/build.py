@@ -28,6 +28,10 @@ FLAGS = [
     "-ffp-contract=off",
     # packed FP32 VALU forms are kept out of every device code object
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar / pointer kernel arguments arrive in scalar registers at
+    # dispatch (kernel argument preloading), so a kernel's first loads need
+    # not wait for its argument block to be read from memory
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",

@@ -47,7 +47,7 @@ __device__ unsigned long long g_skv_trace_blk[12][4096][4];
 // memory).  Sum of squares: X^2 < 2^44 is split into 22-bit halves so that
 // both wave sums stay below 2^30 (exact in int32).
 __device__ void prep_head(const StepArgs& a, int g, int v, QOperand* out, int h, int lane,
-                          uint2 qw);
+                          uint2 qw, bool own);
 
 // This lane's 4 BF16 query elements of head h of group g (dims 4 lane ..).
 __device__ __forceinline__ uint2 load_qw(const StepArgs& a, int g, int h, int lane) {
@@ -55,17 +55,19 @@ __device__ __forceinline__ uint2 load_qw(const StepArgs& a, int g, int h, int la
 }
 
 // Waves 0..3 form one head each from qw, their lanes' query words; the
-// operand is complete after the barrier.
+// operand is complete after the barrier.  Later waves repeat head H - 1 and
+// write nothing: every thread uses its query word, so the compiler keeps
+// the caller's query load where the caller issued it (first).
 __device__ void prep_operand(const StepArgs& a, int g, int v, QOperand* out, uint2 qw) {
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
-  if (h < H) prep_head(a, g, v, out, h, lane, qw);
+  prep_head(a, g, v, out, min(h, H - 1), lane, qw, h < H);
   __syncthreads();
 }
 
 // One wave per head: the integers X, their sum, the scale exponent and
 // ||q|| lambda (raw variant) of query head 4g + h.
 __device__ void prep_head(const StepArgs& a, int g, int v, QOperand* out, int h, int lane,
-                          uint2 qw) {
+                          uint2 qw, bool own) {
   const uint32_t qb[4] = {qw.x & 0xffffu, qw.x >> 16, qw.y & 0xffffu, qw.y >> 16};
   uint32_t bits[4];
   if (v != QV_RAW) {
@@ -99,7 +101,7 @@ __device__ void prep_head(const StepArgs& a, int g, int v, QOperand* out, int h,
     sq_lo += (int)(x2 & 0x3fffffu);
     sq_hi += (int)(x2 >> 22);
   }
-  *reinterpret_cast<int4*>(&out->X[h][4 * lane]) = make_int4(X[0], X[1], X[2], X[3]);
+  if (own) *reinterpret_cast<int4*>(&out->X[h][4 * lane]) = make_int4(X[0], X[1], X[2], X[3]);
   // B image: word (kc, lane l, m) holds bytes limb (col % 4) of X_{col/4}[dim]
   // for col = l % 16, dim = (l / 16) * 64 + kc * 16 + 4 byte + m (a lane's
   // 16-dim chunk transposed 4 x 4, to match the A words of expand2t and
@@ -107,23 +109,25 @@ __device__ void prep_head(const StepArgs& a, int g, int v, QOperand* out, int h,
   // of both keeps every dot).  This lane's dims 4 lane + i are byte
   // lane % 4 of words (kc = lane / 4 % 4, l = lane / 16 * 16 + 4h + limb,
   // m = i); X = l0 + 2^8 l1 + 2^16 l2 in signed bytes (|X| < 2^22), limb 3 = 0.
-  uint8_t* img = reinterpret_cast<uint8_t*>(&out->bimg[(lane >> 2) & 3][(lane >> 4) * 16 + 4 * h][0]) +
-                 (lane & 3);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int l0 = (int)(int8_t)(X[i] & 0xff);
-    const int x1 = (X[i] - l0) >> 8;
-    const int l1 = (int)(int8_t)(x1 & 0xff);
-    const int l2 = (x1 - l1) >> 8;
-    img[0 * 16 + 4 * i] = (uint8_t)l0;  // word (kc, l + limb, m = i): 16 bytes per l
-    img[1 * 16 + 4 * i] = (uint8_t)l1;
-    img[2 * 16 + 4 * i] = (uint8_t)l2;
-    img[3 * 16 + 4 * i] = 0;
+  if (own) {
+    uint8_t* img = reinterpret_cast<uint8_t*>(&out->bimg[(lane >> 2) & 3][(lane >> 4) * 16 + 4 * h][0]) +
+                   (lane & 3);
+  #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int l0 = (int)(int8_t)(X[i] & 0xff);
+      const int x1 = (X[i] - l0) >> 8;
+      const int l1 = (int)(int8_t)(x1 & 0xff);
+      const int l2 = (x1 - l1) >> 8;
+      img[0 * 16 + 4 * i] = (uint8_t)l0;  // word (kc, l + limb, m = i): 16 bytes per l
+      img[1 * 16 + 4 * i] = (uint8_t)l1;
+      img[2 * 16 + 4 * i] = (uint8_t)l2;
+      img[3 * 16 + 4 * i] = 0;
+    }
   }
   sx = wave_sum(sx);
   sq_lo = wave_sum(sq_lo);
   sq_hi = wave_sum(sq_hi);
-  if (lane == 0) {
+  if (own && lane == 0) {
     out->fx[h] = exmax - FX_HEADROOM;
     out->sum[h] = sx;
     if (v == QV_RAW) {
@@ -400,7 +404,7 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
 // than one pass of the grid covers), every FR_WAVES * gridDim.x tiles after
 // it, with the next tile's loads in flight while one is scored.
 template <bool LOOP>
-__global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
+__global__ __launch_bounds__(FR_BLOCK) void k_front(const uint16_t* __restrict__ q, StepArgs a) {
   SKV_TSB(4, 0);
   SKV_TS(0, 0);
   const int g = blockIdx.y, nc = a.nc;
@@ -410,7 +414,8 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(StepArgs a) {
   int tile = blockIdx.x * FR_WAVES + (threadIdx.x >> 6);
   // the query first: forming its operand then waits for it alone while the
   // plane loads are still in flight (waves 0 .. H-1 form heads 0 .. H-1)
-  const uint2 qw = load_qw(a, g, min((int)(threadIdx.x >> 6), H - 1), lane);
+  const uint2 qw = *reinterpret_cast<const uint2*>(
+      q + (g * H + min((int)(threadIdx.x >> 6), H - 1)) * D + 4 * lane);
   __builtin_amdgcn_sched_barrier(0);  // keep the query load ahead of the tile's
   FrTile cur = fr_load(a, g, tile, lane);
   __shared__ __align__(16) QOperand sq;
@@ -471,12 +476,14 @@ __device__ __forceinline__ void load_lds_masked(uint16_t* so, const uint16_t* __
 
 // Both selections of one (group, head) with its nc <= OCT_ITEMS centroids
 // held in registers, one octet of lower, upper and fine scores per thread.
-__device__ void select_in_registers(const StepArgs& a, int g, int h, FastScratch& fs) {
-  const int nc = a.nc, t = threadIdx.x;
+__device__ void select_in_registers(const StepArgs& a, const uint16_t* lower,
+                                    const uint16_t* upper, const uint16_t* fine, int nc, int g,
+                                    int h, FastScratch& fs) {
+  const int t = threadIdx.x;
   const size_t row = ((size_t)g * H + h) * nc;
-  const uint4 wl = load_oct(a.lower + row, nc);
-  const uint4 wu = load_oct(a.upper + row, nc);
-  const uint4 wf = load_oct(a.fine_ord + row, nc);
+  const uint4 wl = load_oct(lower + row, nc);
+  const uint4 wu = load_oct(upper + row, nc);
+  const uint4 wf = load_oct(fine + row, nc);
   auto cid = [](int i) { return (uint32_t)i; };
   const OctResult r1 = oct_select<true, true>(wl, a.P[g], cid, fs, 2);
   const uint32_t thr = r1.sel.all ? 0u : r1.sel.v;
@@ -493,11 +500,16 @@ __device__ void select_in_registers(const StepArgs& a, int g, int h, FastScratch
   SKV_TS(2, 15);
 }
 
-__global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
+// The leading arguments repeat the fields of a that the selection blocks'
+// first loads need (preloaded into scalar registers at dispatch).
+__global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint16_t* lower, const uint16_t* upper,
+                                                      const uint16_t* fine, int nc_arg,
+                                                      int exact_select, int dense_slices,
+                                                      StepArgs a) {
   SKV_TSB(5, 0);
   SKV_TS(2, 0);
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int n_dense = G * H * a.dense_slices;
+  const int n_dense = G * H * dense_slices;
   if ((int)blockIdx.x >= G * H + n_dense) {  // the q15 / qs operands of the later scorers
     const int i = blockIdx.x - G * H - n_dense, g = i / 2, v = QV_Q15 + i % 2;
     const int hq = min((int)(threadIdx.x >> 6), H - 1);
@@ -515,9 +527,9 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(StepArgs a) {
     SKV_TSE(5);
     return;
   }
-  const int g = blockIdx.x / H, h = blockIdx.x % H, nc = a.nc;
-  if (a.exact_select == 0 && nc <= OCT_ITEMS) {
-    select_in_registers(a, g, h, *reinterpret_cast<FastScratch*>(dyn));
+  const int g = blockIdx.x / H, h = blockIdx.x % H, nc = nc_arg;
+  if (exact_select == 0 && nc <= OCT_ITEMS) {
+    select_in_registers(a, lower, upper, fine, nc, g, h, *reinterpret_cast<FastScratch*>(dyn));
     SKV_TSE(5);
     return;
   }
@@ -764,10 +776,16 @@ __device__ __forceinline__ void lb_store(unsigned long long* p, unsigned long lo
 // postings at their pool positions, one posting per thread.  The prefix
 // rows of the range's postings are loaded before the look-back and scored
 // while wave 0 walks it, so the scores are ready with the positions.
-__global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
+// The leading arguments repeat the fields of a that the prologue loads need
+// (preloaded into scalar registers at dispatch).
+__global__ __launch_bounds__(PL_BLOCK) void k_pool(const uint32_t* selbm, const int* csr_off,
+                                                   const uint16_t* upper, const uint32_t* thr,
+                                                   const QOperand* qop,
+                                                   const unsigned* pool_epoch, int nc_arg,
+                                                   int pool_range, StepArgs a) {
   SKV_TSB(0, 0);
   SKV_TS(5, 0);
-  const int g = blockIdx.y, nc = a.nc, nb = gridDim.x;
+  const int g = blockIdx.y, nc = nc_arg, nb = gridDim.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
   extern __shared__ uint32_t s_bm[];
   __shared__ int s_off[PL_RANGE_MAX + 1], s_cum[PL_RANGE_MAX + 1], s_cl[PL_RANGE_MAX];
@@ -777,17 +795,17 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   // range b = block b: workgroups are dispatched in index order within each
   // XCD, so the lowest unfinished range always gets a slot and every wait
   // below ends.  The launch epoch tags this launch's records.
-  const int b = blockIdx.x, c0 = b * a.pool_range;
-  const int ncr = min(a.pool_range, nc - c0);  // centroids of the range (a multiple of 32)
+  const int b = blockIdx.x, c0 = b * pool_range;
+  const int ncr = min(pool_range, nc - c0);  // centroids of the range (a multiple of 32)
   // every load of the prologue is issued before the first wait: the group's
   // selected-cluster bitmap (<= 2048 words), the range's CSR offsets
   // (<= 513), and its centroids' upper bounds and the thresholds
-  const unsigned epoch = a.pool_epoch[g];
+  const unsigned epoch = pool_epoch[g];
   const unsigned long long tag = (unsigned long long)(epoch % LB_EPOCHS) << LB_EPOCH;
   constexpr int BM_PER = 65536 / 32 / PL_BLOCK;
   const int nbw = nc / 32;
-  const uint32_t* bm = a.selbm + (size_t)g * nbw;
-  const int* off = a.csr_off + (size_t)g * (nc + 1) + c0;
+  const uint32_t* bm = selbm + (size_t)g * nbw;
+  const int* off = csr_off + (size_t)g * (nc + 1) + c0;
   uint32_t bmw[BM_PER];
 #pragma unroll
   for (int u = 0; u < BM_PER; ++u) bmw[u] = bm[min(t + u * PL_BLOCK, nbw - 1)];
@@ -796,11 +814,11 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(StepArgs a) {
   uint32_t upv[H], thv[H];
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    upv[h] = a.upper[((size_t)g * H + h) * nc + cu];
-    thv[h] = a.thr[g * H + h];
+    upv[h] = upper[((size_t)g * H + h) * nc + cu];
+    thv[h] = thr[g * H + h];
   }
   // the 2-bit scorer's query operand (B image of 16 q15, its sum and scale)
-  const QOperand* q15 = &a.qop[g * QV_COUNT + QV_Q15];
+  const QOperand* q15 = &qop[g * QV_COUNT + QV_Q15];
   uint32_t bq[4][4];
   load_b(q15, bq);
   // lane l's head l / 16: s2 = (2 dq - 3 sum q15) 2^(fx + 4)
@@ -1059,19 +1077,25 @@ size_t topk_dynamic_lds(int lds_items) {
 // Per (group, head): members = top-k by (ordered score, lowest token) of the
 // n items; writes the membership bitmap.  LDS-resident when n <= lds_items,
 // otherwise 8-bit radix passes over the full 40-bit keys in memory.
-__global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
+// The leading arguments repeat the fields of t that the first loads need
+// (preloaded into scalar registers at dispatch, so those loads do not wait
+// for the argument block).
+__global__ __launch_bounds__(SEL_BLOCK) void k_topk(const int* count_word, const uint16_t* scores,
+                                                    int stride, int exact_select,
+                                                    const uint16_t* tile_max, int words,
+                                                    TopkArgs t) {
   SKV_TSB((t.count_slot == ST_POOL ? 6 : 7), 0);
   const int ts = t.count_slot == ST_POOL ? 7 : 10;
   SKV_TS(ts, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H;
   __shared__ SelectScratch s;
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int n = t.status[g * ST_WORDS + t.count_slot];
-  const uint16_t* sc = t.scores + ((size_t)g * H + h) * t.stride;
+  const int n = count_word[g * ST_WORDS];
+  const uint16_t* sc = scores + ((size_t)g * H + h) * stride;
   const int* tok = t.tokens + (size_t)g * t.stride;
-  uint64_t* bm = t.bitmap + ((size_t)g * H + h) * t.words;
+  uint64_t* bm = t.bitmap + ((size_t)g * H + h) * words;
   auto id = [tok](int i) { return (uint32_t)tok[i]; };
-  if (t.exact_select == 0 && n <= OCT_ITEMS) {  // the scores fit in registers
+  if (exact_select == 0 && n <= OCT_ITEMS) {  // the scores fit in registers
     const OctResult r = oct_select<false, false>(load_oct(sc, n), t.k, id,
                                                  *reinterpret_cast<FastScratch*>(dyn), ts);
     if (r.ok) {
@@ -1081,7 +1105,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
       return;
     }
   }
-  if (t.exact_select != 1) {
+  if (exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
     // the member bitmap: in LDS beside the scratch (cleared before the
     // selection) when it fits, else in place
@@ -1092,17 +1116,17 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(TopkArgs t) {
       for (int w = threadIdx.x; w < words; w += SEL_BLOCK) mb[w] = 0;
     FastResult r{};
     r.ok = false;
-    if (t.tile_max && t.exact_select != 1 && n > OCT_ITEMS && (n + 15) / 16 <= 4 * SEL_BLOCK) {
+    if (tile_max && exact_select != 1 && n > OCT_ITEMS && (n + 15) / 16 <= 4 * SEL_BLOCK) {
       // the producer wrote the max of every 16-item tile: only the tiles
       // reaching the cut are read for candidates
       uint32_t sv[FS_PER];
 #pragma unroll
       for (int u = 0; u < FS_PER; ++u) sv[u] = sc[fs_sample_item(n, u)];
-      r = tiled_select(RowTiles{sc}, t.tile_max + ((size_t)g * H + h) * t.tile_stride, sv, n, t.k,
-                       id, fs, t.exact_select == 2, ts);
+      r = tiled_select(RowTiles{sc}, tile_max + ((size_t)g * H + h) * t.tile_stride, sv, n, t.k,
+                       id, fs, exact_select == 2, ts);
       __syncthreads();
     }
-    if (!r.ok) r = fast_select(RowScores{sc}, n, t.k, id, fs, t.exact_select == 2, ts);
+    if (!r.ok) r = fast_select(RowScores{sc}, n, t.k, id, fs, exact_select == 2, ts);
     if (r.ok) {
       SKV_TS(ts, 6);
       if (!local) {
@@ -1182,8 +1206,15 @@ constexpr int us_block(int stage) { return stage == 4 ? 1024 : 512; }
 constexpr int US_GRID_U1 = 64;  // blocks per group over the pool
 constexpr int US_GRID_U2 = 32;  // blocks per group over U1 (<= 100 words; spans of >= US_CHUNK)
 
+// The leading arguments are the input count word (status + slot), the input
+// member bitmaps, the input token list, bitmap words per head and the token
+// list's stride per group: the fields the first loads need, preloaded into
+// scalar registers at dispatch.
 template <int STAGE>
-__global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
+__global__ __launch_bounds__(us_block(STAGE)) void k_union_score(const int* count_word,
+                                                                 const uint64_t* bm_in,
+                                                                 const int* tok_base, int W,
+                                                                 int tok_stride, StepArgs a) {
   constexpr bool U1 = STAGE == 4;
   constexpr int US_BLOCK = us_block(STAGE);
   constexpr int US_CHUNK = US_BLOCK / 64;  // bitmap words listed per pass (1 item per thread)
@@ -1192,11 +1223,10 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
   SKV_TS(ts, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n_in = a.status[g * ST_WORDS + (U1 ? ST_POOL : ST_U1)];
+  const int n_in = count_word[g * ST_WORDS];
   const int words_in = (n_in + 63) / 64;
-  const int W = U1 ? a.words_u1 : a.words_u2;
-  const uint64_t* __restrict__ bm = (U1 ? a.bm_u1 : a.bm_u2) + (size_t)g * H * W;
-  const int* __restrict__ tok_in = U1 ? a.pool_tok + (size_t)g * a.cap : a.u1_tok + (size_t)g * U1_MAX;
+  const uint64_t* __restrict__ bm = bm_in + (size_t)g * H * W;
+  const int* __restrict__ tok_in = tok_base + (size_t)g * tok_stride;
   const int cap_out = U1 ? U1_MAX : U2_MAX;
   int* __restrict__ tok_out = (U1 ? a.u1_tok : a.u2_tok) + (size_t)g * cap_out;
   uint16_t* __restrict__ s_out = U1 ? a.s4 : a.s8;
@@ -1343,7 +1373,12 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(StepArgs a) {
 constexpr int TOP_KPW = (TOPK + ATTN_WAVES - 1) / ATTN_WAVES;  // selected keys per wave
 constexpr int DENSE_PREF = 2;  // sink/local partials prefetched per merge thread
 
-__global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
+// The leading arguments repeat the fields of a that the first loads need
+// (preloaded into scalar registers at dispatch).
+__global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const uint16_t* s8,
+                                                      const int* u2_tok, const uint16_t* q_in,
+                                                      const float* dense_part, int dense_slices,
+                                                      int exact_select, StepArgs a) {
   SKV_TSB(9, 0);
   SKV_TS(13, 0);
   const int g = blockIdx.x / H, h = blockIdx.x % H, j = g * H + h;
@@ -1352,28 +1387,32 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
   __shared__ __align__(16) uint64_t s_key[TOPK];
   __shared__ int s_cnt;
   __shared__ AttnScratch att;
-  const int n = a.status[g * ST_WORDS + ST_U2];
-  const uint16_t* sc = a.s8 + (size_t)j * U2_MAX;
-  const int* tok = a.u2_tok + (size_t)g * U2_MAX;
+  const int n = status[g * ST_WORDS + ST_U2];
+  const uint16_t* sc = s8 + (size_t)j * U2_MAX;
+  const int* tok = u2_tok + (size_t)g * U2_MAX;
   auto id = [tok](int i) { return (uint32_t)tok[i]; };
   extern __shared__ __align__(16) unsigned char dyn[];
   // loads independent of the selection, issued first: the query and the
   // sink/local partials (consumed only by the final merge)
   float q[4];
-  load_q4(a, j, q);
+  {
+    const uint2 qw = *reinterpret_cast<const uint2*>(q_in + j * D + 4 * lane);
+    q[0] = bf16_f32(qw.x & 0xffff); q[1] = bf16_f32(qw.x >> 16);
+    q[2] = bf16_f32(qw.y & 0xffff); q[3] = bf16_f32(qw.y >> 16);
+  }
   const int d = threadIdx.x & (D - 1);
-  const float* parts = a.dense_part + (size_t)j * a.dense_slices * (D + 2);
+  const float* parts = dense_part + (size_t)j * dense_slices * (D + 2);
   float pm[DENSE_PREF], pl[DENSE_PREF], po[DENSE_PREF];
 #pragma unroll
   for (int r = 0; r < DENSE_PREF; ++r) {
-    const bool has = r < a.dense_slices && (int)threadIdx.x < D;
+    const bool has = r < dense_slices && (int)threadIdx.x < D;
     pm[r] = has ? parts[r * (D + 2) + D] : -INFINITY;
     pl[r] = has ? parts[r * (D + 2) + D + 1] : 0.f;
     po[r] = has ? parts[r * (D + 2) + d] : 0.f;
   }
   if (threadIdx.x == 0) s_cnt = 0;
   bool done = false;
-  if (a.exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: scores and IDs in registers
+  if (exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: scores and IDs in registers
     const uint4 w = load_oct(sc, n);
     uint4 t0 = make_uint4(0, 0, 0, 0), t1 = t0;
     if (8 * (int)threadIdx.x < n) {  // rows hold U2_MAX (a multiple of 8) entries
@@ -1408,9 +1447,9 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
       done = true;
     }
   }
-  if (!done && a.exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
+  if (!done && exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(RowScores{sc}, n, TOPK, id, fs, a.exact_select == 2, 13);
+    const FastResult r = fast_select(RowScores{sc}, n, TOPK, id, fs, exact_select == 2, 13);
     if (r.ok) {
       SKV_TS(13, 6);
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
@@ -1473,7 +1512,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
     float Mt = M;
 #pragma unroll
     for (int r = 0; r < DENSE_PREF; ++r) Mt = fmaxf(Mt, pm[r]);
-    for (int r = DENSE_PREF; r < a.dense_slices; ++r) Mt = fmaxf(Mt, parts[r * (D + 2) + D]);
+    for (int r = DENSE_PREF; r < dense_slices; ++r) Mt = fmaxf(Mt, parts[r * (D + 2) + D]);
     float Lt = 0.f, Ot = 0.f;
     if (M != -INFINITY) {
       const float sc0 = __expf(M - Mt);
@@ -1487,7 +1526,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
       Lt += pl[r] * f;
       Ot += po[r] * f;
     }
-    for (int r = DENSE_PREF; r < a.dense_slices; ++r) {
+    for (int r = DENSE_PREF; r < dense_slices; ++r) {
       const float mr = parts[r * (D + 2) + D];
       if (mr == -INFINITY) continue;
       const float f = __expf(mr - Mt);
@@ -1506,6 +1545,11 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(StepArgs a) {
 const char* const kKernelNames[N_STEP_KERNELS] = {
     "front", "select", "pool", "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
 
+static void launch_topk(const TopkArgs& t, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), lds, st, t.status + t.count_slot,
+                     t.scores, t.stride, t.exact_select, t.tile_max, t.words, t);
+}
+
 // Launch every kernel of one decode step on stream st.  If ev is non-NULL
 // (N_STEP_KERNELS + 1 events), ev[i] is recorded before kernel i and
 // ev[N_STEP_KERNELS] after the last one.
@@ -1515,32 +1559,41 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
   switch (k) {
     case 0:
       if (tiles_blocks * FR_CENTROIDS >= a.nc)
-        hipLaunchKernelGGL(k_front<false>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a);
+        hipLaunchKernelGGL(k_front<false>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a.q, a);
       else
-        hipLaunchKernelGGL(k_front<true>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a);
+        hipLaunchKernelGGL(k_front<true>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a.q, a);
       break;
     case 1:
       hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
-                         w.select_lds, st, a);
+                         w.select_lds, st, (const uint16_t*)a.lower, (const uint16_t*)a.upper,
+                         (const uint16_t*)a.fine_ord, a.nc, a.exact_select, a.dense_slices, a);
       break;
     case 2:
       hipLaunchKernelGGL(k_pool, dim3((a.nc + a.pool_range - 1) / a.pool_range, G), dim3(PL_BLOCK),
-                         bm_lds, st, a);
+                         bm_lds, st, (const uint32_t*)a.selbm, (const int*)a.csr_off,
+                         (const uint16_t*)a.upper, (const uint32_t*)a.thr, (const QOperand*)a.qop,
+                         (const unsigned*)a.pool_epoch, a.nc, a.pool_range, a);
       break;
     case 3:
-      hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u1_lds, st, w.top_u1);
+      launch_topk(w.top_u1, w.top_u1_lds, st);
       break;
     case 4:
-      hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(us_block(4)), 0, st, a);
+      hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(us_block(4)), 0, st,
+                         (const int*)a.status + ST_POOL, (const uint64_t*)a.bm_u1,
+                         (const int*)a.pool_tok, a.words_u1, a.cap, a);
       break;
     case 5:
-      hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), w.top_u2_lds, st, w.top_u2);
+      launch_topk(w.top_u2, w.top_u2_lds, st);
       break;
     case 6:
-      hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(us_block(8)), 0, st, a);
+      hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(us_block(8)), 0, st,
+                         (const int*)a.status + ST_U1, (const uint64_t*)a.bm_u2,
+                         (const int*)a.u1_tok, a.words_u2, U1_MAX, a);
       break;
     case 7:
-      hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st, a);
+      hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st,
+                         (const int*)a.status, (const uint16_t*)a.s8, (const int*)a.u2_tok, a.q,
+                         (const float*)a.dense_part, a.dense_slices, a.exact_select, a);
       break;
     default:
       break;
