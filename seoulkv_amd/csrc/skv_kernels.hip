@@ -692,19 +692,22 @@ __device__ __forceinline__ int lb_field(unsigned long long v, int shift, int bit
 // (the posting-ordered copy), 16 keys per int8 matrix-core tile.  A wave
 // scores the 64 postings its lanes hold, 4 tiles: s2_rows loads tile u's
 // rows (lane (kb, row) reads bytes 16 kb .. 16 kb + 15 of the row of the
-// posting held by lane 16 u + row; j < 0: absent, zeros).  s2_score
+// posting held by lane 16 u + row; j < 0, absent: row 0 is read instead,
+// and its score is never emitted).  The loads are unconditional, so all
+// four are in flight together (a conditional load makes the compiler wait
+// for it where the branches join).  s2_score
 // multiplies the query image (rows: head x limb) by the keys (columns), so
 // lane l receives the 4 limb sums of key l % 16 for head l / 16 in its 4
 // accumulator registers (no exchange between lanes), and returns in sc[u]
 // that key's ordered score; ls is head l / 16's scale.
 __device__ __forceinline__ void s2_rows(const uint8_t* __restrict__ rows, int j, uint4 (&w)[4]) {
   const int lane = threadIdx.x & 63, row = lane & 15, kb = lane >> 4;
+  int jj[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int jj = __shfl(j, 16 * u + row);
-    w[u] = jj >= 0 ? *reinterpret_cast<const uint4*>(rows + (size_t)jj * 64 + kb * 16)
-                   : make_uint4(0, 0, 0, 0);
-  }
+  for (int u = 0; u < 4; ++u) jj[u] = max(__shfl(j, 16 * u + row), 0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    w[u] = *reinterpret_cast<const uint4*>(rows + (size_t)jj[u] * 64 + kb * 16);
 }
 
 __device__ __forceinline__ void s2_score(const uint4 (&w)[4], const uint32_t (&bq)[4][4],
@@ -898,9 +901,11 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(const uint32_t* selbm, const 
   // mates are in; the rows (64 B per key) are the kernel's bulk traffic and
   // arrive during the scans and the look-back
   const uint8_t* __restrict__ rows = a.post_p2 + (size_t)g * a.np_max * 64;
+  // (every wave, both pages: straight-line loads stay in flight together;
+  // wave 0 and a missing second page read row 0, never scored)
   uint4 rw0[4], rw1[4];
-  if (wave > 0) s2_rows(rows, o0 ? j0 : -1, rw0);  // wave-uniform
-  if (wave > 0 && S > PL_PAGE) s2_rows(rows, o1 ? j1 : -1, rw1);
+  s2_rows(rows, o0 ? j0 : -1, rw0);
+  s2_rows(rows, o1 ? j1 : -1, rw1);
   // one scan for both pages: page 1 in the high half (a page owns < 2^16)
   int both;
   const int exb = block_excl_scan((o1 ? 1 << 16 : 0) | (o0 ? 1 : 0), s_scan, &both);
