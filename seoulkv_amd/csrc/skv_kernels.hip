@@ -666,6 +666,7 @@ constexpr int PL_SEL_BITS = 11;
 constexpr unsigned PL_SEL_MASK = (1u << PL_SEL_BITS) - 1u;
 static_assert(PL_RANGE_MAX <= (int)PL_SEL_MASK, "a range's selected count fits its scan field");
 constexpr int PL_PAGE = PL_BLOCK - WAVE;     // postings per page (waves 1..)
+constexpr int PL_BM_WORDS = 65536 / 32;      // selected-cluster bitmap words held in LDS (any nc)
 // 16-key tiles of s2 the first two pages' owned postings overlap (at most)
 constexpr int PL_TM_TILES = (2 * PL_PAGE + 15) / 16 + 1;
 
@@ -791,7 +792,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(const uint32_t* selbm, const 
   const int g = blockIdx.y, nc = nc_arg, nb = gridDim.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
   extern __shared__ uint32_t s_bm[];
-  __shared__ int s_off[PL_RANGE_MAX + 1], s_cum[PL_RANGE_MAX + 1], s_cl[PL_RANGE_MAX];
+  __shared__ int s_off[2 * PL_BLOCK], s_cum[PL_RANGE_MAX + 1], s_cl[PL_RANGE_MAX];
   __shared__ int s_scan[PL_WAVES + 1], s_surv;
   __shared__ unsigned long long s_excl;
   __shared__ uint32_t s_tm[H * PL_TM_TILES];  // tile maxima of the first two pages' keys
@@ -805,7 +806,7 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(const uint32_t* selbm, const 
   // (<= 513), and its centroids' upper bounds and the thresholds
   const unsigned epoch = pool_epoch[g];
   const unsigned long long tag = (unsigned long long)(epoch % LB_EPOCHS) << LB_EPOCH;
-  constexpr int BM_PER = 65536 / 32 / PL_BLOCK;
+  constexpr int BM_PER = PL_BM_WORDS / PL_BLOCK;
   const int nbw = nc / 32;
   const uint32_t* bm = selbm + (size_t)g * nbw;
   const int* off = csr_off + (size_t)g * (nc + 1) + c0;
@@ -827,11 +828,14 @@ __global__ __launch_bounds__(PL_BLOCK) void k_pool(const uint32_t* selbm, const 
   // lane l's head l / 16: s2 = (2 dq - 3 sum q15) 2^(fx + 4)
   const LimbScale ls(q15->fx[lane >> 4] + 4, 1);
   const double lc = LimbScale::offset(-3 * q15->sum[lane >> 4], q15->fx[lane >> 4] + 4);
+  // every slot stored (the bitmap's LDS copy is PL_BM_WORDS long; slots past
+  // nbw repeat the last word and are never read): a conditional store would
+  // let the compiler sink the bitmap load into it and wait there for every
+  // load issued before
 #pragma unroll
-  for (int u = 0; u < BM_PER; ++u)
-    if (t + u * PL_BLOCK < nbw) s_bm[t + u * PL_BLOCK] = bmw[u];
-  if (t <= ncr) s_off[t] = off0;
-  if (t + PL_BLOCK <= ncr) s_off[t + PL_BLOCK] = off1;
+  for (int u = 0; u < BM_PER; ++u) s_bm[t + u * PL_BLOCK] = bmw[u];
+  s_off[t] = off0;  // (unconditional, as s_bm: slots past ncr hold off[ncr], never read)
+  s_off[t + PL_BLOCK] = off1;
   if (t == 0) {
     s_surv = 0;
   }
@@ -1560,7 +1564,7 @@ static void launch_topk(const TopkArgs& t, size_t lds, hipStream_t st) {
 // ev[N_STEP_KERNELS] after the last one.
 void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) {
   const int tiles_blocks = std::min((a.nc + FR_CENTROIDS - 1) / FR_CENTROIDS, FR_MAX_BLOCKS);
-  const size_t bm_lds = (size_t)(a.nc / 32) * 4;
+  const size_t bm_lds = (size_t)PL_BM_WORDS * 4;
   switch (k) {
     case 0:
       if (tiles_blocks * FR_CENTROIDS >= a.nc)
@@ -1612,7 +1616,7 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   switch (k) {
     case 0: fn = reinterpret_cast<const void*>(&k_front<true>); break;
     case 1: fn = reinterpret_cast<const void*>(&k_select); dyn = w.select_lds; break;
-    case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)(a.nc / 32) * 4; break;
+    case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)PL_BM_WORDS * 4; break;
     case 3: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u1_lds; break;
     case 4: fn = reinterpret_cast<const void*>(&k_union_score<4>); break;
     case 5: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u2_lds; break;
