@@ -17,6 +17,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import random
 import statistics
 import sys
 import time
@@ -27,7 +28,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from seoulkv_amd import SeoulKV4, SeoulKV4Config, SeoulKV4Index  # noqa: E402
+from seoulkv_amd import KVPagePool, SeoulKV4, SeoulKV4Config, SeoulKV4Index  # noqa: E402
 from seoulkv_amd.index import build_cell, list_agreement, posting_cosine  # noqa: E402
 from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 
@@ -35,6 +36,7 @@ HBM_PEAK_GBS = 8000.0
 G_KV = 4  # KV heads of the layer
 APPEND_TOKENS = 128  # tokens appended after the measured steps (cache-append check)
 N_COLD = 10  # independent instances the cold-cache steps rotate over
+PAGE_TOKENS = 256  # tokens per page of the paged-records measurement
 METRIC = "µs/layer decode step at T=128K (1 GPU); achieved HBM GB/s; top-100 ID match"
 
 
@@ -388,6 +390,46 @@ def main() -> int:
         dn_kernel_ms, dn_merge_ms, dn_ms = rt.time_dense(reps=max(20, args.steps // 4))
         log(f"dense FP8 decode {dn_ms * 1e3:.1f} µs (partials {dn_kernel_ms * 1e3:.1f} µs)")
 
+        # the same cache with its FP8 records in 256-token pages of a shared
+        # pool, handed out in a scrambled order: same results, step and dense
+        # decode timed the same way
+        pool = KVPagePool(2 * (-(-p.context // PAGE_TOKENS)), page_tokens=PAGE_TOKENS,
+                          device=dev)
+        scrambled = pool.allocate(pool.n_pages)
+        random.Random(5).shuffle(scrambled)
+        pool.release(scrambled)
+        paged = SeoulKV4(device=dev, k=k, v=v, index=index,
+                         config=SeoulKV4Config(stage15_capacity=None, debug=True), kv_pool=pool)
+        paged_out = paged.run(q).to_torch().view(torch.int16).clone()
+        paged_ids = paged.debug_snapshot()["selected_ids"].numpy()
+        attn.run(q)
+        same_out = bool(torch.equal(paged_out, attn.run(q).to_torch().view(torch.int16)))
+        for _ in range(args.warmup):
+            paged._run_bound()
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            paged._run_bound()
+        end.record(stream)
+        end.synchronize()
+        paged_us = start.elapsed_time(end) / args.steps * 1e3
+        prt = paged._state
+        prt.dense_decode()
+        paged_dense_same = bool(torch.equal(prt.read_dense_output(), rt.read_dense_output()))
+        _, _, paged_dn_ms = prt.time_dense(reps=max(20, args.steps // 4))
+        paged.close()
+        del pool
+        log(f"paged records ({PAGE_TOKENS}-token pages): step {paged_us:.1f} µs, dense "
+            f"{paged_dn_ms * 1e3:.1f} µs, results identical: {same_out and paged_dense_same}")
+        paged_entry = {
+            "page_tokens": PAGE_TOKENS, "step_us": round(paged_us, 2),
+            "dense_us": round(paged_dn_ms * 1e3, 2),
+            "top100_equal": bool(np.array_equal(paged_ids, top_gpu)),
+            "output_equal": same_out, "dense_output_equal": paged_dense_same,
+            "note": "FP8 records in pool pages handed out in a scrambled order, read through "
+                    "the page table; device time of back-to-back steps",
+        }
+
         # cache append (after every measurement above: it grows the local
         # window): single-token host appends, one device append, then the
         # step over the grown window
@@ -517,6 +559,7 @@ def main() -> int:
             "sparse_over_dense": round(ms_per_step / dn_ms, 3),
         },
         "append": append,
+        "paged": paged_entry,
         "profiled_steps": n_prof,
         "stage_sizes": {k_: status[k_] for k_ in ("survivors", "selected", "pool", "u1", "u2")},
         "cpu_baseline": cpu,

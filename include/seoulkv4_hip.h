@@ -79,6 +79,34 @@ int skv_create(const skv_index_desc *index, const uint16_t *k_bf16,
                const uint16_t *v_bf16, int device, void *stream,
                void **handle_out);
 
+/* Paged FP8 K/V records (the next step after the reference's contiguous
+ * static cache; its README.md:66-69 leaves paged attention out).  The
+ * records live in a caller-owned device pool of pages:
+ *   pool = [n_pages][4 KV heads][page_tokens][512 B] FP8 [V || K],
+ * and logical page p (tokens p*page_tokens ..) of this cache is physical
+ * page page_table[p].  page_tokens is a power of two in [16, 65536];
+ * page_table (host, read during the call) holds ceil((context +
+ * append_capacity) / page_tokens) distinct entries in [0, n_pages); the pool
+ * is at most 2^31 records (n_pages x 4 x page_tokens).  The handle writes
+ * only its own pages, so several handles (sequences) may share one pool with
+ * disjoint tables; the pool must outlive the handle. */
+typedef struct {
+  void *pool;                  /* device pointer, 256-byte aligned */
+  int64_t n_pages;             /* pages in the pool */
+  int32_t page_tokens;         /* tokens per page */
+  const int32_t *page_table;   /* host [table_len] physical page of each logical page */
+  int32_t table_len;
+} skv_kv_pages;
+
+/* skv_create with the FP8 records in caller pages: the prefill records are
+ * written into them, skv_append fills them further, and the decode step and
+ * the dense decode read every record through the page table.  The key codes
+ * of the index (its retrieval region, fixed at prefill) stay in the handle's
+ * own memory.  Results are bit-identical to skv_create's contiguous layout. */
+int skv_create_paged(const skv_index_desc *index, const uint16_t *k_bf16,
+                     const uint16_t *v_bf16, const skv_kv_pages *pages,
+                     int device, void *stream, void **handle_out);
+
 /* Reference bind_query (_runtime.py:180-186): copies host Q [16][256] BF16
  * (query head j belongs to KV head j/4) to the device, asynchronously,
  * through a ring of 16 pinned staging slots: q_bf16 may be reused on return,
@@ -189,7 +217,8 @@ enum {
   SKV_STAGE_QPREP = 14,    /* int32  [4][3][260] fixed-point query operands */
   SKV_STAGE_KEYREC = 15,   /* uint8  [T][256] key records: 2-bit prefix plane |
                               2-bit residual plane | 4-bit residual plane */
-  SKV_STAGE_KV8 = 16,      /* uint8  [T][512] FP8 [V||K] records (group) */
+  SKV_STAGE_KV8 = 16,      /* uint8  [T][512] FP8 [V||K] records (group), in
+                              token order (paged records gathered page by page) */
   SKV_STAGE_KSCALE = 17    /* float  [256] key codec scales (group) */
 };
 int skv_read_stage(void *handle, int stage, int group, void *host_out,

@@ -9,6 +9,7 @@ The decode step runs as hand-written gfx950 HIP kernels behind the C ABI in
 from seoulkv_amd.api import SeoulKV4
 from seoulkv_amd.config import SeoulKV4Config
 from seoulkv_amd.index import SeoulKV4Index
+from seoulkv_amd.paged import KVPagePool
 from seoulkv_amd.result import DecodeResult
 
-__all__ = ["DecodeResult", "SeoulKV4", "SeoulKV4Config", "SeoulKV4Index"]
+__all__ = ["DecodeResult", "KVPagePool", "SeoulKV4", "SeoulKV4Config", "SeoulKV4Index"]

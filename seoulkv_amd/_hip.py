@@ -60,6 +60,16 @@ class IndexDesc(ctypes.Structure):
     ]
 
 
+class KVPagesDesc(ctypes.Structure):
+    _fields_ = [
+        ("pool", ctypes.c_void_p),
+        ("n_pages", ctypes.c_int64),
+        ("page_tokens", ctypes.c_int32),
+        ("page_table", ctypes.c_void_p),
+        ("table_len", ctypes.c_int32),
+    ]
+
+
 _lib = None
 
 
@@ -77,6 +87,8 @@ def load_library() -> ctypes.CDLL:
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     sig = {
         "skv_create": (i32, [ctypes.POINTER(IndexDesc), vp, vp, i32, vp, ctypes.POINTER(vp)]),
+        "skv_create_paged": (i32, [ctypes.POINTER(IndexDesc), vp, vp, ctypes.POINTER(KVPagesDesc),
+                                   i32, vp, ctypes.POINTER(vp)]),
         "skv_bind_query": (i32, [vp, vp]),
         "skv_bind_query_device": (i32, [vp, vp, vp]),
         "skv_enqueue": (i32, [vp]),
@@ -200,17 +212,39 @@ class Runtime:
 
     def __init__(self, device: int, k: torch.Tensor, v: torch.Tensor, index, *,
                  pool_min: int, pool_capacity: int | None, debug: bool, stream=None,
-                 append_capacity: int = 0):
+                 append_capacity: int = 0, kv_pages=None):
+        """``kv_pages``: ``(pool, page_table)`` to keep the FP8 records in
+        pages of a :class:`seoulkv_amd.paged.KVPagePool` (``skv_create_paged``);
+        ``None`` keeps them contiguous in the instance's own memory."""
         self.lib = load_library()
         desc, keep = index_desc(index, pool_min=pool_min, pool_capacity=pool_capacity,
                                 debug=debug, append_capacity=append_capacity)
         kb = _np(k, np.uint16)
         vb = _np(v, np.uint16)
         handle = ctypes.c_void_p()
-        code = self.lib.skv_create(
-            ctypes.byref(desc), _ptr(kb), _ptr(vb), int(device),
-            ctypes.c_void_p(stream or 0), ctypes.byref(handle),
-        )
+        self._pool = None
+        if kv_pages is None:
+            code = self.lib.skv_create(
+                ctypes.byref(desc), _ptr(kb), _ptr(vb), int(device),
+                ctypes.c_void_p(stream or 0), ctypes.byref(handle),
+            )
+        else:
+            pool, table = kv_pages
+            if pool.device.index is not None and pool.device.index != int(device):
+                raise ValueError(f"page pool is on {pool.device}, the instance on cuda:{device}")
+            tab = np.ascontiguousarray(np.asarray(table, dtype=np.int32))
+            pd = KVPagesDesc(pool=pool.pages.data_ptr(), n_pages=pool.n_pages,
+                             page_tokens=pool.page_tokens, page_table=_ptr(tab),
+                             table_len=int(tab.size))
+            # the pool's memory was allocated on torch's stream: order the
+            # prefill writes after it
+            torch.cuda.synchronize(pool.device)
+            code = self.lib.skv_create_paged(
+                ctypes.byref(desc), _ptr(kb), _ptr(vb), ctypes.byref(pd), int(device),
+                ctypes.c_void_p(stream or 0), ctypes.byref(handle),
+            )
+            self._pool = pool  # the pages must outlive the handle
+            self.page_table = tab.tolist()
         if code != 0:
             msg = self.lib.skv_last_error(None).decode()
             raise RuntimeError(f"skv_create failed ({ERRORS.get(code, code)}): {msg}")

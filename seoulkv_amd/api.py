@@ -16,6 +16,7 @@ import torch
 from seoulkv_amd import _hip
 from seoulkv_amd.config import MAX_CONTEXT, STAGE15_M, SeoulKV4Config, _KernelOptions
 from seoulkv_amd.index import MIN_CONTEXT, SeoulKV4Index
+from seoulkv_amd.paged import KVPagePool
 from seoulkv_amd.result import DecodeResult
 
 
@@ -31,16 +32,26 @@ def _device_ordinal(device) -> int:
 
 
 class SeoulKV4:
-    """Static-cache sparse decode.  Call ``run`` with a CPU BF16 post-RoPE query."""
+    """Static-cache sparse decode.  Call ``run`` with a CPU BF16 post-RoPE query.
+
+    ``kv_pool`` (an extension; the reference cache is contiguous): a
+    :class:`~seoulkv_amd.paged.KVPagePool` on the same device.  The instance
+    then takes the pages its context and append capacity need from the pool
+    when it initialises, keeps its FP8 records there (``page_table``) and
+    returns the pages on ``close()``."""
 
     def __init__(self, *, device, k: torch.Tensor, v: torch.Tensor, index: SeoulKV4Index,
-                 config: SeoulKV4Config | None = None):
+                 config: SeoulKV4Config | None = None, kv_pool: KVPagePool | None = None):
         self._config = SeoulKV4Config() if config is None else config
         if not isinstance(self._config, SeoulKV4Config) or not isinstance(index, SeoulKV4Index):
             raise TypeError("expected SeoulKV4Config and SeoulKV4Index")
+        if kv_pool is not None and not isinstance(kv_pool, KVPagePool):
+            raise TypeError("kv_pool must be a KVPagePool")
         if device is None:
             raise ValueError("supply a caller-owned ROCm device")
         ordinal = _device_ordinal(device)
+        if kv_pool is not None and (kv_pool.device.index or 0) != ordinal:
+            raise ValueError(f"kv_pool is on {kv_pool.device}, the instance on cuda:{ordinal}")
         context = index.zones.context
         if not MIN_CONTEXT <= context <= MAX_CONTEXT or context % 4:
             raise ValueError("unsupported context for the fixed SeoulKV4 candidate/tag profile")
@@ -56,6 +67,8 @@ class SeoulKV4:
         if context + self._config.append_capacity > MAX_CONTEXT:
             raise ValueError("context plus append_capacity exceeds 2^20 tokens")
         self._device = ordinal
+        self._kv_pool = kv_pool
+        self._pages: list[int] | None = None
         self._index = index
         self._host_kv = (k, v)
         self._args = _KernelOptions(context, self._config.stage15_capacity, self._config.debug)
@@ -94,14 +107,25 @@ class SeoulKV4:
         # device when it is a created stream; on the legacy default stream
         # the library uses a stream of its own (synchronize() orders both).
         stream = torch.cuda.current_stream(self._device).cuda_stream
-        state = _hip.Runtime(
-            self._device, k, v, self._index,
-            pool_min=self._args.stage15_m,
-            pool_capacity=self._args.stage15_capacity,
-            debug=self._args.debug,
-            stream=stream or None,
-            append_capacity=self._config.append_capacity,
-        )
+        kv_pages = None
+        if self._kv_pool is not None:
+            pool = self._kv_pool
+            self._pages = pool.allocate(
+                pool.pages_for(self._index.zones.context + self._config.append_capacity))
+            kv_pages = (pool, self._pages)
+        try:
+            state = _hip.Runtime(
+                self._device, k, v, self._index,
+                pool_min=self._args.stage15_m,
+                pool_capacity=self._args.stage15_capacity,
+                debug=self._args.debug,
+                stream=stream or None,
+                append_capacity=self._config.append_capacity,
+                kv_pages=kv_pages,
+            )
+        except Exception:
+            self._release_pages()
+            raise
         try:
             # First step is checked like the reference's initialisation
             # handoff (_kernels/stage1_fine/seoulkv4_stage1_live.py:56-81):
@@ -125,8 +149,20 @@ class SeoulKV4:
                 raise AssertionError("device selection changed across replay")
         except Exception:
             state.close()
+            self._release_pages()
             raise
         return state
+
+    def _release_pages(self):
+        if self._pages is not None:
+            self._kv_pool.release(self._pages)
+            self._pages = None
+
+    @property
+    def page_table(self) -> list[int] | None:
+        """Physical pool page of each logical page of this cache (paged
+        instances after initialisation), else ``None``."""
+        return None if self._pages is None else list(self._pages)
 
     def _bind_query(self, q):
         self._validate_query(q)
@@ -179,7 +215,7 @@ class SeoulKV4:
         self._require_open()
         meta = {
             "initialized": self.initialized,
-            "cache_layout": "flat",
+            "cache_layout": "flat" if self._kv_pool is None else "paged",
             "index": self._index.metadata(),
             "implementation": (
                 "query prep -> coarse 2-bit interval scan -> P-th lower bound -> survivor "
@@ -219,6 +255,7 @@ class SeoulKV4:
             self._closed = True
             if self._state is not None:
                 self._state.close()
+            self._release_pages()
             self._state = self._host_kv = self._index = None
 
     def __enter__(self):

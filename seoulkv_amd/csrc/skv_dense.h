@@ -17,7 +17,10 @@ constexpr int DN_TARGET_BLOCKS = 64;       // partials per KV group (upper bound
 constexpr int DN_MERGE_SLICES = 32;        // 8-dim output slices per query head in the merge
 
 struct DenseArgs {
-  const uint8_t* kv8;   // [G][rows][512]: fp8 V | fp8 K
+  const uint8_t* kv8;   // [G][rows][512]: fp8 V | fp8 K; paged: the page pool
+                        // [pages][G][1 << shift][512]
+  const int* table;     // paged records: physical page of each logical page (else NULL)
+  int shift;            // paged records: log2 tokens per page (>= log2 DN_TILE)
   const uint16_t* q;    // [16][256] bf16
   int T;                // keys attended (rows 0 .. T-1 of each group)
   int rows;             // records per group in kv8

@@ -125,6 +125,25 @@ __device__ __forceinline__ DnTile dn_load(const uint8_t* __restrict__ kv, int T,
   return x;
 }
 
+// The same tile from paged records: tile points at the record of its first
+// key t0; a page holds a power-of-two number (>= DN_TILE) of consecutive
+// tokens, so the 16 keys of an aligned tile are consecutive records of one
+// page; last = T - 1 - t0 clamps the rows past the context.
+__device__ __forceinline__ DnTile dn_load_paged(const uint8_t* __restrict__ tile, int last,
+                                                int lane) {
+  const int row = lane & 15, kb = lane >> 4;
+  DnTile x;
+  const uint8_t* kr = tile + (size_t)min(row, last) * 512 + 256 + kb * 32;
+  x.k[0] = *reinterpret_cast<const uint4*>(kr);
+  x.k[1] = *reinterpret_cast<const uint4*>(kr + 16);
+  x.k[2] = *reinterpret_cast<const uint4*>(kr + 128);
+  x.k[3] = *reinterpret_cast<const uint4*>(kr + 144);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    x.v[r] = *reinterpret_cast<const uint4*>(tile + (size_t)min(4 * kb + r, last) * 512 + 16 * row);
+  return x;
+}
+
 __device__ __forceinline__ v8i as_v8i(uint4 a, uint4 b) {
   return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
@@ -180,6 +199,8 @@ __device__ __forceinline__ void dn_tile(const DnTile& x, int t0, int T, int kb, 
   }
 }
 
+// PAGED: the records are read through the page table (a.table, a.shift).
+template <bool PAGED>
 __global__ __launch_bounds__(DN_BLOCK) void k_dense(DenseArgs a) {
   const int g = blockIdx.y, b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -206,18 +227,33 @@ __global__ __launch_bounds__(DN_BLOCK) void k_dense(DenseArgs a) {
   const int first = b * DN_WAVES * a.iters + wave;
   const int n = first < ntiles ? min(a.iters, (ntiles - first + DN_WAVES - 1) / DN_WAVES) : 0;
   auto key0 = [&](int i) { return (first + DN_WAVES * i) * DN_TILE; };
+  // paged: lane i (i + 64 in the second word) holds the record index of the
+  // first key of the wave's tile i (a wave has at most 128 tiles: T <= 2^20)
+  uint32_t prow[2] = {0u, 0u};
+  if (PAGED) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (lane + 64 * r < n) prow[r] = kv_row_paged(a.table, a.shift, g, key0(lane + 64 * r));
+  }
+  auto load = [&](int i) {
+    if (PAGED) {
+      const uint32_t r = __builtin_amdgcn_readlane(i < 64 ? prow[0] : prow[1], i & 63);
+      return dn_load_paged(a.kv8 + (size_t)r * 512, T - 1 - key0(i), lane);
+    }
+    return dn_load(kv, T, key0(i), lane);
+  };
   if (n > 0) {
     // three tiles in registers: two loads in flight while one is processed
-    DnTile b0 = dn_load(kv, T, key0(0), lane), b1, b2;
-    if (n > 1) b1 = dn_load(kv, T, key0(1), lane);
+    DnTile b0 = load(0), b1, b2;
+    if (n > 1) b1 = load(1);
     for (int i = 0;; i += 3) {
-      if (i + 2 < n) b2 = dn_load(kv, T, key0(i + 2), lane);
+      if (i + 2 < n) b2 = load(i + 2);
       dn_tile(b0, key0(i), T, kb, bq, zc, o, m, l);
       if (i + 1 >= n) break;
-      if (i + 3 < n) b0 = dn_load(kv, T, key0(i + 3), lane);
+      if (i + 3 < n) b0 = load(i + 3);
       dn_tile(b1, key0(i + 1), T, kb, bq, zc, o, m, l);
       if (i + 2 >= n) break;
-      if (i + 4 < n) b1 = dn_load(kv, T, key0(i + 4), lane);
+      if (i + 4 < n) b1 = load(i + 4);
       dn_tile(b2, key0(i + 2), T, kb, bq, zc, o, m, l);
       if (i + 3 >= n) break;
     }
@@ -335,7 +371,8 @@ __global__ __launch_bounds__(256) void k_dense_merge(DenseArgs a) {
 
 void launch_dense(const DenseArgs& a, hipStream_t st, int k) {
   if (k == 0)
-    hipLaunchKernelGGL(k_dense, dim3(a.nb, G), dim3(DN_BLOCK), 0, st, a);
+    hipLaunchKernelGGL(a.table ? k_dense<true> : k_dense<false>, dim3(a.nb, G), dim3(DN_BLOCK), 0,
+                       st, a);
   else
     hipLaunchKernelGGL(k_dense_merge, dim3(G * H, DN_MERGE_SLICES), dim3(256), 0, st, a);
 }

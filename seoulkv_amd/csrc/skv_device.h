@@ -28,6 +28,16 @@ constexpr int U2_MAX = H * M16;
 constexpr int FX_HEADROOM = 14;
 constexpr int WAVE = 64;
 
+// Record index of token tok of KV group g in paged FP8 [V || K] records (the
+// record is at pool + 512 * index): token tok lies at slot tok mod 2^shift of
+// logical page tok >> shift, and a physical page holds the G groups' slots
+// one group after another.  Contiguous records are simply g * rows + tok.
+__host__ __device__ __forceinline__ uint32_t kv_row_paged(const int* table, int shift, int g,
+                                                          int tok) {
+  return (((uint32_t)table[tok >> shift] * G + (uint32_t)g) << shift) |
+         ((uint32_t)tok & ((1u << shift) - 1u));
+}
+
 // Query operand variants.
 enum { QV_RAW = 0, QV_Q15 = 1, QV_QS = 2, QV_COUNT = 3 };
 

@@ -271,7 +271,21 @@ __device__ __forceinline__ void merge_waves(const AttnScratch& s, int d, float& 
   }
 }
 
-// Dense slice r of query head j: keys r*128 .. r*128+127 of [sink | local].
+// Record base and per-lane record index of token tk (-1: none) of group g:
+// contiguous records index tokens from the group's first record, paged ones
+// index the pool through the page table.
+template <bool PAGED>
+__device__ __forceinline__ const uint8_t* kv_base(const StepArgs& a, int g) {
+  return PAGED ? a.kv8 : a.kv8 + (size_t)g * a.kv_rows * 512;
+}
+template <bool PAGED>
+__device__ __forceinline__ int kv_lane_row(const StepArgs& a, int g, int tk) {
+  if (!PAGED || tk < 0) return tk;
+  return (int)kv_row_paged(a.kv_table, a.kv_shift, g, tk);
+}
+
+// Dense slice r of query head j: keys r*256 .. r*256+255 of [sink | local].
+template <bool PAGED>
 __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
   const int j = blk / a.dense_slices, r = blk % a.dense_slices, g = j / H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -282,7 +296,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
   const int i = r * DENSE_BLOCK_KEYS + wave * SDPA_WAVE_KEYS + lane;
   if (lane < SDPA_WAVE_KEYS && i < ndense) tk = i < a.sink ? i : a.T - a.local + (i - a.sink);
   float m, l, o[4];
-  wave_attend(a.kv8 + (size_t)g * a.kv_rows * 512, q, tk, m, l, o);
+  wave_attend(kv_base<PAGED>(a, g), q, kv_lane_row<PAGED>(a, g, tk), m, l, o);
   stash_wave(s, m, l, o);
   __syncthreads();
   if (threadIdx.x < D) {
@@ -501,7 +515,9 @@ __device__ void select_in_registers(const StepArgs& a, const uint16_t* lower,
 }
 
 // The leading arguments repeat the fields of a that the selection blocks'
-// first loads need (preloaded into scalar registers at dispatch).
+// first loads need (preloaded into scalar registers at dispatch).  PAGED: the
+// sink/local records are read through the page table.
+template <bool PAGED>
 __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint16_t* lower, const uint16_t* upper,
                                                       const uint16_t* fine, int nc_arg,
                                                       int exact_select, int dense_slices,
@@ -523,7 +539,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint16_t* lower, con
     return;
   }
   if (blockIdx.x >= G * H) {  // sink/local attention slices (depend only on Q)
-    dense_attend(a, blockIdx.x - G * H, *reinterpret_cast<AttnScratch*>(dyn));
+    dense_attend<PAGED>(a, blockIdx.x - G * H, *reinterpret_cast<AttnScratch*>(dyn));
     SKV_TSE(5);
     return;
   }
@@ -1383,7 +1399,9 @@ constexpr int TOP_KPW = (TOPK + ATTN_WAVES - 1) / ATTN_WAVES;  // selected keys 
 constexpr int DENSE_PREF = 2;  // sink/local partials prefetched per merge thread
 
 // The leading arguments repeat the fields of a that the first loads need
-// (preloaded into scalar registers at dispatch).
+// (preloaded into scalar registers at dispatch).  PAGED: the selected records
+// are read through the page table.
+template <bool PAGED>
 __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const uint16_t* s8,
                                                       const int* u2_tok, const uint16_t* q_in,
                                                       const float* dense_part, int dense_slices,
@@ -1499,7 +1517,8 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
     const int i = wave + ATTN_WAVES * lane;
     if (i < m) tk = (int)(0xfffffu - (uint32_t)(s_key[i] & 0xfffffu));
   }
-  const AttnLoads<TOP_KPW> L = attend_load<TOP_KPW>(a.kv8 + (size_t)g * a.kv_rows * 512, tk);
+  const AttnLoads<TOP_KPW> L =
+      attend_load<TOP_KPW>(kv_base<PAGED>(a, g), kv_lane_row<PAGED>(a, g, tk));
   // the output list, best first (member keys are distinct)
   int* out = a.top + j * TOPK;
   if ((int)threadIdx.x < m) {
@@ -1573,7 +1592,8 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
         hipLaunchKernelGGL(k_front<true>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a.q, a);
       break;
     case 1:
-      hipLaunchKernelGGL(k_select, dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
+      hipLaunchKernelGGL(a.kv_table ? k_select<true> : k_select<false>,
+                         dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
                          w.select_lds, st, (const uint16_t*)a.lower, (const uint16_t*)a.upper,
                          (const uint16_t*)a.fine_ord, a.nc, a.exact_select, a.dense_slices, a);
       break;
@@ -1600,7 +1620,8 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
                          (const int*)a.u1_tok, a.words_u2, U1_MAX, a);
       break;
     case 7:
-      hipLaunchKernelGGL(k_top100, dim3(G * H), dim3(SEL_BLOCK), sizeof(FastScratch), st,
+      hipLaunchKernelGGL(a.kv_table ? k_top100<true> : k_top100<false>, dim3(G * H),
+                         dim3(SEL_BLOCK), sizeof(FastScratch), st,
                          (const int*)a.status, (const uint16_t*)a.s8, (const int*)a.u2_tok, a.q,
                          (const float*)a.dense_part, a.dense_slices, a.exact_select, a);
       break;
@@ -1615,13 +1636,21 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   size_t dyn = 0;
   switch (k) {
     case 0: fn = reinterpret_cast<const void*>(&k_front<true>); break;
-    case 1: fn = reinterpret_cast<const void*>(&k_select); dyn = w.select_lds; break;
+    case 1:
+      fn = a.kv_table ? reinterpret_cast<const void*>(&k_select<true>)
+                      : reinterpret_cast<const void*>(&k_select<false>);
+      dyn = w.select_lds;
+      break;
     case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)PL_BM_WORDS * 4; break;
     case 3: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u1_lds; break;
     case 4: fn = reinterpret_cast<const void*>(&k_union_score<4>); break;
     case 5: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u2_lds; break;
     case 6: fn = reinterpret_cast<const void*>(&k_union_score<8>); break;
-    case 7: fn = reinterpret_cast<const void*>(&k_top100); dyn = sizeof(FastScratch); break;
+    case 7:
+      fn = a.kv_table ? reinterpret_cast<const void*>(&k_top100<true>)
+                      : reinterpret_cast<const void*>(&k_top100<false>);
+      dyn = sizeof(FastScratch);
+      break;
     default: return hipErrorInvalidValue;
   }
   hipFuncAttributes attr;

@@ -79,6 +79,7 @@ struct Handle {
   int top_u1_lds_items = 0, top_u2_lds_items = 0;  // LDS-resident sizes (select modes 0-2)
   bool dense_ran = false;
   bool bound = false, ran = false;
+  std::vector<int> page_table;  // paged records: physical page of each logical page
   size_t lds_per_block = 0;
   // per-kernel event timing (skv_profile)
   bool profiling = false, prof_pending = false;
@@ -109,12 +110,13 @@ void build_meta(Handle* h) {
            "\"pool_min\": %d, \"pool_capacity\": %d, \"postings_max\": %d, "
            "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
            "\"kernels_per_step\": %d, \"lds_per_block\": %zu, \"pool_lds_items\": %d, "
-           "\"prefill_context\": %d, \"appended\": %d, \"append_capacity\": %d}",
+           "\"prefill_context\": %d, \"appended\": %d, \"append_capacity\": %d, "
+           "\"kv_page_tokens\": %d}",
            json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), a.T, a.sink,
            a.local, h->n_centroids, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min,
            a.pool_capacity, h->np_max, h->static_bytes, h->work_bytes, N_STEP_KERNELS,
            h->lds_per_block, h->w.top_u1.lds_items, h->context0, a.T - h->context0,
-           h->append_capacity);
+           h->append_capacity, a.kv_table ? 1 << a.kv_shift : 0);
   h->meta = buf;
 }
 
@@ -194,10 +196,12 @@ __global__ void k_init_keyrec(const uint16_t* k, const float* kscale, int T, uin
 }
 
 // FP8 [V || K] records of n tokens: k, v [G][n][256] bf16 (rows of the
-// group g that are src_stride tokens apart) -> kv8 rows row0 .. row0+n-1 of
-// each group (rows records per group).  One thread per (group, token, 4 dims).
+// group g that are src_stride tokens apart) -> records of tokens row0 ..
+// row0+n-1 of each group: rows row0 + t of kv8's [G][rows] records, or with a
+// page table, the paged record of token row0 + t.  One thread per (group,
+// token, 4 dims).
 __global__ void k_pack_kv8(const uint16_t* k, const uint16_t* v, int n, size_t src_stride,
-                           int row0, int rows, uint8_t* kv8) {
+                           int row0, int rows, uint8_t* kv8, const int* table, int shift) {
   const size_t total = (size_t)G * n * (D / 4);
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -213,7 +217,8 @@ __global__ void k_pack_kv8(const uint16_t* k, const uint16_t* v, int n, size_t s
              (f32_to_fp8_e4m3(bf16_f32(w.y & 0xffffu)) << 16) |
              (f32_to_fp8_e4m3(bf16_f32(w.y >> 16)) << 24);
     };
-    uint8_t* rec = kv8 + ((size_t)g * rows + row0 + t) * 512;
+    uint8_t* rec = kv8 + (table ? (size_t)kv_row_paged(table, shift, g, row0 + t)
+                                : (size_t)g * rows + row0 + t) * 512;
     *reinterpret_cast<uint32_t*>(rec + 4 * c) = pack(vw);
     *reinterpret_cast<uint32_t*>(rec + 256 + 4 * c) = pack(kw);
   }
@@ -309,8 +314,10 @@ void skv_destroy(void* handle) {
   delete h;
 }
 
-int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
-               int device, void* stream, void** handle_out) {
+// skv_create / skv_create_paged; pages NULL: contiguous records in the
+// handle's own memory.
+static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
+                       const skv_kv_pages* pages, int device, void* stream, void** handle_out) {
   if (!handle_out) return fail(nullptr, SKV_EINVAL, "handle_out is NULL");
   *handle_out = nullptr;
   if (!ix || !k_bf16 || !v_bf16) return fail(nullptr, SKV_EINVAL, "NULL index or K/V");
@@ -325,6 +332,32 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
                 ix->append_capacity);
   const int cap_app = ix->append_capacity;
   const int R = T - ix->sink - ix->local;
+  int page_shift = 0, table_len = 0;
+  if (pages) {
+    const int pt = pages->page_tokens;
+    if (!pages->pool || ((uintptr_t)pages->pool & 255))
+      return fail(nullptr, SKV_EINVAL, "page pool is NULL or not 256-byte aligned");
+    if (pt < 16 || pt > 65536 || (pt & (pt - 1)))
+      return fail(nullptr, SKV_EINVAL, "page_tokens %d is not a power of two in [16, 65536]", pt);
+    while ((1 << page_shift) < pt) ++page_shift;
+    if (pages->n_pages < 1 || pages->n_pages * G * (int64_t)pt > ((int64_t)1 << 31))
+      return fail(nullptr, SKV_EINVAL, "page pool of %lld pages: 1 to 2^31 records",
+                  (long long)pages->n_pages);
+    table_len = (T + cap_app + pt - 1) / pt;
+    if (!pages->page_table || pages->table_len < table_len)
+      return fail(nullptr, SKV_EINVAL, "page table of %d entries; context %d plus capacity %d "
+                  "needs %d pages of %d tokens", pages->page_table ? pages->table_len : 0, T,
+                  cap_app, table_len, pt);
+    std::vector<int> sorted(pages->page_table, pages->page_table + table_len);
+    std::sort(sorted.begin(), sorted.end());
+    for (int i = 0; i < table_len; ++i) {
+      if (sorted[i] < 0 || sorted[i] >= pages->n_pages)
+        return fail(nullptr, SKV_EINVAL, "page table entry %d outside [0, %lld)", sorted[i],
+                    (long long)pages->n_pages);
+      if (i && sorted[i] == sorted[i - 1])
+        return fail(nullptr, SKV_EINVAL, "page %d appears twice in the page table", sorted[i]);
+    }
+  }
 
   // ---- host-side validation and the spill-2 mate table
   std::vector<std::vector<int>> mates(G);
@@ -448,7 +481,10 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
     a.post_mate = (int*)ar.take((size_t)G * np_max * 4);
     a.post_p2 = (uint8_t*)ar.take((size_t)G * np_max * 64);
     a.keyrec = (uint8_t*)ar.take((size_t)G * T * 256);
-    a.kv8 = (uint8_t*)ar.take((size_t)G * (T + cap_app) * 512);
+    if (pages)  // the records live in the caller's pages
+      a.kv_table = (int*)ar.take((size_t)table_len * 4);
+    else
+      a.kv8 = (uint8_t*)ar.take((size_t)G * (T + cap_app) * 512);
   };
   plan_static(s);
   h->static_bytes = s.used;
@@ -459,6 +495,16 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   s.base = (char*)h->static_mem;
   s.used = 0;
   plan_static(s);
+  if (pages) {
+    a.kv8 = static_cast<const uint8_t*>(pages->pool);
+    a.kv_shift = page_shift;
+    h->page_table.assign(pages->page_table, pages->page_table + table_len);
+    if (hipMemcpy(const_cast<int*>(a.kv_table), h->page_table.data(), (size_t)table_len * 4,
+                  hipMemcpyHostToDevice) != hipSuccess) {
+      fail(h, SKV_EHIP, "page table upload failed");
+      return bail(SKV_EHIP);
+    }
+  }
 
   // ---- workspace arena
   Arena wk;
@@ -508,6 +554,8 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   wk.used = 0;
   plan_work(wk);
   h->dn.kv8 = a.kv8;
+  h->dn.table = a.kv_table;
+  h->dn.shift = a.kv_shift;
   h->dn.q = a.q;
   if (hipMemsetAsync(h->work_mem, 0, h->work_bytes, h->stream) != hipSuccess) {
     fail(h, SKV_EHIP, "workspace clear failed");
@@ -581,7 +629,7 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
       hipLaunchKernelGGL(k_init_keyrec, dim3(8192), dim3(256), 0, h->stream, dk, a.kscale, T,
                          (uint8_t*)a.keyrec);
       hipLaunchKernelGGL(k_pack_kv8, dim3(8192), dim3(256), 0, h->stream, dk, dv, T, (size_t)T, 0,
-                         a.kv_rows, (uint8_t*)a.kv8);
+                         a.kv_rows, (uint8_t*)a.kv8, a.kv_table, a.kv_shift);
       hipLaunchKernelGGL(k_init_postp2, dim3(4096), dim3(256), 0, h->stream, a.post_tok, a.keyrec, T,
                          np_max, dnp, (uint8_t*)a.post_p2);
       ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(h->stream) == hipSuccess;
@@ -645,6 +693,20 @@ int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t*
   build_meta(h);
   *handle_out = h;
   return SKV_OK;
+}
+
+int skv_create(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
+               int device, void* stream, void** handle_out) {
+  return create_impl(ix, k_bf16, v_bf16, nullptr, device, stream, handle_out);
+}
+
+int skv_create_paged(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
+                     const skv_kv_pages* pages, int device, void* stream, void** handle_out) {
+  if (!pages) {
+    if (handle_out) *handle_out = nullptr;
+    return fail(nullptr, SKV_EINVAL, "NULL page descriptor");
+  }
+  return create_impl(ix, k_bf16, v_bf16, pages, device, stream, handle_out);
 }
 
 int skv_bind_query(void* handle, const uint16_t* q) {
@@ -802,7 +864,8 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
   HIPCHK(h, hipSetDevice(h->device));
   if (on_device) {
     hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * n * (D / 4) + 255) / 256)), dim3(256),
-                       0, h->stream, k, v, n, (size_t)n, a.T, a.kv_rows, (uint8_t*)a.kv8);
+                       0, h->stream, k, v, n, (size_t)n, a.T, a.kv_rows, (uint8_t*)a.kv8,
+                       a.kv_table, a.kv_shift);
     HIPCHK(h, hipGetLastError());
   } else {
     const int chunk = std::min(h->append_capacity, APPEND_CHUNK);
@@ -818,7 +881,7 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
       }
       hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * c * (D / 4) + 255) / 256)),
                          dim3(256), 0, h->stream, sk, sv, c, (size_t)c, a.T + t0, a.kv_rows,
-                         (uint8_t*)a.kv8);
+                         (uint8_t*)a.kv8, a.kv_table, a.kv_shift);
       HIPCHK(h, hipGetLastError());
     }
   }
@@ -1056,6 +1119,17 @@ int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t c
                        (int64_t)a.rec_rows * 256, 1);
     }
     case SKV_STAGE_KV8:
+      if (a.kv_table) {  // paged: the group's slots page by page, in token order
+        if ((int64_t)a.T * 512 > cap) return fail(h, SKV_EINVAL, "stage buffer too small");
+        const int pt = 1 << a.kv_shift;
+        for (int t0 = 0; t0 < a.T; t0 += pt) {
+          const size_t row = kv_row_paged(h->page_table.data(), a.kv_shift, group, t0);
+          HIPCHK(h, hipMemcpy((char*)host_out + (size_t)t0 * 512, a.kv8 + row * 512,
+                              (size_t)std::min(pt, a.T - t0) * 512, hipMemcpyDeviceToHost));
+        }
+        if (count_out) *count_out = (int64_t)a.T * 512;
+        return SKV_OK;
+      }
       return copy_rows(a.kv8 + (size_t)group * a.kv_rows * 512, 0, 1, (int64_t)a.T * 512, 1);
     case SKV_STAGE_KSCALE:
       return copy_rows(a.kscale + group * D, 0, 4, D, 1);

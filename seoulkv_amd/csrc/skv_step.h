@@ -77,7 +77,10 @@ struct StepArgs {
   const int* post_mate;     // [G][np_max] (-1: no mate)
   const uint8_t* post_p2;   // [G][np_max][64]
   const uint8_t* keyrec;    // [G][rec_rows][256]: p2 | r2 | r4 planes
-  const uint8_t* kv8;       // [G][kv_rows][512]: fp8 V | fp8 K (rows < T valid)
+  const uint8_t* kv8;       // [G][kv_rows][512]: fp8 V | fp8 K (rows < T valid); paged:
+                            // the page pool [pages][G][1 << kv_shift][512]
+  const int* kv_table;      // paged records: physical page of each logical page (else NULL)
+  int kv_shift;             // paged records: log2 tokens per page
   // per-step workspace
   QOperand* qop;            // [G][QV_COUNT]
   uint16_t* lower;          // [G][H][nc] ordered BF16

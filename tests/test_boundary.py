@@ -98,6 +98,43 @@ def test_create_rejects_spill_violations(lib):
     assert code == SKV_EINVAL and "token ID" in msg
 
 
+def test_create_paged_rejects_bad_page_descriptors_on_the_host(lib):
+    """``skv_create_paged`` validates the page pool and table before it
+    touches a device (no GPU here): alignment, page size, pool size, table
+    length, entries in range and distinct."""
+    desc, keep = _desc()
+    kb = np.zeros(4, dtype=np.uint16)
+    need = -(-desc.context // 256)
+
+    def create(pool=1 << 20, n_pages=need, page_tokens=256, table=None, table_len=None):
+        tab = np.arange(need, dtype=np.int32) if table is None else np.asarray(table, np.int32)
+        pd = _hip.KVPagesDesc(pool=pool, n_pages=n_pages, page_tokens=page_tokens,
+                              page_table=tab.ctypes.data,
+                              table_len=tab.size if table_len is None else table_len)
+        handle = ctypes.c_void_p()
+        code = lib.skv_create_paged(ctypes.byref(desc), kb.ctypes.data, kb.ctypes.data,
+                                    ctypes.byref(pd), 0, None, ctypes.byref(handle))
+        return code, handle.value, lib.skv_last_error(None).decode()
+
+    handle = ctypes.c_void_p()
+    assert lib.skv_create_paged(ctypes.byref(desc), kb.ctypes.data, kb.ctypes.data, None, 0,
+                                None, ctypes.byref(handle)) == SKV_EINVAL
+    for kwargs, text in (
+        (dict(pool=0), "NULL"),
+        (dict(pool=(1 << 20) + 64), "aligned"),
+        (dict(page_tokens=8), "power of two"),
+        (dict(page_tokens=384), "power of two"),
+        (dict(n_pages=0), "pages"),
+        (dict(n_pages=(1 << 21) + 1), "2^31"),
+        (dict(table_len=need - 1), "needs %d pages" % need),
+        (dict(table=[*range(need - 1), need]), "outside"),
+        (dict(table=[*range(need - 1), -1]), "outside"),
+        (dict(table=[*range(need - 1), 0]), "twice"),
+    ):
+        code, h, msg = create(**kwargs)
+        assert code == SKV_EINVAL and h is None and text in msg, (kwargs, msg)
+
+
 def test_handle_entry_points_reject_null(lib):
     # a NULL handle is a closed handle: SKV_ESTATE
     assert lib.skv_enqueue(None) == SKV_ESTATE
