@@ -7,6 +7,7 @@ caller uses."""
 from __future__ import annotations
 
 import functools
+import random
 import types
 
 import numpy as np
@@ -227,16 +228,28 @@ def _with_nprobe(index, nprobe):
 
 
 def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048, queries=(0,),
-                      n_queries=1):
+                      n_queries=1, page_tokens=None):
     """Every funnel stage bit-exact against the oracle on a BASELINE-sized
-    cache (seeded synthetic inputs), output within the attention tolerance."""
+    cache (seeded synthetic inputs), output within the attention tolerance.
+    page_tokens: keep the FP8 records in pages of that size, handed out by a
+    page pool in a seeded random order."""
     print(f"[gpu] {name} P={nprobe} clustered={clustered}: inputs", flush=True)
     prof, k, v, qs, index, (code8, scales, k8, v8) = _full_size_inputs(name, clustered,
                                                                         n_queries)
     if nprobe is not None and nprobe != prof.nprobe:
         index = _with_nprobe(index, nprobe)
     cells = [od.GroupCell.from_cell(c) for c in index.cells]
-    rt = _hip.Runtime(0, k, v, index, pool_min=pool_min, pool_capacity=None, debug=True)
+    kv_pages = None
+    if page_tokens:
+        from seoulkv_amd import KVPagePool
+
+        need = -(-prof.context // page_tokens)
+        pool = KVPagePool(need + 64, page_tokens=page_tokens, device="cuda:0")
+        pages = pool.allocate(pool.n_pages)
+        random.Random(page_tokens).shuffle(pages)
+        kv_pages = (pool, pages[:need])
+    rt = _hip.Runtime(0, k, v, index, pool_min=pool_min, pool_capacity=None, debug=True,
+                      kv_pages=kv_pages)
     try:
         for qi in queries:
             print(f"[gpu] {name}: oracle q{qi}", flush=True)
@@ -264,6 +277,14 @@ def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048, queri
 def test_full_size_parity_config2():
     """T = 131072, nc = 8192, P = 384; three queries."""
     _full_size_parity("cfg2", queries=(0, 1, 2), n_queries=3)
+
+
+@pytest.mark.slow
+def test_full_size_parity_config2_paged_records():
+    """Configuration 2 with the FP8 records in 16-token pages of a pool, in a
+    scrambled order (a page table of 8192 entries): every stage and the
+    output as for the contiguous records."""
+    _full_size_parity("cfg2", queries=(0, 1), n_queries=3, page_tokens=16)
 
 
 @pytest.mark.slow

@@ -9,6 +9,8 @@ half an ulp <= 2^-8 relative) of an FP32 result, so a dropped query term
 
 from __future__ import annotations
 
+import random
+
 import numpy as np
 import pytest
 import torch
@@ -38,12 +40,29 @@ def dense_reference(params, q):
     return np.stack([od.sdpa(qf[j], k8[j // 4], v8[j // 4], ids) for j in range(16)])
 
 
-@pytest.mark.parametrize("name", list(CASES))
-def test_dense_decode_matches_oracle(name):
+def paged_records(context: int, page_tokens: int, seed: int):
+    """(pool, page table): pages for the context, handed out in a seeded
+    random order by a pool with spare pages."""
+    from seoulkv_amd import KVPagePool
+
+    need = -(-context // page_tokens)
+    pool = KVPagePool(need + 3, page_tokens=page_tokens, device="cuda:0")
+    pages = pool.allocate(pool.n_pages)
+    random.Random(seed).shuffle(pages)
+    return pool, pages[:need]
+
+
+@pytest.mark.parametrize("name,page_tokens", [(n, None) for n in CASES] +
+                         [("t8200_odd", 16), ("t40008", 64)])
+def test_dense_decode_matches_oracle(name, page_tokens):
+    """page_tokens: the FP8 records in pages of that size (16: every tile is a
+    page; the odd contexts end in a partial tile of a partial page)."""
     p = CASES[name]
     index, k, v, qs = case(**p)
-    print(f"[gpu] dense {name}", flush=True)
-    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=False)
+    print(f"[gpu] dense {name} pages {page_tokens}", flush=True)
+    kv_pages = paged_records(p["context"], page_tokens, 7) if page_tokens else None
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=False,
+                      kv_pages=kv_pages)
     try:
         for qi, q in enumerate(qs):
             rt.bind_query(q)
