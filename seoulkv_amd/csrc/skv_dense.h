@@ -15,6 +15,7 @@ constexpr int DN_BLOCK = DN_WAVES * 64;
 constexpr int DN_TILE = 16;                // keys per wave iteration (one MFMA row block)
 constexpr int DN_TARGET_BLOCKS = 64;       // partials per KV group (upper bound): one block per CU
 constexpr int DN_MERGE_SLICES = 32;        // 8-dim output slices per query head in the merge
+constexpr int DN_PAGED_MAX_TILES = 128;    // tiles per wave whose record index a paged wave holds
 
 struct DenseArgs {
   const uint8_t* kv8;   // [G][rows][512]: fp8 V | fp8 K; paged: the page pool

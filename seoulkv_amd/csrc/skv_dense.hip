@@ -228,7 +228,9 @@ __global__ __launch_bounds__(DN_BLOCK) void k_dense(DenseArgs a) {
   const int n = first < ntiles ? min(a.iters, (ntiles - first + DN_WAVES - 1) / DN_WAVES) : 0;
   auto key0 = [&](int i) { return (first + DN_WAVES * i) * DN_TILE; };
   // paged: lane i (i + 64 in the second word) holds the record index of the
-  // first key of the wave's tile i (a wave has at most 128 tiles: T <= 2^20)
+  // first key of the wave's tile i (a wave has at most DN_PAGED_MAX_TILES
+  // tiles: T <= 2^20, checked at create)
+  static_assert(DN_PAGED_MAX_TILES == 2 * WAVE, "two index words per lane");
   uint32_t prow[2] = {0u, 0u};
   if (PAGED) {
 #pragma unroll

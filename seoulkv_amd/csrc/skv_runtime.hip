@@ -466,6 +466,17 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     fail(h, SKV_EINVAL, "dense decode shape: %d blocks per group", h->dn.nb);
     return bail(SKV_EINVAL);
   }
+  {  // the paged dense kernel holds the record index of each wave's tiles in
+     // two registers: at most DN_PAGED_MAX_TILES tiles per wave at the largest
+     // context the handle can reach
+    int it = 0, nb = 0;
+    dense_shape(T + cap_app, it, nb);
+    if (pages && it > DN_PAGED_MAX_TILES) {
+      fail(h, SKV_EINVAL, "paged dense decode: %d tiles per wave (at most %d)", it,
+           DN_PAGED_MAX_TILES);
+      return bail(SKV_EINVAL);
+    }
+  }
 
   // ---- static arena
   Arena s;
