@@ -30,6 +30,46 @@ RECORD_BYTES = 512  # FP8 V (256 B) || FP8 K (256 B)
 MAX_POOL_RECORDS = 1 << 31
 
 
+class PageFreeList:
+    """First-in, first-out free list of page indices 0 .. n_pages-1 (the
+    bookkeeping of :class:`KVPagePool`, kept apart from device memory)."""
+
+    def __init__(self, n_pages: int):
+        if type(n_pages) is not int or n_pages < 1:
+            raise ValueError("n_pages must be a positive int")
+        self.n_pages = n_pages
+        self._free = deque(range(n_pages))
+        self._owned: set[int] = set()
+
+    def __len__(self) -> int:
+        return len(self._free)
+
+    def allocate(self, n: int) -> list[int]:
+        """Take ``n`` pages from the front of the list (raises when fewer are
+        free; nothing is taken then)."""
+        if type(n) is not int or n < 0:
+            raise ValueError("page count must be a non-negative int")
+        if n > len(self._free):
+            raise RuntimeError(f"page pool exhausted: {n} pages requested, "
+                               f"{len(self._free)} of {self.n_pages} free")
+        got = [self._free.popleft() for _ in range(n)]
+        self._owned.update(got)
+        return got
+
+    def release(self, pages) -> None:
+        """Return allocated pages to the end of the list (raises, returning
+        none, when one is not allocated or appears twice)."""
+        pages = [int(p) for p in pages]
+        if len(set(pages)) != len(pages):
+            raise ValueError("a page appears twice in the release")
+        for p in pages:
+            if p not in self._owned:
+                raise ValueError(f"page {p} is not allocated from this pool")
+        for p in pages:
+            self._owned.discard(p)
+            self._free.append(p)
+
+
 class KVPagePool:
     """A device pool of ``n_pages`` pages of ``page_tokens`` tokens (a power
     of two in [16, 65536]) for all 4 KV heads; pages are handed out first in,
@@ -48,15 +88,14 @@ class KVPagePool:
             raise ValueError("the page pool lives on a ROCm GPU device ('cuda' in PyTorch)")
         self.page_tokens = page_tokens
         self.n_pages = n_pages
+        self._list = PageFreeList(n_pages)
         self.pages = torch.empty((n_pages, N_KV_HEADS, page_tokens, RECORD_BYTES),
                                  dtype=torch.uint8, device=dev)
         self.device = self.pages.device
-        self._free = deque(range(n_pages))
-        self._owned: set[int] = set()
 
     @property
     def free_pages(self) -> int:
-        return len(self._free)
+        return len(self._list)
 
     def pages_for(self, tokens: int) -> int:
         """Pages that hold ``tokens`` tokens."""
@@ -64,24 +103,11 @@ class KVPagePool:
 
     def allocate(self, n: int) -> list[int]:
         """Take ``n`` pages from the free list (raises when fewer are free)."""
-        if type(n) is not int or n < 0:
-            raise ValueError("page count must be a non-negative int")
-        if n > len(self._free):
-            raise RuntimeError(f"page pool exhausted: {n} pages requested, "
-                               f"{len(self._free)} of {self.n_pages} free")
-        got = [self._free.popleft() for _ in range(n)]
-        self._owned.update(got)
-        return got
+        return self._list.allocate(n)
 
     def release(self, pages) -> None:
         """Return pages to the end of the free list."""
-        pages = [int(p) for p in pages]
-        for p in pages:
-            if p not in self._owned:
-                raise ValueError(f"page {p} is not allocated from this pool")
-        for p in pages:
-            self._owned.discard(p)
-            self._free.append(p)
+        self._list.release(pages)
 
     def gather(self, page_table, group: int, tokens: int) -> torch.Tensor:
         """The FP8 records of ``tokens`` tokens of KV head ``group`` of the
