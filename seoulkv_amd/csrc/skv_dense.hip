@@ -210,6 +210,24 @@ __global__ __launch_bounds__(DN_BLOCK) void k_dense(DenseArgs a) {
   __shared__ float s_o[DN_WAVES][H][D];
   __shared__ float s_m[DN_WAVES][H], s_l[DN_WAVES][H];
 
+  // this wave's tiles: the block sweeps its DN_WAVES x iters tiles in order,
+  // consecutive waves taking consecutive tiles
+  const int ntiles = (T + DN_TILE - 1) / DN_TILE;
+  const int first = b * DN_WAVES * a.iters + wave;
+  const int n = first < ntiles ? min(a.iters, (ntiles - first + DN_WAVES - 1) / DN_WAVES) : 0;
+  auto key0 = [&](int i) { return (first + DN_WAVES * i) * DN_TILE; };
+  // paged: lane i (i + 64 in the second word) holds the record index of the
+  // first key of the wave's tile i (a wave has at most DN_PAGED_MAX_TILES
+  // tiles: T <= 2^20, checked at create); loaded before the query is split,
+  // so the first tile loads need not wait for the table
+  static_assert(DN_PAGED_MAX_TILES == 2 * WAVE, "two index words per lane");
+  uint32_t prow[2] = {0u, 0u};
+  if (PAGED) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (lane + 64 * r < n) prow[r] = kv_row_paged(a.table, a.shift, g, key0(lane + 64 * r));
+  }
+
   v8i bq[2];
   float zc;
   dense_query(a.q + (size_t)g * H * D, lane, bq, zc);
@@ -221,22 +239,6 @@ __global__ __launch_bounds__(DN_BLOCK) void k_dense(DenseArgs a) {
     for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
   float m = -INFINITY, l = 0.f;  // running max / sum of head col / 4 over this row's keys
 
-  // this wave's tiles: the block sweeps its DN_WAVES x iters tiles in order,
-  // consecutive waves taking consecutive tiles
-  const int ntiles = (T + DN_TILE - 1) / DN_TILE;
-  const int first = b * DN_WAVES * a.iters + wave;
-  const int n = first < ntiles ? min(a.iters, (ntiles - first + DN_WAVES - 1) / DN_WAVES) : 0;
-  auto key0 = [&](int i) { return (first + DN_WAVES * i) * DN_TILE; };
-  // paged: lane i (i + 64 in the second word) holds the record index of the
-  // first key of the wave's tile i (a wave has at most DN_PAGED_MAX_TILES
-  // tiles: T <= 2^20, checked at create)
-  static_assert(DN_PAGED_MAX_TILES == 2 * WAVE, "two index words per lane");
-  uint32_t prow[2] = {0u, 0u};
-  if (PAGED) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-      if (lane + 64 * r < n) prow[r] = kv_row_paged(a.table, a.shift, g, key0(lane + 64 * r));
-  }
   auto load = [&](int i) {
     if (PAGED) {
       const uint32_t r = __builtin_amdgcn_readlane(i < 64 ? prow[0] : prow[1], i & 63);
