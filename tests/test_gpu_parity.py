@@ -209,3 +209,44 @@ def test_graph_replay_matches_eager(runtimes, name):
                 np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
     finally:
         rt.graph_mode(False)
+
+
+def degenerate_queries(q: torch.Tensor) -> dict:
+    """Queries at the edges of the fixed-point query scaling and of the
+    selections' tie handling: all zero (every score of a head ties, so every
+    cut is decided by lowest ID), one nonzero coordinate, and a real query
+    scaled by 2^-100 and 2^100 (BF16 exponents far from 0; the scores are
+    the unscaled query's up to the power of two)."""
+    z = torch.zeros(1, 1, 16, 256, dtype=torch.bfloat16)
+    one = z.clone()
+    one[..., 7] = 1.0
+    qf = q.float()
+    return {"zero": z, "onehot": one, "tiny": (qf * 2.0**-100).bfloat16(),
+            "huge": (qf * 2.0**100).bfloat16()}
+
+
+@pytest.mark.parametrize("kind", ["zero", "onehot", "tiny", "huge"])
+def test_degenerate_queries_match_the_oracle(runtimes, kind):
+    p = CASES["t8192_clustered"]
+    rt = runtime_for(runtimes, "t8192_clustered")
+    _, _, _, qs = case(**p)
+    q = degenerate_queries(qs[0])[kind]
+    print(f"[gpu] degenerate query {kind}", flush=True)
+    rt.bind_query(q)
+    rt.enqueue()
+    status = rt.synchronize()
+    assert status["err"] == [0, 0, 0, 0]
+    traces, out = oracle_step(p, q)
+    for g, tr in enumerate(traces):
+        np.testing.assert_array_equal(rt.read_stage("thresh", g), tr.thr, err_msg=f"g{g}")
+        np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected, err_msg=f"g{g}")
+        np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool, err_msg=f"g{g}")
+        np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1, err_msg=f"g{g}")
+        np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2, err_msg=f"g{g}")
+        np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100, err_msg=f"g{g}")
+    got = rt.read_output().float().numpy().reshape(16, 256)
+    assert np.isfinite(got).all()
+    for j in range(16):
+        assert np.abs(got[j] - out[j]).max() <= 2e-2, f"head {j} max-abs"
+        if np.linalg.norm(out[j]) > 0:
+            assert cosine(got[j], out[j]) >= 0.999, f"head {j} cosine"
