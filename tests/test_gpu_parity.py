@@ -24,6 +24,10 @@ CASES = {
     "t8192_clustered": dict(context=8192, components=256, nc=512, nprobe=64),
     "t8192_iid_p128": dict(context=8192, components=1, nc=512, nprobe=128, clustered=False),
     "t8192_p16_sink0": dict(context=8192, components=64, nc=256, nprobe=16, sink=0, local=64),
+    # no sink and no local window: the attention is the top-100 alone (no
+    # sink/local slice blocks, nothing to merge)
+    "t8192_no_window": dict(context=8192, components=256, nc=512, nprobe=64, sink=0, local=0,
+                            seed_shift=11),
     "t16384_nc1024_p256": dict(context=16384, components=512, nc=1024, nprobe=256, seed_shift=7),
     # sizes that are not multiples of 64: context, sink, local, centroids
     "t8200_nc160_odd": dict(context=8200, components=64, nc=160, nprobe=32, sink=40, local=200,
