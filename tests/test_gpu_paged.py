@@ -8,7 +8,8 @@ bits, the dense decode's output bits, the records read back in token order),
 the top-100 IDs must equal the oracle's, and the output must stay within the
 north-star bound of the oracle (max-abs <= 2e-2, cosine >= 0.999).  Pages of
 16 tokens put every 16-key tile and every sink/local slice across page
-boundaries; pages of 4096 hold the whole sink and local window in two pages.
+boundaries; pages of 4096 hold the whole sink and local window in two pages,
+and one page of 65536 tokens holds the whole cache.
 """
 
 from __future__ import annotations
@@ -61,7 +62,7 @@ def runtimes(page_tokens: int, seed: int, append_capacity: int = 0):
     return flat, paged, pool, table, qs
 
 
-@pytest.mark.parametrize("page_tokens", [16, 256, 4096])
+@pytest.mark.parametrize("page_tokens", [16, 32, 256, 4096, 65536])
 def test_paged_step_matches_contiguous(page_tokens):
     print(f"[gpu] paged step, {page_tokens}-token pages", flush=True)
     flat, paged, pool, table, qs = runtimes(page_tokens, seed=page_tokens)

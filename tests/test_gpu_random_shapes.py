@@ -8,15 +8,19 @@ i.i.d. keys.  It checks the status words, the selected clusters, the pool
 (encounter order), U1, U2 and the top-100 IDs bit for bit, and the
 attention output within max-abs 2e-2 / cosine 0.999 per query head.  The
 fixed shapes of ``test_gpu_parity.py`` check every intermediate score;
-these check that shapes nobody picked by hand reach the same results.
+these check that shapes nobody picked by hand reach the same results.  The
+odd seeds keep the FP8 records in pages of a random power-of-two size
+(16 .. 1024 tokens) handed out in a random order.
 """
 
 from __future__ import annotations
 
+import random
+
 import numpy as np
 import pytest
 
-from seoulkv_amd import _hip
+from seoulkv_amd import KVPagePool, _hip
 from tests.helpers import case, cosine, oracle_step
 
 pytestmark = pytest.mark.gpu
@@ -44,7 +48,17 @@ def test_random_shape_matches_the_oracle(seed):
     p = _shape(seed)
     index, k, v, qs = case(**p)
     print(f"[gpu] random shape {seed}: {p}", flush=True)
-    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    kv_pages = None
+    if seed % 2:
+        page_tokens = 16 << (seed % 7)
+        need = -(-p["context"] // page_tokens)
+        pool = KVPagePool(need + 9, page_tokens=page_tokens, device="cuda:0")
+        pages = pool.allocate(pool.n_pages)
+        random.Random(seed).shuffle(pages)
+        kv_pages = (pool, pages[:need])
+        print(f"[gpu]   paged records, {page_tokens}-token pages", flush=True)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True,
+                      kv_pages=kv_pages)
     try:
         rt.bind_query(qs[0])
         rt.enqueue()
