@@ -409,6 +409,15 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     fail(h, SKV_EHIP, "hipSetDevice(%d) failed", device);
     return bail(SKV_EHIP);
   }
+  if (pages) {  // the page pool must be device memory of this device
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, pages->pool) != hipSuccess ||
+        attr.type != hipMemoryTypeDevice || attr.device != device) {
+      (void)hipGetLastError();  // clear the query's error state
+      fail(h, SKV_EINVAL, "page pool is not device memory of device %d", device);
+      return bail(SKV_EINVAL);
+    }
+  }
   {
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=

@@ -174,3 +174,25 @@ def test_instances_share_one_pool():
         for inst in paged + flat:
             inst.close()
     assert pool.free_pages == pool.n_pages
+
+
+def test_create_paged_rejects_memory_that_is_not_a_device_pool():
+    """A page descriptor whose pool is host memory is refused at creation
+    (SKV_EINVAL), before any record is written."""
+    import ctypes
+
+    index, k, v, _ = case(**P)
+    desc, keep = _hip.index_desc(index, pool_min=0, pool_capacity=0, debug=False)
+    host = torch.empty(1 << 20, dtype=torch.uint8, pin_memory=True)
+    need = -(-P["context"] // 256)
+    table = np.arange(need, dtype=np.int32)
+    pd = _hip.KVPagesDesc(pool=host.data_ptr(), n_pages=need, page_tokens=256,
+                          page_table=table.ctypes.data, table_len=need)
+    kb = bits(k)
+    vb = bits(v)
+    handle = ctypes.c_void_p()
+    lib = _hip.load_library()
+    code = lib.skv_create_paged(ctypes.byref(desc), kb.ctypes.data, vb.ctypes.data,
+                                ctypes.byref(pd), 0, None, ctypes.byref(handle))
+    assert code == 1 and handle.value is None  # SKV_EINVAL
+    assert "device memory" in lib.skv_last_error(None).decode()
