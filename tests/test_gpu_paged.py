@@ -93,6 +93,36 @@ def test_paged_step_matches_contiguous(page_tokens):
         flat.close()
 
 
+def test_paged_graph_replay_and_selection_paths():
+    """16-token pages under graph replay (replayed several times, eager
+    steps between) and with every selection path forced (full selection only,
+    sampled cuts forced to miss): each step equals the contiguous instance's
+    eager step bit for bit."""
+    flat, paged, _, _, qs = runtimes(16, seed=5)
+    try:
+        want = [step(flat, q)[:2] for q in qs]
+        paged.graph_mode(True)
+        for rep in range(3):
+            for qi, q in enumerate(qs):
+                print(f"[gpu] paged graph replay {rep}, q{qi}", flush=True)
+                ids, out, _ = step(paged, q)
+                assert torch.equal(ids, want[qi][0]) and torch.equal(out, want[qi][1]), (rep, qi)
+            paged.graph_mode(False)
+            ids, out, _ = step(paged, qs[0])  # an eager step between replays
+            assert torch.equal(out, want[0][1]), rep
+            paged.graph_mode(True)
+        paged.graph_mode(False)
+        for mode in (1, 2, 0):
+            paged.select_mode(mode)
+            for qi, q in enumerate(qs):
+                print(f"[gpu] paged select mode {mode}, q{qi}", flush=True)
+                ids, out, _ = step(paged, q)
+                assert torch.equal(ids, want[qi][0]) and torch.equal(out, want[qi][1]), (mode, qi)
+    finally:
+        paged.close()
+        flat.close()
+
+
 def test_paged_append_matches_contiguous():
     """Host and device appends into 16-token pages (the 700-token capacity
     spans 44 pages, every append crosses page boundaries): records, steps and
