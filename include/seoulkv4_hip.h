@@ -88,7 +88,8 @@ int skv_create(const skv_index_desc *index, const uint16_t *k_bf16,
  * page_table (host, read during the call) holds ceil((context +
  * append_capacity) / page_tokens) distinct entries in [0, n_pages); the pool
  * is at most 2^31 records (n_pages x 4 x page_tokens) and must be device
- * memory of the handle's device (checked: SKV_EINVAL otherwise).  The handle
+ * memory of the handle's device whose allocation holds all n_pages pages
+ * from the pool address on (both checked: SKV_EINVAL otherwise).  The handle
  * writes only its own pages, so several handles (sequences) may share one
  * pool with disjoint tables; the pool must outlive the handle. */
 typedef struct {

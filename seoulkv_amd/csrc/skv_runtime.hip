@@ -417,6 +417,22 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
       fail(h, SKV_EINVAL, "page pool is not device memory of device %d", device);
       return bail(SKV_EINVAL);
     }
+    // ... and hold all n_pages pages inside the allocation it points into
+    void* base = nullptr;
+    size_t size = 0;
+    const uint64_t need = (uint64_t)pages->n_pages * G * pages->page_tokens * 512;
+    if (hipMemGetAddressRange(&base, &size, pages->pool) != hipSuccess) {
+      (void)hipGetLastError();
+      fail(h, SKV_EINVAL, "page pool: no device allocation found at the pool address");
+      return bail(SKV_EINVAL);
+    }
+    const uint64_t off = (uint64_t)((const char*)pages->pool - (const char*)base);
+    if (off > size || need > size - off) {
+      fail(h, SKV_EINVAL, "page pool of %lld pages needs %llu bytes; its allocation holds %llu "
+           "from the pool address", (long long)pages->n_pages, (unsigned long long)need,
+           (unsigned long long)(size - std::min<uint64_t>(off, size)));
+      return bail(SKV_EINVAL);
+    }
   }
   {
     int lds = 0;

@@ -226,3 +226,32 @@ def test_create_paged_rejects_memory_that_is_not_a_device_pool():
                                 ctypes.byref(pd), 0, None, ctypes.byref(handle))
     assert code == 1 and handle.value is None  # SKV_EINVAL
     assert "device memory" in lib.skv_last_error(None).decode()
+
+
+def test_create_paged_rejects_a_pool_smaller_than_its_page_count():
+    """A descriptor that declares more pages than the pool's allocation holds
+    (2^21 pages of 256 tokens: 1 TiB of records) is refused at creation
+    (SKV_EINVAL), before any record is written, and a correct descriptor of
+    the same pool is accepted."""
+    import ctypes
+
+    index, k, v, _ = case(**P)
+    desc, keep = _hip.index_desc(index, pool_min=0, pool_capacity=0, debug=False)
+    need = -(-P["context"] // 256)
+    pool = KVPagePool(need, page_tokens=256, device="cuda:0")
+    table = np.arange(need, dtype=np.int32)[::-1].copy()
+    kb, vb = bits(k), bits(v)
+    lib = _hip.load_library()
+    for n_pages, want in ((1 << 21, 1), (need, 0)):
+        pd = _hip.KVPagesDesc(pool=pool.pages.data_ptr(), n_pages=n_pages, page_tokens=256,
+                              page_table=table.ctypes.data, table_len=need)
+        handle = ctypes.c_void_p()
+        print(f"[gpu] paged create with {n_pages} declared pages", flush=True)
+        code = lib.skv_create_paged(ctypes.byref(desc), kb.ctypes.data, vb.ctypes.data,
+                                    ctypes.byref(pd), 0, None, ctypes.byref(handle))
+        assert code == want, lib.skv_last_error(handle).decode()
+        if want:
+            assert handle.value is None
+            assert "allocation holds" in lib.skv_last_error(None).decode()
+        else:
+            lib.skv_destroy(handle)
