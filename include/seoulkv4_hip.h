@@ -162,8 +162,10 @@ int skv_debug_ids(void *handle, uint32_t *host_out);
  * region [S, T0 - L) stay as built (T0 = the context at skv_create, L = its
  * local window).  k, v: [4][n][256] BF16, host memory (skv_append, staged
  * through a device buffer) or device memory (skv_append_device, 8-byte
- * aligned).  Enqueued on the handle's stream; fails with SKV_EINVAL, the
- * cache unchanged, when n < 1 or n exceeds the capacity left. */
+ * aligned, of the handle's device, each array inside one allocation).
+ * Enqueued on the handle's stream; fails with SKV_EINVAL, the cache
+ * unchanged, when n < 1, n exceeds the capacity left or a device array is
+ * not such memory. */
 int skv_append(void *handle, const uint16_t *k_bf16, const uint16_t *v_bf16,
                int n);
 int skv_append_device(void *handle, const void *k_dev, const void *v_dev,

@@ -316,6 +316,26 @@ void skv_destroy(void* handle) {
 
 // skv_create / skv_create_paged; pages NULL: contiguous records in the
 // handle's own memory.
+// Whether ptr is device memory of `device` whose allocation holds `bytes`
+// from ptr on (nullptr) or why not.  Runtime queries only: no allocation.
+static const char* device_range_error(const void* ptr, uint64_t bytes, int device) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess || attr.type != hipMemoryTypeDevice ||
+      attr.device != device) {
+    (void)hipGetLastError();  // clear the query's error state
+    return "is not device memory of the handle's device";
+  }
+  void* base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess) {
+    (void)hipGetLastError();
+    return "has no device allocation at its address";
+  }
+  const uint64_t off = (uint64_t)((const char*)ptr - (const char*)base);
+  if (off > size || bytes > size - off) return "extends past the end of its device allocation";
+  return nullptr;
+}
+
 static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
                        const skv_kv_pages* pages, int device, void* stream, void** handle_out) {
   if (!handle_out) return fail(nullptr, SKV_EINVAL, "handle_out is NULL");
@@ -409,28 +429,11 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     fail(h, SKV_EHIP, "hipSetDevice(%d) failed", device);
     return bail(SKV_EHIP);
   }
-  if (pages) {  // the page pool must be device memory of this device
-    hipPointerAttribute_t attr;
-    if (hipPointerGetAttributes(&attr, pages->pool) != hipSuccess ||
-        attr.type != hipMemoryTypeDevice || attr.device != device) {
-      (void)hipGetLastError();  // clear the query's error state
-      fail(h, SKV_EINVAL, "page pool is not device memory of device %d", device);
-      return bail(SKV_EINVAL);
-    }
-    // ... and hold all n_pages pages inside the allocation it points into
-    void* base = nullptr;
-    size_t size = 0;
+  if (pages) {  // device memory of this device holding all n_pages pages
     const uint64_t need = (uint64_t)pages->n_pages * G * pages->page_tokens * 512;
-    if (hipMemGetAddressRange(&base, &size, pages->pool) != hipSuccess) {
-      (void)hipGetLastError();
-      fail(h, SKV_EINVAL, "page pool: no device allocation found at the pool address");
-      return bail(SKV_EINVAL);
-    }
-    const uint64_t off = (uint64_t)((const char*)pages->pool - (const char*)base);
-    if (off > size || need > size - off) {
-      fail(h, SKV_EINVAL, "page pool of %lld pages needs %llu bytes; its allocation holds %llu "
-           "from the pool address", (long long)pages->n_pages, (unsigned long long)need,
-           (unsigned long long)(size - std::min<uint64_t>(off, size)));
+    if (const char* why = device_range_error(pages->pool, need, device)) {
+      fail(h, SKV_EINVAL, "page pool of %lld pages (%llu bytes) %s", (long long)pages->n_pages,
+           (unsigned long long)need, why);
       return bail(SKV_EINVAL);
     }
   }
@@ -899,6 +902,11 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
                 h->context0 + h->append_capacity - a.T, h->append_capacity);
   HIPCHK(h, hipSetDevice(h->device));
   if (on_device) {
+    const uint64_t bytes = (uint64_t)G * n * D * 2;
+    for (const uint16_t* src : {k, v})
+      if (const char* why = device_range_error(src, bytes, h->device))
+        return fail(h, SKV_EINVAL, "device %s of %d tokens (%llu bytes) %s", src == k ? "K" : "V",
+                    n, (unsigned long long)bytes, why);
     hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * n * (D / 4) + 255) / 256)), dim3(256),
                        0, h->stream, k, v, n, (size_t)n, a.T, a.kv_rows, (uint8_t*)a.kv8,
                        a.kv_table, a.kv_shift);

@@ -105,6 +105,13 @@ def test_append_host_and_device():
         with pytest.raises(RuntimeError, match="append"):
             rt.append(kn, vn)
         check_step(rt, q, ks, vs, "after refused append")
+        # a device append whose arrays are host memory: refused, cache unchanged
+        host = torch.empty(4 * 8 * 256 * 2, dtype=torch.uint8, pin_memory=True)
+        code = rt.lib.skv_append_device(rt.handle, host.data_ptr(), host.data_ptr(), 8)
+        assert code == 1, code  # SKV_EINVAL
+        assert "not device memory" in rt.lib.skv_last_error(rt.handle).decode()
+        assert rt.metadata()["appended"] == 558
+        check_step(rt, q, ks, vs, "after refused device append")
         # the dense comparison path covers the appended keys too
         rt.dense_decode()
         dense = rt.read_dense_output().float().numpy().reshape(16, 256).astype(np.float64)

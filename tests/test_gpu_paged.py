@@ -252,6 +252,6 @@ def test_create_paged_rejects_a_pool_smaller_than_its_page_count():
         assert code == want, lib.skv_last_error(handle).decode()
         if want:
             assert handle.value is None
-            assert "allocation holds" in lib.skv_last_error(None).decode()
+            assert "past the end of its device allocation" in lib.skv_last_error(None).decode()
         else:
             lib.skv_destroy(handle)
