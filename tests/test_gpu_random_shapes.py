@@ -10,17 +10,20 @@ attention output within max-abs 2e-2 / cosine 0.999 per query head.  The
 fixed shapes of ``test_gpu_parity.py`` check every intermediate score;
 these check that shapes nobody picked by hand reach the same results.  The
 odd seeds keep the FP8 records in pages of a random power-of-two size
-(16 .. 1024 tokens) handed out in a random order.
+(16 .. 1024 tokens) handed out in a random order.  ``SKV_RANDOM_SHAPES=N``
+runs N seeds instead of the default 10.
 """
 
 from __future__ import annotations
 
+import os
 import random
 
 import numpy as np
 import pytest
 
 from seoulkv_amd import KVPagePool, _hip
+from seoulkv_amd.index import MIN_CONTEXT
 from tests.helpers import case, cosine, oracle_step
 
 pytestmark = pytest.mark.gpu
@@ -29,7 +32,8 @@ pytestmark = pytest.mark.gpu
 def _shape(seed: int) -> dict:
     rng = np.random.default_rng(seed)
     nc = int(rng.choice([96, 160, 224, 352, 480, 608, 736, 864]))
-    context = 4 * int(rng.integers(1500, 6000))  # the index takes multiples of 4
+    # the index takes multiples of 4 from MIN_CONTEXT on
+    context = max(4 * int(rng.integers(1500, 6000)), MIN_CONTEXT)
     context += 4 if context % 64 == 0 else 0
     sink = int(rng.integers(0, 200))
     local = int(rng.integers(16, 400))
@@ -40,7 +44,8 @@ def _shape(seed: int) -> dict:
                 clustered=clustered, sink=sink, local=local, seed_shift=1000 + seed)
 
 
-SEEDS = list(range(10))
+# 10 seeds by default; SKV_RANDOM_SHAPES=N runs seeds 0 .. N-1 (a wider sweep)
+SEEDS = list(range(int(os.environ.get("SKV_RANDOM_SHAPES", "10"))))
 
 
 @pytest.mark.parametrize("seed", SEEDS)
