@@ -11,7 +11,9 @@ fixed shapes of ``test_gpu_parity.py`` check every intermediate score;
 these check that shapes nobody picked by hand reach the same results.  The
 odd seeds keep the FP8 records in pages of a random power-of-two size
 (16 .. 1024 tokens) handed out in a random order.  ``SKV_RANDOM_SHAPES=N``
-runs N seeds instead of the default 10.
+runs N seeds instead of the default 10; the long caches of
+``test_wide_random_shape_matches_the_oracle`` (1 by default,
+``SKV_RANDOM_WIDE=N``) take the paths of long centroid lists and pools.
 """
 
 from __future__ import annotations
@@ -44,15 +46,41 @@ def _shape(seed: int) -> dict:
                 clustered=clustered, sink=sink, local=local, seed_shift=1000 + seed)
 
 
+def _wide_shape(seed: int) -> dict:
+    """Long caches past the register-resident selections: more than 8192
+    centroids per head (the tile-maxima threshold path), pools of tens of
+    thousands of keys (the sampled-cut top-1600)."""
+    rng = np.random.default_rng(10_000 + seed)
+    nc = 32 * int(rng.integers(257, 513))  # 8224 .. 16384
+    context = 4 * int(rng.integers(10000, 40000))  # 40K .. 160K
+    context += 4 if context % 64 == 0 else 0
+    sink = int(rng.integers(0, 200))
+    local = int(rng.integers(16, 400))
+    nprobe = tuple(int(x) for x in rng.choice(np.arange(16, 513, 16), size=4))
+    return dict(context=context, components=int(rng.integers(512, 8192)), nc=nc, nprobe=nprobe,
+                clustered=bool(rng.integers(0, 2)), sink=sink, local=local,
+                seed_shift=5000 + seed)
+
+
 # 10 seeds by default; SKV_RANDOM_SHAPES=N runs seeds 0 .. N-1 (a wider sweep)
 SEEDS = list(range(int(os.environ.get("SKV_RANDOM_SHAPES", "10"))))
+# 1 long cache by default; SKV_RANDOM_WIDE=N runs N
+WIDE_SEEDS = list(range(int(os.environ.get("SKV_RANDOM_WIDE", "1"))))
 
 
 @pytest.mark.parametrize("seed", SEEDS)
 def test_random_shape_matches_the_oracle(seed):
-    p = _shape(seed)
+    _check(_shape(seed), seed, f"random shape {seed}")
+
+
+@pytest.mark.parametrize("seed", WIDE_SEEDS)
+def test_wide_random_shape_matches_the_oracle(seed):
+    _check(_wide_shape(seed), seed, f"wide random shape {seed}")
+
+
+def _check(p: dict, seed: int, label: str) -> None:
     index, k, v, qs = case(**p)
-    print(f"[gpu] random shape {seed}: {p}", flush=True)
+    print(f"[gpu] {label}: {p}", flush=True)
     kv_pages = None
     if seed % 2:
         page_tokens = 16 << (seed % 7)
