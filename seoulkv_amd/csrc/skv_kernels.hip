@@ -1412,6 +1412,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ SelectScratch s;
   __shared__ __align__(16) uint64_t s_key[TOPK];
+  __shared__ __align__(16) uint32_t s_pos[TOPK];  // U2 positions (atomic-order paths)
   __shared__ int s_cnt;
   __shared__ AttnScratch att;
   const int n = status[g * ST_WORDS + ST_U2];
@@ -1438,7 +1439,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
     po[r] = has ? parts[r * (D + 2) + d] : 0.f;
   }
   if (threadIdx.x == 0) s_cnt = 0;
-  bool done = false;
+  bool done = false, listed = false;  // listed: s_key is in U2 list order
   if (exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: scores and IDs in registers
     const uint4 w = load_oct(sc, n);
     uint4 t0 = make_uint4(0, 0, 0, 0), t1 = t0;
@@ -1471,7 +1472,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
         ++slot;
       }
       if (threadIdx.x == 0) s_cnt = nm;
-      done = true;
+      done = listed = true;
     }
   }
   if (!done && exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
@@ -1484,7 +1485,10 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
         if (fs_member(r, key, id)) {
           const uint32_t t = id(cand_pos(key));
           const int slot = atomicAdd(&s_cnt, 1);
-          if (slot < TOPK) s_key[slot] = ((uint64_t)cand_ord(key) << 20) | (0xfffffu - t);
+          if (slot < TOPK) {
+            s_key[slot] = ((uint64_t)cand_ord(key) << 20) | (0xfffffu - t);
+            s_pos[slot] = (uint32_t)cand_pos(key);
+          }
         }
       }
       done = true;
@@ -1503,13 +1507,30 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
       const uint32_t t = tok[i];
       if (sel.member(o, t)) {
         const int slot = atomicAdd(&s_cnt, 1);
-        if (slot < TOPK) s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
+        if (slot < TOPK) {
+          s_key[slot] = ((uint64_t)o << 20) | (0xfffffu - t);
+          s_pos[slot] = (uint32_t)i;
+        }
       }
     });
   }
   __syncthreads();
   SKV_TS(13, 7);
   const int m = min(s_cnt, TOPK);
+  if (!listed) {  // block-uniform
+    // members listed in atomic order: put them in U2 list order, as the
+    // register path lists them, so that the attention sums run in the same
+    // order on every selection path (bit-identical, reproducible outputs)
+    uint64_t key = 0;
+    int rank = 0;
+    if ((int)threadIdx.x < m) {
+      key = s_key[threadIdx.x];
+      rank = count_below(s_pos, m, s_pos[threadIdx.x]);  // positions are distinct
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < m) s_key[rank] = key;
+    __syncthreads();
+  }
   // attention over the members: wave w takes list entries w + 16 b; the
   // record loads are issued before the output list is ranked
   int tk = -1;

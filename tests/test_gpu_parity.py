@@ -142,11 +142,16 @@ def test_selection_paths_agree(runtimes, name, mode):
     forced to miss, i.e. the fallback (mode 2), and through the full path
     with the token top-k kernels' in-memory radix passes (mode 3: the path a
     pool beyond the LDS capacity takes) equals the oracle; the status bits
-    record which selections fell back."""
+    record which selections fell back.  The attention output bits equal the
+    default path's: every path attends the members in the same order."""
     p = CASES[name]
     rt = runtime_for(runtimes, name)
     _, _, _, qs = case(**p)
     print(f"[gpu] select mode {mode} {name}", flush=True)
+    rt.bind_query(qs[0])
+    rt.enqueue()
+    rt.synchronize()
+    want = rt.read_output().view(torch.int16).clone()
     rt.select_mode(mode)
     try:
         rt.bind_query(qs[0])
@@ -154,6 +159,7 @@ def test_selection_paths_agree(runtimes, name, mode):
         status = rt.synchronize()
     finally:
         rt.select_mode(0)
+    assert torch.equal(rt.read_output().view(torch.int16), want)
     traces, _ = oracle_step(p, qs[0])
     for g, tr in enumerate(traces):
         np.testing.assert_array_equal(rt.read_stage("thresh", g), tr.thr)
