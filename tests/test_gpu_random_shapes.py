@@ -8,7 +8,9 @@ i.i.d. keys.  It checks the status words, the selected clusters, the pool
 (encounter order), U1, U2 and the top-100 IDs bit for bit, and the
 attention output within max-abs 2e-2 / cosine 0.999 per query head.  The
 fixed shapes of ``test_gpu_parity.py`` check every intermediate score;
-these check that shapes nobody picked by hand reach the same results.  The
+these check that shapes nobody picked by hand reach the same results, on
+every selection path (forced full, forced-miss and radix selections give
+the oracle's IDs and the default path's output bits).  The
 odd seeds keep the FP8 records in pages of a random power-of-two size
 (16 .. 1024 tokens) handed out in a random order.  ``SKV_RANDOM_SHAPES=N``
 runs N seeds instead of the default 10; the long caches of
@@ -23,6 +25,7 @@ import random
 
 import numpy as np
 import pytest
+import torch
 
 from seoulkv_amd import KVPagePool, _hip
 from seoulkv_amd.index import MIN_CONTEXT
@@ -111,5 +114,21 @@ def _check(p: dict, seed: int, label: str) -> None:
         for j in range(16):
             assert np.abs(got[j] - out[j]).max() <= 2e-2, f"head {j} max-abs"
             assert cosine(got[j], out[j]) >= 0.999, f"head {j} cosine"
+        # every other selection path: full selections (1), sampled cuts
+        # forced to miss (2), in-memory radix passes (3) give the same IDs
+        # and the same output bits
+        want = rt.read_output().view(torch.int16).clone()
+        for mode in (1, 2, 3):
+            rt.select_mode(mode)
+            try:
+                rt.bind_query(qs[0])
+                rt.enqueue()
+                assert rt.synchronize()["err"] == [0, 0, 0, 0], mode
+            finally:
+                rt.select_mode(0)
+            for g, tr in enumerate(traces):
+                np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100,
+                                              err_msg=f"mode {mode} g{g} top100")
+            assert torch.equal(rt.read_output().view(torch.int16), want), f"mode {mode} output"
     finally:
         rt.close()
