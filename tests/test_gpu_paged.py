@@ -255,3 +255,38 @@ def test_create_paged_rejects_a_pool_smaller_than_its_page_count():
             assert "past the end of its device allocation" in lib.skv_last_error(None).decode()
         else:
             lib.skv_destroy(handle)
+
+
+def test_handles_on_concurrent_streams():
+    """Two caches (one contiguous, one paged) stepped on two streams of
+    their own, 12 steps each enqueued alternately with no host
+    synchronisation between them, so their kernels may overlap on the
+    device: every step's result equals that cache's step run alone
+    (no state is shared between handles)."""
+    inputs = [case(**P), case(**P, seed_shift=1)]
+    kw = dict(pool_min=0, pool_capacity=None, debug=True)
+    streams = [torch.cuda.Stream(device="cuda:0") for _ in range(2)]
+    need = -(-P["context"] // 64)
+    pool = scrambled_pool(need, 64, seed=11)
+    rts = [_hip.Runtime(0, inputs[0][1], inputs[0][2], inputs[0][0], stream=streams[0].cuda_stream,
+                        **kw),
+           _hip.Runtime(0, inputs[1][1], inputs[1][2], inputs[1][0], stream=streams[1].cuda_stream,
+                        kv_pages=(pool, pool.allocate(need)), **kw)]
+    try:
+        qs = [inputs[0][3], inputs[1][3]]
+        want = []
+        for i, rt in enumerate(rts):  # each alone, synchronised
+            want.append([step(rt, q)[1] for q in qs[i]])
+        print("[gpu] two handles on concurrent streams", flush=True)
+        for n in range(12):
+            for i, rt in enumerate(rts):
+                rt.bind_query(qs[i][n % 2])
+                rt.enqueue()
+            if n % 4 == 3:  # check the last steps of both
+                for i, rt in enumerate(rts):
+                    assert rt.synchronize()["err"] == [0, 0, 0, 0]
+                    got = rt.read_output().view(torch.int16)
+                    assert torch.equal(got, want[i][n % 2]), (n, i)
+    finally:
+        for rt in rts:
+            rt.close()
