@@ -314,8 +314,6 @@ void skv_destroy(void* handle) {
   delete h;
 }
 
-// skv_create / skv_create_paged; pages NULL: contiguous records in the
-// handle's own memory.
 // Whether ptr is device memory of `device` whose allocation holds `bytes`
 // from ptr on (nullptr) or why not.  Runtime queries only: no allocation.
 static const char* device_range_error(const void* ptr, uint64_t bytes, int device) {
@@ -336,6 +334,8 @@ static const char* device_range_error(const void* ptr, uint64_t bytes, int devic
   return nullptr;
 }
 
+// skv_create / skv_create_paged; pages NULL: contiguous records in the
+// handle's own memory.
 static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const uint16_t* v_bf16,
                        const skv_kv_pages* pages, int device, void* stream, void** handle_out) {
   if (!handle_out) return fail(nullptr, SKV_EINVAL, "handle_out is NULL");
