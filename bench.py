@@ -387,6 +387,7 @@ def main() -> int:
         # the dense FP8 decode over all T keys, the sparse step's comparison
         rt.dense_decode()
         dense_gpu = rt.read_dense_output().float().numpy().reshape(16, 256)
+        rt.time_dense(reps=5)  # warm-up: the first timed set runs 1-4 µs slower
         dn_kernel_ms, dn_merge_ms, dn_ms = rt.time_dense(reps=max(20, args.steps // 4))
         log(f"dense FP8 decode {dn_ms * 1e3:.1f} µs (partials {dn_kernel_ms * 1e3:.1f} µs)")
 
@@ -416,6 +417,7 @@ def main() -> int:
         prt = paged._state
         prt.dense_decode()
         paged_dense_same = bool(torch.equal(prt.read_dense_output(), rt.read_dense_output()))
+        prt.time_dense(reps=5)  # warm-up, as for the contiguous records
         _, _, paged_dn_ms = prt.time_dense(reps=max(20, args.steps // 4))
         paged.close()
         del pool
