@@ -29,7 +29,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from seoulkv_amd import KVPagePool, SeoulKV4, SeoulKV4Config, SeoulKV4Index  # noqa: E402
-from seoulkv_amd.index import build_cell, list_agreement, posting_cosine  # noqa: E402
+from seoulkv_amd.index import (  # noqa: E402
+    build_cell,
+    centroid_count,
+    list_agreement,
+    posting_cosine,
+)
 from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -172,7 +177,22 @@ def cpu_baseline(index, k, v, q, top_gpu, budget_s: float):
         "cpu_model": cpu_model(),
         "dense_fp32_us": statistics.median(dt) * 1e6,
         "dense_fp8_cast_us": statistics.median(d8) * 1e6,
-    }, match, out, dense_fp8
+    }, match, out, dense_fp8, (code8, scales, k8, v8)
+
+
+def reference_profile_check(entry, indexes, q, prefill) -> None:
+    """Top-100 IDs of the reference-profile runs against the oracle on the
+    same index (the checker of that leg; untimed)."""
+    from oracle import decode as od
+
+    code8, scales, k8, v8 = prefill
+    qb = q.view(torch.int16).numpy().view(np.uint16).reshape(16, 256)
+    for nprobe, (ix, ids) in indexes.items():
+        cells = [od.GroupCell.from_cell(c) for c in ix.cells]
+        traces, _ = od.decode_step(cells, code8, scales, k8, v8, qb, sink=ix.zones.sink,
+                                   local=ix.zones.local)
+        ref = np.stack([tr.top100 for tr in traces])
+        entry["nprobe"][str(nprobe)]["top100_match"] = float((ref == ids).mean())
 
 
 _CONFIG = {"name": "cfg2"}
@@ -180,6 +200,12 @@ _CONFIG = {"name": "cfg2"}
 
 def args_config() -> str:
     return _CONFIG["name"]
+
+
+def workload_name(config: str) -> str:
+    if config.startswith("cfg"):
+        return f"BASELINE config {config[3:]}"
+    return "the reference's default index profile (SeoulKV4Index.build defaults)"
 
 
 def calibrate_copy(mib: int) -> int:
@@ -221,13 +247,14 @@ def index_build(args) -> int:
     line."""
     p, k, v, _ = make_profile(args.config, n_queries=1)
     r0, r1 = p.sink, p.context - p.local
-    log(f"{args.config}: T={p.context}, nc={p.n_centroids}")
+    nc = p.n_centroids or centroid_count(r1 - r0)
+    log(f"{args.config}: T={p.context}, nc={nc}")
 
     def build(device: str):
         cells, t0 = [], time.time()
         for head in range(4):
             cells.append(build_cell(k[head], p=p.nprobe, lam=0.0625, seed=0, r0=r0, r1=r1,
-                                    nc=p.n_centroids, device=torch.device(device)))
+                                    nc=nc, device=torch.device(device)))
             if device != "cpu":
                 torch.cuda.synchronize()
             log(f"{device} build: cell {head} done at {time.time() - t0:.1f} s")
@@ -249,7 +276,7 @@ def index_build(args) -> int:
     print(json.dumps({
         "metric": "index build seconds (4 KV heads, one cell at a time)",
         "config": {"workload": args.config, "context": p.context,
-                   "n_centroids": p.n_centroids, "nprobe": p.nprobe},
+                   "n_centroids": nc, "nprobe": p.nprobe},
         "cpu_s": round(cpu_s, 2), "gpu_s": round(gpu_s, 2),
         "cpu_threads": torch.get_num_threads(), "host_cpus": os.cpu_count(),
         "cpu_model": cpu_model(),
@@ -259,6 +286,76 @@ def index_build(args) -> int:
     return 0
 
 
+def time_steps(inst, stream, steps: int, warmup: int) -> float:
+    """µs per step of ``steps`` back-to-back steps of an initialised instance
+    on its bound query (HIP events on ``stream``) after ``warmup``."""
+    for _ in range(warmup):
+        inst._run_bound()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        inst._run_bound()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / steps * 1e3
+
+
+def reference_profile(k, v, q, dev, stream, steps: int, warmup: int) -> dict:
+    """The reference's own 128K profile on the same cache: the index that
+    ``SeoulKV4Index.build(k, v)`` makes at its defaults (ceil(R / 128) * 32 =
+    32672 centroids per KV head, nprobe 256; reference
+    ``_index_build.py:16-19``, ``config.py:5``) run with ``SeoulKV4Config()``
+    (pool capacity 13056, ``config.py:10-22``), and the same index re-probed
+    at nprobe 384 (the README's figure, ``README.md:50``) through
+    ``SeoulKV4Index.load(path, nprobe=384)``.  Device time of back-to-back
+    steps, timed like ``value``."""
+    import tempfile
+
+    t0 = time.time()
+    index = SeoulKV4Index.build(k, v)
+    build_s = time.time() - t0
+    log(f"reference profile: default index (nc={index.n_centroids}) built in {build_s:.1f}s")
+    entry = {"n_centroids": index.n_centroids, "stage15_capacity": 13056,
+             "index_build_s": round(build_s, 2), "nprobe": {}}
+    indexes = {}
+    with tempfile.TemporaryDirectory(prefix="skv_ref128k_") as tmp:
+        path = os.path.join(tmp, "index.npz")
+        index.dump(path)
+        indexes[256] = index
+        indexes[384] = SeoulKV4Index.load(path, nprobe=384)
+    for nprobe, ix in indexes.items():
+        with SeoulKV4(device=dev, k=k, v=v, index=ix,
+                      config=SeoulKV4Config(debug=True)) as inst:
+            inst.run(q)
+            inst.synchronize()
+            status = inst._state.synchronize()
+            ids = inst.debug_snapshot()["selected_ids"].numpy()
+            us = time_steps(inst, stream, steps, warmup)
+            rt = inst._state
+            rt.profile(True)
+            for _ in range(steps):
+                inst._run_bound()
+            kernel_ms, _ = rt.profile_read()
+            rt.profile(False)
+            inst.synchronize()
+        log(f"reference profile nprobe {nprobe}: {us:.1f} µs/step, pools {status['pool']}")
+        entry["nprobe"][str(nprobe)] = {
+            "us": round(us, 2),
+            "vs_published": round(us / 518.0, 4),
+            "in_step_us": {n: round(t * 1e3, 2) for n, t in kernel_ms.items()},
+            "stage_sizes": {k_: status[k_] for k_ in ("selected", "pool", "u1", "u2")},
+            "source": "SeoulKV4Index.build(k, v)" if nprobe == 256
+                      else "SeoulKV4Index.load(path, nprobe=384)",
+        }
+        indexes[nprobe] = (ix, ids)
+    entry["note"] = ("same cache, query and timing as `value`; index and pool capacity at the "
+                     "reference's defaults (the profile of its published 518 µs/layer on a "
+                     "Tenstorrent Blackhole p150a, README.md:7); vs_published = µs / 518")
+    return entry, indexes
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,6 +363,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2", choices=sorted(PROFILES))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference-profile", action="store_true",
+                    help="skip the reference's default 128K profile leg (config 2 only)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--build-device", default="cpu")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -301,7 +400,8 @@ def main() -> int:
     t0 = time.time()
     index = SeoulKV4Index.build(k, v, sink=p.sink, local=p.local, nprobe=p.nprobe,
                                 n_centroids=p.n_centroids, build_device=args.build_device)
-    log(f"index built in {time.time() - t0:.1f}s (nc={p.n_centroids}, nprobe={p.nprobe})")
+    nc = index.n_centroids
+    log(f"index built in {time.time() - t0:.1f}s (nc={nc}, nprobe={p.nprobe})")
 
     dev = torch.device("cuda", 0)
     stream = torch.cuda.Stream(dev)
@@ -432,6 +532,11 @@ def main() -> int:
                     "the page table; device time of back-to-back steps",
         }
 
+        ref_entry, ref_indexes = None, None
+        if args.config == "cfg2" and not args.no_reference_profile:
+            ref_entry, ref_indexes = reference_profile(k, v, q, dev, stream, args.steps,
+                                                       args.warmup)
+
         # cache append (after every measurement above: it grows the local
         # window): single-token host appends, one device append, then the
         # step over the grown window
@@ -468,7 +573,7 @@ def main() -> int:
 
     gather_bytes = kv_gather_bytes(top_gpu, p)
     gather_us = alone_ms["top100_sdpa"] * 1e3
-    nbytes = kernel_bytes(status, p, p.n_centroids)
+    nbytes = kernel_bytes(status, p, nc)
     total_bytes = sum(nbytes.values())
     dominant = max(alone_ms, key=alone_ms.get)
     dom_us = alone_ms[dominant] * 1e3
@@ -486,7 +591,10 @@ def main() -> int:
     dense_err = None
     dense_bytes = G_KV * p.context * 512  # every FP8 [V || K] record once
     if not args.no_cpu_baseline:
-        cpu, match, out_ref, dense_ref = cpu_baseline(index, k, v, q, top_gpu, args.cpu_budget)
+        cpu, match, out_ref, dense_ref, prefill = cpu_baseline(index, k, v, q, top_gpu,
+                                                               args.cpu_budget)
+        if ref_entry is not None:
+            reference_profile_check(ref_entry, ref_indexes, q, prefill)
         err = np.abs(out_gpu - out_ref).max()
         cos = min(
             float(out_gpu[j] @ out_ref[j] / (np.linalg.norm(out_gpu[j]) * np.linalg.norm(out_ref[j])))
@@ -510,11 +618,11 @@ def main() -> int:
         "dtype": "int8-mfma scores / fp8-e4m3 attention",
         "data": "synthetic: seeded 4096-component Gaussian-mixture K with RoPE, N(0,1) V",
         "config": {
-            "workload": f"{args.config}: BASELINE config {args.config[3:]} (T={p.context}, 4 KV x 16 Q heads, "
-                        f"d=256, nc={p.n_centroids}, nprobe={p.nprobe}, top-100, sink "
+            "workload": f"{args.config}: {workload_name(args.config)} (T={p.context}, 4 KV x 16 Q heads, "
+                        f"d=256, nc={nc}, nprobe={p.nprobe}, top-100, sink "
                         f"{p.sink}, local {p.local}, FP8 K/V records)",
             "context": p.context,
-            "n_centroids": p.n_centroids,
+            "n_centroids": nc,
             "nprobe": p.nprobe,
             "kv_heads": 4,
             "q_heads": 16,
@@ -565,10 +673,12 @@ def main() -> int:
         "profiled_steps": n_prof,
         "stage_sizes": {k_: status[k_] for k_ in ("survivors", "selected", "pool", "u1", "u2")},
         "cpu_baseline": cpu,
+        "reference_profile": ref_entry,
         "reference_published": {
             "value": 518, "unit": "µs/layer", "hardware": "Tenstorrent Blackhole p150a",
-            "note": "reference README 128K profile at its own centroid count (~32672/head); "
-                    "not this config, so vs_baseline is null",
+            "note": "reference README 128K profile at its own centroid count (32672/head); "
+                    "measured here on that profile in reference_profile (vs_published); "
+                    "`value` is config 2 (8192 centroids/head), so vs_baseline is null",
         },
     }
     print(json.dumps(result), flush=True)

@@ -192,8 +192,11 @@ int skv_read_dense_output(void *handle, uint16_t *host_out);
  * array of 1 MiB (4 x 64 x 4 x 258 FP32) that each GPU holds until the
  * process ends, its address looked up on the first call on a device.  Every
  * call on one GPU shares that array: calls that overlap on one GPU (other
- * streams, other threads) race.  Requires 1 <= T <= 2^20 and rows >= T, else
- * SKV_EINVAL; errors are read with skv_last_error(NULL). */
+ * streams, other threads) race.  Requires 1 <= T <= 2^20, rows >= T, and
+ * kv8 (4 x rows x 512 bytes), q_dev and out_dev (8 KiB each) in device
+ * allocations of the current device that hold them, else SKV_EINVAL (runtime
+ * pointer queries, no allocation); errors are read with
+ * skv_last_error(NULL). */
 int skv_dense_decode_static(const void *kv8, int rows, int T, const void *q_dev,
                             void *out_dev, void *stream);
 

@@ -12,12 +12,21 @@ same as the reference's: the same generators and seeds, the same score-chunk
 sizes and the same reductions.  Any change here changes which centroid a key
 lands in.  Each block cites the reference lines it restates.
 
-One deliberate difference: the leaf seeds of the batched local solves are
-drawn from a CPU generator on every build device and then moved (the
-reference draws them from a generator on the build device,
-``_clustering.py:125,177``).  The CPU build, the one the golden vectors pin,
-is unchanged; a GPU build then starts from the same seeds as the CPU build,
-so the two indexes differ only where floating-point rounding on the GPU
+Two deliberate differences, both on a GPU build device only (the CPU build,
+the one the golden vectors pin, is the reference's sequence):
+
+* the leaf seeds of the batched local solves are drawn from a CPU generator
+  on every build device and then moved (the reference draws them from a
+  generator on the build device, ``_clustering.py:125,177``), so a GPU build
+  starts from the same seeds as the CPU build;
+* the centroid sums (the reference's ``index_add_`` / ``scatter_add_``,
+  ``:27,192``) are accumulated in 64-bit fixed point (``fixed_row_sums``):
+  on a GPU those float additions are atomics whose order varies from run to
+  run, integer additions give the same bits in every order, so two GPU
+  builds of the same keys are identical.  The sums are then exact to 2^-40
+  per term, at least as accurate as the CPU's sequential FP32 sums.
+
+The two indexes then differ only where floating-point rounding on the GPU
 changes an assignment.
 """
 
@@ -27,6 +36,25 @@ import torch
 
 EPS = 1e-12
 SCORE_BUDGET = 16 * 2**20  # FP32 score elements per slab (64 MiB)
+FIXED_ONE = 2.0**40  # fixed-point unit of the GPU centroid sums
+
+
+def fixed_row_sums(out_rows: int, index: torch.Tensor, src: torch.Tensor, dim: int = 0):
+    """Order-independent sums of the rows of ``src`` (|elements| <= 1, at
+    most 2^20 rows per sum) into ``out_rows`` buckets along ``dim`` by
+    ``index``: each element is rounded to a multiple of 2^-40 and summed as
+    a 64-bit integer (|sum| <= 2^60), so every summation order gives the same
+    result.  ``dim=0``: ``src`` [n, d], ``index`` [n] (``index_add_``);
+    ``dim=1``: ``src`` [b, n, d], ``index`` [b, n] (``scatter_add_``)."""
+    q = torch.round(src.double() * FIXED_ONE).long()
+    if dim == 0:
+        acc = torch.zeros(out_rows, src.shape[1], dtype=torch.long, device=src.device)
+        acc.index_add_(0, index, q)
+    else:
+        acc = torch.zeros(src.shape[0], out_rows, src.shape[2], dtype=torch.long,
+                          device=src.device)
+        acc.scatter_add_(1, index[..., None].expand(-1, -1, src.shape[2]), q)
+    return (acc.double() / FIXED_ONE).to(src.dtype)
 
 
 def score_rows(n_centroids: int) -> int:
@@ -52,7 +80,10 @@ def spherical_kmeans(x: torch.Tensor, k: int, iters: int, seed: int) -> torch.Te
         label = torch.empty(n, dtype=torch.long, device=x.device)
         for start in range(0, n, rows):
             label[start : start + rows] = (x[start : start + rows] @ cent.t()).argmax(1)
-        sums = torch.zeros_like(cent).index_add_(0, label, x)
+        if x.device.type == "cpu":
+            sums = torch.zeros_like(cent).index_add_(0, label, x)
+        else:
+            sums = fixed_row_sums(k, label, x)
         count = torch.bincount(label, minlength=k).unsqueeze(1).float()
         cent = torch.where(count > 0, sums / count.clamp_min(1), cent)
         cent = cent / cent.norm(dim=-1, keepdim=True).clamp_min(1e-9)
@@ -220,8 +251,11 @@ def hierarchical_ivf(
                 ~col_ok[:, None, :], -torch.inf
             )
             lab = score.argmax(2)
-            sums = torch.zeros_like(cf)
-            sums.scatter_add_(1, lab[..., None].expand(-1, -1, d), xb * row_ok[..., None])
+            if dev.type == "cpu":
+                sums = torch.zeros_like(cf)
+                sums.scatter_add_(1, lab[..., None].expand(-1, -1, d), xb * row_ok[..., None])
+            else:
+                sums = fixed_row_sums(max_l, lab, xb * row_ok[..., None], dim=1)
             cnt = torch.zeros(b1 - b0, max_l, dtype=keys.dtype, device=dev)
             cnt.scatter_add_(1, lab, row_ok.to(keys.dtype))
             cf = torch.where(cnt[..., None] > 0, sums / cnt[..., None].clamp_min(1), cf)
@@ -244,7 +278,8 @@ def hierarchical_ivf(
     # CSR posting lists and build statistics (:219-236)
     flat = labels.reshape(-1)
     key_of = torch.arange(n, device=dev).unsqueeze(1).expand_as(labels).reshape(-1)
-    list_order = torch.argsort(flat)
+    # a GPU sort is asked for stability outright (equal leaves keep key order)
+    list_order = torch.argsort(flat) if dev.type == "cpu" else torch.argsort(flat, stable=True)
     counts = torch.bincount(flat, minlength=n_leaves)
     offsets = torch.cat([torch.zeros(1, dtype=torch.long, device=dev), counts.cumsum(0)])
     stats = {

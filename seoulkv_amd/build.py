@@ -45,12 +45,33 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the SeoulKV4 HIP library cannot be built")
 
 
-def build(verbose: bool = False, trace: bool = False) -> Path:
+# host code only: AddressSanitizer + UndefinedBehaviorSanitizer on the CPU
+# side of the library (descriptor validation, mate and page tables, staging);
+# the device code objects are built exactly as in the product library
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=all",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-g",
+]
+
+
+def build(verbose: bool = False, trace: bool = False, sanitize_dir: Path | None = None) -> Path:
     """Compile the library; ``trace`` builds the phase-timestamp variant
-    ``libseoulkv4_hip_trace.so`` (development only) instead."""
-    lib = LIB.with_name("libseoulkv4_hip_trace.so") if trace else LIB
+    ``libseoulkv4_hip_trace.so`` (development only) instead; ``sanitize_dir``
+    builds ``libseoulkv4_hip_asan.so`` there, its host code instrumented with
+    the address and undefined-behaviour sanitizers (tests only: a program
+    that loads it must itself be linked with ``-fsanitize=address,undefined``
+    by clang, which provides the runtime)."""
+    if sanitize_dir is not None:
+        lib = Path(sanitize_dir) / "libseoulkv4_hip_asan.so"
+    else:
+        lib = LIB.with_name("libseoulkv4_hip_trace.so") if trace else LIB
     tmp = lib.with_suffix(".so.tmp")
     extra = ["-DSKV_TRACE"] if trace else []
+    if sanitize_dir is not None:
+        extra += SANITIZE_FLAGS
     cmd = [hipcc(), *FLAGS, *extra, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -47,4 +47,8 @@ void launch_dense(const DenseArgs& a, hipStream_t st, int k);
 // skv_last_error(NULL)) and returns code.
 int note_call_error(int code, const char* fmt, ...);
 
+// NULL when ptr is device memory of `device` whose allocation holds `bytes`
+// from ptr on, else the reason it is not (runtime queries; no allocation).
+const char* device_range_error(const void* ptr, uint64_t bytes, int device);
+
 }  // namespace skv

@@ -432,6 +432,18 @@ extern "C" int skv_dense_decode_static(const void* kv8, int rows, int T, const v
   float* part = device_scratch(&device, &e);
   if (!part)
     return note_call_error(SKV_EHIP, "device scratch lookup failed: %s", hipGetErrorString(e));
+  // every operand must be device memory of the current device large enough
+  // for what the kernels touch (a wrong size or a host pointer is refused
+  // here rather than faulting in a kernel)
+  const struct { const void* ptr; uint64_t bytes; const char* name; } operands[] = {
+      {kv8, (uint64_t)G * rows * 512, "records"},
+      {q_dev, 16 * D * 2, "query"},
+      {out_dev, 16 * D * 2, "output"}};
+  for (const auto& op : operands)
+    if (const char* why = device_range_error(op.ptr, op.bytes, device))
+      return note_call_error(SKV_EINVAL, "%s (%llu bytes) %s", op.name,
+                             (unsigned long long)op.bytes, why);
+  (void)hipGetLastError();  // a launch error below is this call's, not an earlier one's
   DenseArgs a{};
   a.kv8 = static_cast<const uint8_t*>(kv8);
   a.q = static_cast<const uint16_t*>(q_dev);

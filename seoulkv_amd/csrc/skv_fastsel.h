@@ -18,6 +18,8 @@
 // depends on the sample.
 #pragma once
 
+#include <cstddef>
+
 #include "skv_select.h"
 
 namespace skv {
@@ -44,15 +46,17 @@ struct FastScratch {
     uint32_t hist[4096];
     KthScratch k;
   };
-  uint64_t cand[CAND_CAP];  // ord << 40 | position
+  alignas(16) uint64_t cand[CAND_CAP];  // ord << 40 | position
   uint32_t hist4[16];
-  uint32_t tie[FS_TIE_RANK];
+  alignas(16) uint32_t tie[FS_TIE_RANK];  // read as uint4 by count_below
   int ncand;
   int maxo;
   int ntie;
   int sel[4];
   int scan[SEL_WAVES + 1];
 };
+static_assert(offsetof(FastScratch, cand) % 16 == 0, "cand is read 16 bytes at a time");
+static_assert(offsetof(FastScratch, tie) % 16 == 0, "tie is read 16 bytes at a time");
 
 // Candidate key: ordered score (bits 40..55) | position (bits 0..19); a key
 // tied at the k-th score also carries its ID (bits 20..39, flag bit 56).

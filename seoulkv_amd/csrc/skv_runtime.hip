@@ -286,6 +286,26 @@ int skv::note_call_error(int code, const char* fmt, ...) {
   return code;
 }
 
+// Whether ptr is device memory of `device` whose allocation holds `bytes`
+// from ptr on (nullptr) or why not.  Runtime queries only: no allocation.
+const char* skv::device_range_error(const void* ptr, uint64_t bytes, int device) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess || attr.type != hipMemoryTypeDevice ||
+      attr.device != device) {
+    (void)hipGetLastError();  // clear the query's error state
+    return "is not device memory of the handle's device";
+  }
+  void* base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess) {
+    (void)hipGetLastError();
+    return "has no device allocation at its address";
+  }
+  const uint64_t off = (uint64_t)((const char*)ptr - (const char*)base);
+  if (off > size || bytes > size - off) return "extends past the end of its device allocation";
+  return nullptr;
+}
+
 extern "C" {
 
 const char* skv_version(void) { return "seoulkv4-hip gfx950 1"; }
@@ -314,25 +334,6 @@ void skv_destroy(void* handle) {
   delete h;
 }
 
-// Whether ptr is device memory of `device` whose allocation holds `bytes`
-// from ptr on (nullptr) or why not.  Runtime queries only: no allocation.
-static const char* device_range_error(const void* ptr, uint64_t bytes, int device) {
-  hipPointerAttribute_t attr;
-  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess || attr.type != hipMemoryTypeDevice ||
-      attr.device != device) {
-    (void)hipGetLastError();  // clear the query's error state
-    return "is not device memory of the handle's device";
-  }
-  void* base = nullptr;
-  size_t size = 0;
-  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess) {
-    (void)hipGetLastError();
-    return "has no device allocation at its address";
-  }
-  const uint64_t off = (uint64_t)((const char*)ptr - (const char*)base);
-  if (off > size || bytes > size - off) return "extends past the end of its device allocation";
-  return nullptr;
-}
 
 // skv_create / skv_create_paged; pages NULL: contiguous records in the
 // handle's own memory.
@@ -360,7 +361,8 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     if (pt < 16 || pt > 65536 || (pt & (pt - 1)))
       return fail(nullptr, SKV_EINVAL, "page_tokens %d is not a power of two in [16, 65536]", pt);
     while ((1 << page_shift) < pt) ++page_shift;
-    if (pages->n_pages < 1 || pages->n_pages * G * (int64_t)pt > ((int64_t)1 << 31))
+    // n_pages is bounded before it is multiplied, so the product cannot wrap
+    if (pages->n_pages < 1 || pages->n_pages > ((int64_t)1 << 31) / (G * (int64_t)pt))
       return fail(nullptr, SKV_EINVAL, "page pool of %lld pages: 1 to 2^31 records",
                   (long long)pages->n_pages);
     table_len = (T + cap_app + pt - 1) / pt;

@@ -25,7 +25,7 @@ class Profile:
     name: str
     context: int
     components: int
-    n_centroids: int
+    n_centroids: int | None  # None: the index builder's default, ceil(R / 128) * 32
     nprobe: int
     sink: int = 128
     local: int = 256
@@ -36,6 +36,10 @@ PROFILES = {
     "cfg1": Profile("cfg1", 32768, 1024, 2048, 384),
     "cfg2": Profile("cfg2", 131072, 4096, 8192, 384),
     "cfg4": Profile("cfg4", 1048576, 32768, 65536, 512),
+    # the reference's own 128K profile: config 2's cache indexed by
+    # SeoulKV4Index.build(k, v) at its defaults (32672 centroids per head,
+    # nprobe 256; reference _index_build.py:16-19, config.py:5)
+    "ref128k": Profile("ref128k", 131072, 4096, None, 256),
 }
 
 

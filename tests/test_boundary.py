@@ -126,6 +126,9 @@ def test_create_paged_rejects_bad_page_descriptors_on_the_host(lib):
         (dict(page_tokens=384), "power of two"),
         (dict(n_pages=0), "pages"),
         (dict(n_pages=(1 << 21) + 1), "2^31"),
+        # products that would wrap a 64-bit record count are refused too
+        (dict(n_pages=1 << 58), "2^31"),
+        (dict(n_pages=(1 << 63) - 1), "2^31"),
         (dict(table_len=need - 1), "needs %d pages" % need),
         (dict(table=[*range(need - 1), need]), "outside"),
         (dict(table=[*range(need - 1), -1]), "outside"),

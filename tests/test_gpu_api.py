@@ -8,7 +8,8 @@ from __future__ import annotations
 
 import functools
 import random
-import types
+import tempfile
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -205,26 +206,33 @@ def test_host_runs_ahead_through_the_query_ring():
         rt.close()
 
 
+_ARCHIVES = tempfile.TemporaryDirectory(prefix="skv_index_")
+
+
 @functools.lru_cache(maxsize=2)
 def _full_size_inputs(name, clustered, n_queries):
-    """(profile, k, v, queries, index at the profile's nprobe, oracle inputs)."""
+    """(profile, k, v, queries, index at the profile's nprobe, oracle inputs,
+    path of the index dumped as NPZ)."""
     from seoulkv_amd.index import SeoulKV4Index
     from seoulkv_amd.synthetic import make_profile
 
     prof, k, v, qs = make_profile(name, clustered=clustered, n_queries=n_queries)
     index = SeoulKV4Index.build(k, v, sink=prof.sink, local=prof.local, nprobe=prof.nprobe,
                                 n_centroids=prof.n_centroids)
+    path = Path(_ARCHIVES.name) / f"{name}_{'clustered' if clustered else 'iid'}.npz"
+    index.dump(path)
     kb, vb = bits(k), bits(v)
     code8, scales = od.key_codec(kb)
     k8, v8 = od.fp8_records(kb, vb)
-    return prof, k, v, qs, index, (code8, scales, k8, v8)
+    return prof, k, v, qs, index, (code8, scales, k8, v8), path
 
 
-def _with_nprobe(index, nprobe):
-    """The same index cells probed with another nprobe (the clustering does
-    not depend on it; SeoulKV4Index.load(path, nprobe=...) does the same)."""
-    cells = tuple(dict(c, p=nprobe) for c in index.cells)
-    return types.SimpleNamespace(cells=cells, zones=index.zones)
+def _reprobed(path, nprobe):
+    """The dumped index re-probed with another nprobe by the reference's own
+    route, ``SeoulKV4Index.load(path, nprobe=...)`` (``index.py:58-72``)."""
+    index = SeoulKV4Index.load(path, nprobe=nprobe)
+    assert index.metadata()["nprobe"] == [nprobe] * 4
+    return index
 
 
 def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048, queries=(0,),
@@ -234,10 +242,10 @@ def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048, queri
     page_tokens: keep the FP8 records in pages of that size, handed out by a
     page pool in a seeded random order."""
     print(f"[gpu] {name} P={nprobe} clustered={clustered}: inputs", flush=True)
-    prof, k, v, qs, index, (code8, scales, k8, v8) = _full_size_inputs(name, clustered,
-                                                                        n_queries)
+    prof, k, v, qs, index, (code8, scales, k8, v8), path = _full_size_inputs(
+        name, clustered, n_queries)
     if nprobe is not None and nprobe != prof.nprobe:
-        index = _with_nprobe(index, nprobe)
+        index = _reprobed(path, nprobe)
     cells = [od.GroupCell.from_cell(c) for c in index.cells]
     kv_pages = None
     if page_tokens:
@@ -295,7 +303,9 @@ def test_full_size_parity_config2_paged_records():
 def test_full_size_parity_config3_nprobe_sweep(nprobe, clustered):
     """config-2 shapes over the whole nprobe sweep
     (16, 64, 128, 256, 384, 512), clustered and i.i.d. keys (the i.i.d. keys
-    give the largest pools; P = 384 clustered is configuration 2)."""
+    give the largest pools; P = 384 clustered is configuration 2).  Each
+    nprobe other than the build's comes from the dumped index through
+    ``SeoulKV4Index.load(path, nprobe=...)``."""
     _full_size_parity("cfg2", nprobe=nprobe, clustered=clustered, pool_min=0,
                       n_queries=3 if clustered else 1)
 
