@@ -36,13 +36,16 @@ namespace {
 
 thread_local std::string g_create_error;
 
+// Bump allocator over one device allocation.  A plan runs twice: first with
+// base == nullptr to size the allocation (take() then returns nullptr: no
+// arithmetic on a null pointer), then over the allocation itself.
 struct Arena {
   char* base = nullptr;
   size_t size = 0, used = 0;
   void* take(size_t bytes) {
     size_t at = (used + 255) & ~size_t(255);
     used = at + bytes;
-    return base + at;
+    return base ? base + at : nullptr;
   }
 };
 

@@ -55,3 +55,82 @@ def test_static_dense_decode_matches_handle_dense_decode():
             ref = od.sdpa(qf[j], k8[j // 4], v8[j // 4], np.arange(T))
             assert np.abs(g[j] - ref).max() <= 2e-2, (T, j)
             assert cosine(g[j], ref) >= 0.999, (T, j)
+
+
+def test_static_dense_decode_rejects_operands_it_cannot_hold():
+    """Records shorter than ``rows`` claims (2 GiB past a small tensor's
+    allocation) and a host query are refused with SKV_EINVAL by the runtime
+    pointer checks before any launch."""
+    lib = _hip.load_library()
+    dev = torch.device("cuda", 0)
+    kv = torch.zeros(4, 1024, 512, dtype=torch.uint8, device=dev)
+    qd = torch.zeros(16, 256, dtype=torch.bfloat16, device=dev)
+    out = torch.zeros(16, 256, dtype=torch.bfloat16, device=dev)
+    host_q = torch.zeros(16, 256, dtype=torch.bfloat16)
+    cases = ((kv.data_ptr(), 1 << 20, qd.data_ptr(), out.data_ptr(), "extends past"),
+             (kv.data_ptr(), 1024, host_q.data_ptr(), out.data_ptr(), "not device memory"))
+    for kv_ptr, rows, q_ptr, out_ptr, text in cases:
+        code = lib.skv_dense_decode_static(kv_ptr, rows, 1024, q_ptr, out_ptr, None)
+        assert code == 1, text
+        assert text in lib.skv_last_error(None).decode()
+    torch.cuda.synchronize()
+    assert not out.float().abs().sum().item()  # nothing ran
+
+
+CAPTURE_SCRIPT = r"""
+import sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from seoulkv_amd import _hip
+
+gen = torch.Generator().manual_seed(7)
+k = torch.randn(4, 8192, 256, generator=gen).bfloat16()
+v = torch.randn(4, 8192, 256, generator=gen).bfloat16()
+dev = torch.device("cuda", 0)
+k8 = k.float().to(torch.float8_e4m3fn).view(torch.uint8)
+v8 = v.float().to(torch.float8_e4m3fn).view(torch.uint8)
+kv = torch.cat([v8, k8], dim=-1).contiguous().to(dev)
+qs = [torch.randn(16, 256, generator=gen).bfloat16().to(dev) for _ in range(2)]
+qbuf = qs[0].clone()
+out = torch.zeros(16, 256, dtype=torch.bfloat16, device=dev)
+torch.cuda.synchronize()
+print("capturing the first call of this process", flush=True)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    _hip.dense_decode_static(kv, 8192, qbuf, out)
+replays = []
+for q in (qs[0], qs[1], qs[0]):
+    qbuf.copy_(q)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays.append(out.clone())
+eager = []
+for q in qs:
+    qbuf.copy_(q)
+    _hip.dense_decode_static(kv, 8192, qbuf, out)
+    torch.cuda.synchronize()
+    eager.append(out.clone())
+same = [torch.equal(replays[0].view(torch.int16), eager[0].view(torch.int16)),
+        torch.equal(replays[1].view(torch.int16), eager[1].view(torch.int16)),
+        torch.equal(replays[2].view(torch.int16), eager[0].view(torch.int16)),
+        not torch.equal(eager[0], eager[1])]
+print("replays equal eager:", same, flush=True)
+sys.exit(0 if all(same) else 3)
+"""
+
+
+def test_static_dense_decode_captured_on_first_call():
+    """A fresh process whose first call of the entry point happens under
+    stream capture (so the device-array lookup and the operand checks run
+    while capturing): the graph replays with a changed query, then the
+    first query again, each bit-identical to an eager call."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    print("[gpu] static dense decode captured in a fresh process", flush=True)
+    res = subprocess.run([sys.executable, "-c", CAPTURE_SCRIPT, root], capture_output=True,
+                         text=True, timeout=240)
+    assert res.returncode == 0, (res.returncode, res.stdout[-2000:], res.stderr[-4000:])
+    assert "replays equal eager: [True, True, True, True]" in res.stdout
