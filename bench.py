@@ -39,7 +39,7 @@ from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 G_KV = 4  # KV heads of the layer
-APPEND_TOKENS = 128  # tokens appended after the measured steps (cache-append check)
+APPEND_BULK = 64  # tokens of the bulk host and device appends after the measured steps
 N_COLD = 10  # independent instances the cold-cache steps rotate over
 PAGE_TOKENS = 256  # tokens per page of the paged-records measurement
 METRIC = "µs/layer decode step at T=128K (1 GPU); achieved HBM GB/s; top-100 ID match"
@@ -406,7 +406,10 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     stream = torch.cuda.Stream(dev)
     # token IDs stay below 2^20: at T = 2^20 (config 4) there is no room to append
-    n_append = min(APPEND_TOKENS, (1 << 20) - p.context)
+    # the decode loops append one token per step (host, then device), then
+    # two bulk appends; token IDs stay below 2^20, so config 4 has no room
+    loop_steps = max(args.steps, 200)
+    n_append = min(2 * loop_steps + 2 * APPEND_BULK, (1 << 20) - p.context)
     config = SeoulKV4Config(stage15_capacity=None, debug=True, append_capacity=n_append)
     with torch.cuda.stream(stream):
         attn = SeoulKV4(device=dev, k=k, v=v, index=index, config=config)
@@ -460,13 +463,19 @@ def main() -> int:
         log(f"cold-cache device time {cold_ms * 1e3:.1f} µs/step over {n_cold} steps "
             f"({N_COLD} instances)")
 
-        # host-inclusive: 8 KiB H2D query bind + enqueue per step
-        t = time.perf_counter()
-        for _ in range(args.steps):
+        # host-inclusive: 8 KiB H2D query bind + enqueue per step, host clock
+        # from the first bind to the last step's end, over at least 200 steps
+        # (a short run's start-up and final drain would weigh on each step)
+        for _ in range(args.warmup):
             attn._bind_query(q)
             attn._run_bound()
         torch.cuda.synchronize()
-        host_us = (time.perf_counter() - t) / args.steps * 1e6
+        t = time.perf_counter()
+        for _ in range(loop_steps):
+            attn._bind_query(q)
+            attn._run_bound()
+        torch.cuda.synchronize()
+        host_us = (time.perf_counter() - t) / loop_steps * 1e6
 
         # per-kernel HIP-event profile of the same steps (includes the gaps
         # between dependent kernels)
@@ -538,37 +547,96 @@ def main() -> int:
                                                        args.warmup)
 
         # cache append (after every measurement above: it grows the local
-        # window): single-token host appends, one device append, then the
-        # step over the grown window
+        # window).  A decoder's loop: each step appends the token it decoded
+        # (1 token, from the host or from the device), binds the next query
+        # and enqueues the step, with no host synchronisation; device time of
+        # `loop_steps` such iterations against the same loop without appends.
         append = None
-        if n_append >= 2:
-            half = n_append // 2
-            kn, vn = k[:, -n_append:].clone(), v[:, -n_append:].clone()
+        if n_append >= 2 * loop_steps + 2 * APPEND_BULK:
+            rt = attn._state
+            kn = k[:, -n_append:].clone()
+            vn = v[:, -n_append:].clone()
+            kd, vd = kn.to(dev), vn.to(dev)
+            torch.cuda.synchronize()
+
+            def loop(append_fn) -> tuple[float, float]:
+                """(device µs per iteration, host µs per append call)."""
+                host = 0.0
+                start.record(stream)
+                for i in range(loop_steps):
+                    if append_fn is not None:
+                        t = time.perf_counter()
+                        append_fn(i)
+                        host += time.perf_counter() - t
+                    rt.bind_query(q)
+                    rt.enqueue()
+                end.record(stream)
+                end.synchronize()
+                return start.elapsed_time(end) / loop_steps * 1e3, host / loop_steps * 1e6
+
+            loop(None)  # warm-up of the bind + step loop
+            # each append loop is bracketed by the loop without appends, since
+            # the step itself grows with the local window
+            base_us, _ = loop(None)
+            used = 0
+            host_slices = [(kn[:, i:i + 1].contiguous(), vn[:, i:i + 1].contiguous())
+                           for i in range(loop_steps)]
+
+            def host_one(i):
+                rt.append(*host_slices[i])
+
+            host_us_, host_call_us = loop(host_one)
+            used += loop_steps
+            mid_us, _ = loop(None)
+            dev_slices = [(kd[:, used + i:used + i + 1].contiguous(),
+                           vd[:, used + i:used + i + 1].contiguous()) for i in range(loop_steps)]
+            torch.cuda.synchronize()
+
+            def dev_one(i):
+                rt.append(*dev_slices[i])
+
+            dev_us_, dev_call_us = loop(dev_one)
+            used += loop_steps
+            after_us, _ = loop(None)
+            # bulk appends (wall time including the host sync)
             attn.synchronize()
             t = time.perf_counter()
-            for i in range(half):
-                attn.append(kn[:, i:i + 1], vn[:, i:i + 1])
+            attn.append(kn[:, used:used + APPEND_BULK], vn[:, used:used + APPEND_BULK])
             attn.synchronize()
-            app_host_us = (time.perf_counter() - t) / half * 1e6
-            kd, vd = kn[:, half:].to(dev), vn[:, half:].to(dev)
+            bulk_host_us = (time.perf_counter() - t) * 1e6
+            used += APPEND_BULK
             t = time.perf_counter()
-            attn.append(kd, vd)
-            app_dev_us = (time.perf_counter() - t) * 1e6
-            start.record(stream)
-            for _ in range(args.steps):
-                attn._run_bound()
-            end.record(stream)
-            end.synchronize()
-            grown_us = start.elapsed_time(end) / args.steps * 1e3
-            log(f"append: {app_host_us:.1f} µs per 1-token host append, {app_dev_us:.1f} µs for "
-                f"{n_append - half} tokens from device; step after {n_append}: {grown_us:.1f} µs")
+            attn.append(kd[:, used:used + APPEND_BULK], vd[:, used:used + APPEND_BULK])
+            attn.synchronize()
+            bulk_dev_us = (time.perf_counter() - t) * 1e6
+            used += APPEND_BULK
+            host_ref, dev_ref = (base_us + mid_us) / 2, (mid_us + after_us) / 2
+            log(f"decode loop: step {base_us:.1f} / {mid_us:.1f} / {after_us:.1f} µs (local "
+                f"window {p.local} / +{loop_steps} / +{2 * loop_steps}); with a 1-token host "
+                f"append {host_us_:.1f} µs ({host_call_us:.1f} µs host per append call), device "
+                f"append {dev_us_:.1f} µs; bulk {APPEND_BULK} tokens host {bulk_host_us:.0f} µs, "
+                f"device {bulk_dev_us:.0f} µs")
             append = {
-                "host_1token_us": round(app_host_us, 1),
-                "device_tokens": n_append - half,
-                "device_us": round(app_dev_us, 1),
-                "step_us_after": round(grown_us, 2),
-                "appended": n_append,
-                "note": "wall time incl. host sync; the step attends the grown local window",
+                "loop_steps": loop_steps,
+                "step_us": round(base_us, 2),
+                "host_1token_step_us": round(host_us_, 2),
+                "device_1token_step_us": round(dev_us_, 2),
+                "host_over_step": round(host_us_ / host_ref, 4),
+                "device_over_step": round(dev_us_ / dev_ref, 4),
+                "host_append_call_us": round(host_call_us, 1),
+                "device_append_call_us": round(dev_call_us, 1),
+                "step_us_between_loops": round(mid_us, 2),
+                "step_us_after_loops": round(after_us, 2),
+                "bulk_tokens": APPEND_BULK,
+                "bulk_host_us": round(bulk_host_us, 1),
+                "bulk_device_us": round(bulk_dev_us, 1),
+                "appended": used,
+                "note": "decode loop per iteration: append 1 token, bind the query (8 KiB "
+                        "upload; a host token rides along and the step's first kernel packs "
+                        "it), enqueue the step; device time between HIP events over "
+                        "loop_steps iterations, no host sync; *_over_step = against the mean "
+                        "of the same loop without appends just before and after (the step "
+                        "grows with the local window); bulk = wall time incl. host sync",
             }
 
     gather_bytes = kv_gather_bytes(top_gpu, p)

@@ -160,12 +160,20 @@ int skv_debug_ids(void *handle, uint32_t *host_out);
  * and the local window by n: later steps attend [0, S) + [T0 - L, T) densely
  * plus the top-100 of the prefill index, whose key codec, CSR and retrieval
  * region [S, T0 - L) stay as built (T0 = the context at skv_create, L = its
- * local window).  k, v: [4][n][256] BF16, host memory (skv_append, staged
- * through a device buffer) or device memory (skv_append_device, 8-byte
- * aligned, of the handle's device, each array inside one allocation).
- * Enqueued on the handle's stream; fails with SKV_EINVAL, the cache
- * unchanged, when n < 1, n exceeds the capacity left or a device array is
- * not such memory. */
+ * local window).  k, v: [4][n][256] BF16, host memory (skv_append) or
+ * device memory (skv_append_device, 8-byte aligned, of the handle's device,
+ * each array inside one allocation).  skv_append copies k and v before it
+ * returns.  Up to 16 host tokens wait in the pinned query staging slot of
+ * the next skv_bind_query, travel with that query's upload and are packed
+ * by the next step's first kernel (a decoder's per-token append costs the
+ * step about 1 %); any other reader of the records (the dense decode, a
+ * record readback, kernel timing, graph capture, another append) packs them
+ * first.  Longer host appends are staged through a device buffer in
+ * 1024-token rounds.  skv_append_device reads k and v on the handle's
+ * stream; the allocations it has accepted (the last 8) are remembered, and
+ * arrays inside one of them are not queried again.  Enqueued on the
+ * handle's stream; fails with SKV_EINVAL, the cache unchanged, when n < 1,
+ * n exceeds the capacity left or a device array is not such memory. */
 int skv_append(void *handle, const uint16_t *k_bf16, const uint16_t *v_bf16,
                int n);
 int skv_append_device(void *handle, const void *k_dev, const void *v_dev,

@@ -249,12 +249,12 @@ class Runtime:
             msg = self.lib.skv_last_error(None).decode()
             raise RuntimeError(f"skv_create failed ({ERRORS.get(code, code)}): {msg}")
         self.handle = handle
+        self.stream = int(stream) if stream else None  # the caller's stream (else the library's)
         self.device = int(device)
         self.nc = desc.n_centroids
         self.context = desc.context  # prefill context: key records, pool bound
         self.T = desc.context  # current context (grows with append)
         self.debug = bool(debug)
-        self._qbuf = np.zeros((16, D), dtype=np.uint16)
 
     # -------------------------------------------------------------- checks
     def _check(self, code: int, what: str) -> None:
@@ -264,9 +264,12 @@ class Runtime:
 
     # ------------------------------------------------------------ the seam
     def bind_query(self, q: torch.Tensor) -> None:
-        """Host Q [1, 1, 16, 256] BF16 -> device (async H2D, 8 KiB)."""
-        self._qbuf[...] = _np(q.reshape(16, D), np.uint16)
-        self._check(self.lib.skv_bind_query(self.handle, _ptr(self._qbuf)), "bind_query")
+        """Host Q [1, 1, 16, 256] BF16 -> device (async H2D, 8 KiB; the call
+        copies the query into a pinned staging slot before it returns)."""
+        if q.device.type != "cpu" or q.dtype != torch.bfloat16 or q.numel() != 16 * D:
+            raise ValueError("expected a CPU BF16 Q with 16 x 256 elements")
+        q = q.contiguous()
+        self._check(self.lib.skv_bind_query(self.handle, q.data_ptr()), "bind_query")
 
     def bind_query_device(self, q_dev: torch.Tensor) -> None:
         """Device-resident Q [16, 256] BF16 on this device, written by work on
@@ -327,21 +330,36 @@ class Runtime:
         return int(p.value)
 
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Append n tokens: ``k``, ``v`` [4, n, 256] BF16, CPU (staged copy)
-        or on this device (read in place).  The local window grows by n."""
+        """Append n tokens: ``k``, ``v`` [4, n, 256] BF16, CPU (staged copy;
+        up to 16 tokens ride with the next query upload and are packed by the
+        next step) or on this device (read in place on the instance's stream,
+        ordered after PyTorch's current stream).  The local window grows by n."""
         if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.shape != v.shape \
                 or k.dim() != 3 or k.shape[0] != G or k.shape[2] != D:
             raise ValueError("expected BF16 K/V [4, n, 256] of one shape")
         n = int(k.shape[1])
         if k.device.type == "cpu" and v.device.type == "cpu":
-            kb, vb = _np(k, np.uint16), _np(v, np.uint16)
-            code = self.lib.skv_append(self.handle, _ptr(kb), _ptr(vb), n)
+            k, v = k.contiguous(), v.contiguous()  # read by the call itself (staged)
+            code = self.lib.skv_append(self.handle, k.data_ptr(), v.data_ptr(), n)
         elif k.device == v.device and k.device.type == "cuda" and k.device.index == self.device:
             k, v = k.contiguous(), v.contiguous()
-            torch.cuda.synchronize(self.device)  # k/v written by torch's streams
-            code = self.lib.skv_append_device(self.handle, k.data_ptr(), v.data_ptr(), n)
-            if code == 0:  # read on the handle's stream: keep k/v alive until done
-                self._check(self.lib.skv_sync(self.handle, None), "append sync")
+            cur = torch.cuda.current_stream(k.device)
+            if self.stream is not None and cur.cuda_stream == self.stream:
+                # one stream: the pack follows k/v's producers, and the
+                # caching allocator reuses their memory only after it
+                code = self.lib.skv_append_device(self.handle, k.data_ptr(), v.data_ptr(), n)
+            elif self.stream is not None:
+                ext = torch.cuda.ExternalStream(self.stream, device=k.device)
+                ext.wait_stream(cur)
+                code = self.lib.skv_append_device(self.handle, k.data_ptr(), v.data_ptr(), n)
+                if code == 0:  # keep k/v until the instance's stream has read them
+                    k.record_stream(ext)
+                    v.record_stream(ext)
+            else:  # the library's own stream: order by waiting on the host
+                torch.cuda.synchronize(self.device)
+                code = self.lib.skv_append_device(self.handle, k.data_ptr(), v.data_ptr(), n)
+                if code == 0:
+                    self._check(self.lib.skv_sync(self.handle, None), "append sync")
         else:
             raise ValueError("K/V must both be CPU tensors or both on the runtime's device")
         self._check(code, "append")

@@ -152,6 +152,29 @@ __host__ __device__ inline uint32_t f32_to_fp8_e4m3(float f) {
   return sign | ((uint32_t)e << 3) | m;
 }
 
+// Four BF16 values (packed in w) -> four FP8 e4m3fn bytes (torch's cast).
+// The gfx950 converter (v_cvt_pk_fp8_f32, round to nearest even) gives
+// torch's byte for every finite and infinite BF16 input (checked on all
+// 65536 patterns); a NaN input becomes torch's NaN byte (sign | 0x7f).
+__device__ __forceinline__ uint32_t bf16x4_to_fp8(uint2 w) {
+  const float f0 = bf16_f32(w.x & 0xffffu), f1 = bf16_f32(w.x >> 16);
+  const float f2 = bf16_f32(w.y & 0xffffu), f3 = bf16_f32(w.y >> 16);
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(f0, f1, 0, false);
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(f2, f3, r, true);
+  uint32_t out = (uint32_t)r;
+  // BF16 NaN: exponent all ones, mantissa nonzero (rare: one test per lane)
+  const uint32_t nan_lo = ((w.x & 0x7fffu) > 0x7f80u) | (((w.x >> 16) & 0x7fffu) > 0x7f80u) << 1 |
+                          ((w.y & 0x7fffu) > 0x7f80u) << 2 | (((w.y >> 16) & 0x7fffu) > 0x7f80u) << 3;
+  if (nan_lo) {
+    const uint32_t hv[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if ((nan_lo >> e) & 1u)
+        out = (out & ~(0xffu << (8 * e))) | ((((hv[e] >> 8) & 0x80u) | 0x7fu) << (8 * e));
+  }
+  return out;
+}
+
 // ---------------------------------------------------------------- wave ops
 // Cross-lane scans and reductions on the DPP data paths (row shifts within
 // 16-lane rows, then row broadcasts 15 and 31 across rows), the wave64 scan

@@ -315,6 +315,7 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
 constexpr int FR_BLOCK = 512;   // front: one 16-centroid tile per wave
 constexpr int FR_WAVES = FR_BLOCK / WAVE;
 static_assert(FR_WAVES >= H, "front: wave w < H forms query head w");
+static_assert(APPEND_FUSE * 512 <= FR_BLOCK * 16, "front block 0 packs a folded append");
 constexpr int FR_CENTROIDS = 16 * FR_WAVES;
 constexpr int FR_MAX_BLOCKS = 128;  // front blocks per group (each loops over its tiles)
 
@@ -432,6 +433,18 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(const uint16_t* __restrict__
       q + (g * H + min((int)(threadIdx.x >> 6), H - 1)) * D + 4 * lane);
   __builtin_amdgcn_sched_barrier(0);  // keep the query load ahead of the tile's
   FrTile cur = fr_load(a, g, tile, lane);
+  // a folded host append: block 0 of the group packs 16 bytes of the new
+  // tokens' records per thread (record byte 16 t: token t / 32, V for the
+  // first 256 bytes, then K); the BF16 source is loaded now and converted
+  // after the tiles are scored.  Every thread issues the two loads (from
+  // the query when it packs nothing): a conditional load would make the
+  // compiler wait for it where the branches join, here.
+  const int app_i = (int)threadIdx.x >> 5, app_w = ((int)threadIdx.x & 31) * 16;
+  const bool app = blockIdx.x == 0 && app_i < a.app_n;
+  const size_t app_off = (app_w < D ? (size_t)G * a.app_n * D : 0) +
+                         ((size_t)g * a.app_n + app_i) * D + (app_w < D ? app_w : app_w - D);
+  const uint4* app_p = reinterpret_cast<const uint4*>(app ? a.app_src + app_off : q);
+  const uint4 app_s0 = app_p[0], app_s1 = app_p[1];
   __shared__ __align__(16) QOperand sq;
   prep_operand(a, g, QV_RAW, &sq, qw);
   SKV_TS(0, 1);
@@ -469,6 +482,16 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(const uint16_t* __restrict__
     const uint32_t* src = reinterpret_cast<const uint32_t*>(&sq);
     uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + QV_RAW]);
     for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += FR_BLOCK) dst[i] = src[i];
+  }
+  if (app) {  // the folded append's records (read from the next kernel on)
+    const int row = a.app_row + app_i;
+    uint8_t* rec = const_cast<uint8_t*>(a.kv8) +
+                   (a.kv_table ? (size_t)kv_row_paged(a.kv_table, a.kv_shift, g, row)
+                               : (size_t)g * a.kv_rows + row) * 512;
+    const uint4 w0 = app_s0, w1 = app_s1;
+    *reinterpret_cast<uint4*>(rec + app_w) =
+        make_uint4(bf16x4_to_fp8(make_uint2(w0.x, w0.y)), bf16x4_to_fp8(make_uint2(w0.z, w0.w)),
+                   bf16x4_to_fp8(make_uint2(w1.x, w1.y)), bf16x4_to_fp8(make_uint2(w1.z, w1.w)));
   }
   SKV_TSE(4);
 }

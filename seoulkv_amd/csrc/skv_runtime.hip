@@ -53,6 +53,11 @@ constexpr int APPEND_CHUNK = 1024;  // tokens per host-append staging round
 constexpr int Q_RING = 16;          // query staging slots (host run-ahead, in steps)
 constexpr int Q_MARK = 8;           // uploads per completion event of the staging ring
 
+constexpr int DEV_OK_SLOTS = 8;
+struct DevRange {
+  uintptr_t lo, hi;
+};
+
 struct Handle {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -64,8 +69,20 @@ struct Handle {
   // Q_MARK-th slot (slot % Q_MARK == Q_MARK - 1) records one: event
   // q_marked[i / Q_MARK] covers slot i's upload and the uploads before it.
   hipEvent_t q_marked[Q_RING / Q_MARK] = {};
-  uint16_t* q_host = nullptr;  // [Q_RING][16][D]
+  uint16_t* q_host = nullptr;  // [Q_RING][q_slot]: query [16][D], then a staged append
+  size_t q_slot = 16 * D;      // elements per slot: + K and V of APPEND_FUSE tokens when
+                               // the handle can append
   unsigned q_next = 0;
+  // A host append of at most APPEND_FUSE tokens waits in the next ring slot
+  // (pend_host) until the next query upload carries it to pend_dev (the
+  // device buffer after the query), and is packed by the next step's k_front
+  // or, before any other reader of the records, by k_pack_kv8.
+  int pend_n = 0, pend_row = 0;
+  bool pend_host = false;
+  uint16_t* pend_dev = nullptr;  // [2][G][pend_n][D] BF16 K then V
+  // device allocations skv_append_device has accepted (see checked_device_range)
+  DevRange dev_ok[DEV_OK_SLOTS] = {};
+  int dev_ok_n = 0, dev_ok_next = 0;
   // device-query binding on a producer stream: the handle's steps so far
   // (readers of the query buffer) and the copy on the producer stream
   hipEvent_t steps_done = nullptr, q_ready = nullptr;
@@ -214,16 +231,10 @@ __global__ void k_pack_kv8(const uint16_t* k, const uint16_t* v, int n, size_t s
     const size_t src = ((size_t)g * src_stride + t) * D + 4 * c;
     const uint2 kw = *reinterpret_cast<const uint2*>(k + src);
     const uint2 vw = *reinterpret_cast<const uint2*>(v + src);
-    auto pack = [](uint2 w) {
-      return f32_to_fp8_e4m3(bf16_f32(w.x & 0xffffu)) |
-             (f32_to_fp8_e4m3(bf16_f32(w.x >> 16)) << 8) |
-             (f32_to_fp8_e4m3(bf16_f32(w.y & 0xffffu)) << 16) |
-             (f32_to_fp8_e4m3(bf16_f32(w.y >> 16)) << 24);
-    };
     uint8_t* rec = kv8 + (table ? (size_t)kv_row_paged(table, shift, g, row0 + t)
                                 : (size_t)g * rows + row0 + t) * 512;
-    *reinterpret_cast<uint32_t*>(rec + 4 * c) = pack(vw);
-    *reinterpret_cast<uint32_t*>(rec + 256 + 4 * c) = pack(kw);
+    *reinterpret_cast<uint32_t*>(rec + 4 * c) = bf16x4_to_fp8(vw);
+    *reinterpret_cast<uint32_t*>(rec + 256 + 4 * c) = bf16x4_to_fp8(kw);
   }
 }
 
@@ -553,7 +564,8 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
   // ---- workspace arena
   Arena wk;
   auto plan_work = [&](Arena& ar) {
-    a.q = (uint16_t*)ar.take(16 * D * 2);
+    // the query, then a folded append's BF16 K and V (one upload for both)
+    a.q = (uint16_t*)ar.take((16 + (cap_app ? 2 * G * APPEND_FUSE : 0)) * D * 2);
     a.qop = (QOperand*)ar.take(sizeof(QOperand) * G * QV_COUNT);
     a.lower = (uint16_t*)ar.take((size_t)G * H * nc * 2);
     a.upper = (uint16_t*)ar.take((size_t)G * H * nc * 2);
@@ -723,7 +735,9 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     }
   }
 
-  bool ring_ok = hipHostMalloc((void**)&h->q_host, (size_t)Q_RING * 16 * D * 2,
+  h->q_slot = (size_t)(16 + (cap_app ? 2 * G * APPEND_FUSE : 0)) * D;
+  h->pend_dev = cap_app ? const_cast<uint16_t*>(a.q) + 16 * D : nullptr;
+  bool ring_ok = hipHostMalloc((void**)&h->q_host, (size_t)Q_RING * h->q_slot * 2,
                                hipHostMallocDefault) == hipSuccess;
   for (int i = 0; i < Q_RING / Q_MARK && ring_ok; ++i)
     ring_ok = hipEventCreateWithFlags(&h->q_marked[i], hipEventDisableTiming) == hipSuccess;
@@ -763,13 +777,46 @@ int skv_bind_query(void* handle, const uint16_t* q) {
   // the host waits only when it is Q_RING - Q_MARK + 1 or more steps ahead.
   HIPCHK(h, hipSetDevice(h->device));
   const unsigned slot = h->q_next % Q_RING;
-  uint16_t* stage = h->q_host + (size_t)slot * 16 * D;
+  uint16_t* stage = h->q_host + (size_t)slot * h->q_slot;
   HIPCHK(h, hipEventSynchronize(h->q_marked[slot / Q_MARK]));
   memcpy(stage, q, 16 * D * 2);
-  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, stage, 16 * D * 2, hipMemcpyHostToDevice, h->stream));
+  // a staged append in this slot travels with the query: one upload
+  const size_t bytes = (16 + (h->pend_host ? (size_t)2 * G * h->pend_n : 0)) * D * 2;
+  HIPCHK(h, hipMemcpyAsync((void*)h->a.q, stage, bytes, hipMemcpyHostToDevice, h->stream));
   if (slot % Q_MARK == Q_MARK - 1) HIPCHK(h, hipEventRecord(h->q_marked[slot / Q_MARK], h->stream));
   ++h->q_next;
+  h->pend_host = false;
   h->bound = true;
+  return SKV_OK;
+}
+
+// A staged append still in its ring slot goes up on its own (no query bind
+// came after it); the slot is used up as a bind would use it.
+static int upload_pending(Handle* h) {
+  if (!h->pend_host) return SKV_OK;
+  const unsigned slot = h->q_next % Q_RING;
+  const uint16_t* stage = h->q_host + (size_t)slot * h->q_slot + 16 * D;
+  HIPCHK(h, hipMemcpyAsync(h->pend_dev, stage, (size_t)2 * G * h->pend_n * D * 2,
+                           hipMemcpyHostToDevice, h->stream));
+  if (slot % Q_MARK == Q_MARK - 1) HIPCHK(h, hipEventRecord(h->q_marked[slot / Q_MARK], h->stream));
+  ++h->q_next;
+  h->pend_host = false;
+  return SKV_OK;
+}
+
+// Packs a pending append's records now (before a reader other than the next
+// step: the dense decode, a record readback, kernel timing, graph capture,
+// another append).
+static int flush_pending(Handle* h) {
+  if (h->pend_n == 0) return SKV_OK;
+  if (const int rc = upload_pending(h)) return rc;
+  const StepArgs& a = h->a;
+  const int n = h->pend_n;
+  hipLaunchKernelGGL(k_pack_kv8, dim3((G * n * (D / 4) + 255) / 256), dim3(256), 0, h->stream,
+                     h->pend_dev, h->pend_dev + (size_t)G * n * D, n, (size_t)n, h->pend_row,
+                     a.kv_rows, (uint8_t*)a.kv8, a.kv_table, a.kv_shift);
+  HIPCHK(h, hipGetLastError());
+  h->pend_n = 0;
   return SKV_OK;
 }
 
@@ -777,6 +824,7 @@ int skv_bind_query_device(void* handle, const void* q_dev, void* producer_stream
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
   if (!q_dev) return fail(h, SKV_EINVAL, "NULL device query");
+  if (const int rc = upload_pending(h)) return rc;
   const hipStream_t ps = static_cast<hipStream_t>(producer_stream);
   if (ps == h->stream) {
     HIPCHK(h, hipMemcpyAsync((void*)h->a.q, q_dev, 16 * D * 2, hipMemcpyDeviceToDevice, h->stream));
@@ -801,6 +849,17 @@ int skv_enqueue(void* handle) {
   if (!h) return SKV_ESTATE;
   if (!h->bound) return fail(h, SKV_ESTATE, "bind a query before enqueue");
   HIPCHK(h, hipSetDevice(h->device));
+  // a pending host append: packed by this step's k_front (eager launches),
+  // or now, before a captured step that takes no append arguments
+  if (h->use_graph) {
+    if (const int rc = flush_pending(h)) return rc;
+  } else if (h->pend_n) {
+    if (const int rc = upload_pending(h)) return rc;
+    h->a.app_src = h->pend_dev;
+    h->a.app_n = h->pend_n;
+    h->a.app_row = h->pend_row;
+    h->pend_n = 0;
+  }
   if (h->profiling) {
     if (h->prof_pending) {  // fold the previous step's events in first
       HIPCHK(h, hipEventSynchronize(h->prof_ev[N_STEP_KERNELS]));
@@ -826,6 +885,8 @@ int skv_enqueue(void* handle) {
   } else {
     launch_step(h->a, h->w, h->stream, nullptr);
   }
+  h->a.app_n = 0;  // later steps (and kernel timings) pack nothing
+  h->a.app_src = nullptr;
   HIPCHK(h, hipGetLastError());
   h->ran = true;
   return SKV_OK;
@@ -834,6 +895,7 @@ int skv_enqueue(void* handle) {
 int skv_graph_mode(void* handle, int enable) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
+  if (const int rc = flush_pending(h)) return rc;
   HIPCHK(h, hipStreamSynchronize(h->stream));
   h->use_graph = enable != 0;
   drop_graph(h);
@@ -859,6 +921,7 @@ int skv_time_kernel(void* handle, int kernel, int reps, float* mean_ms) {
   if (kernel < 0 || kernel >= N_STEP_KERNELS || reps < 1 || !mean_ms)
     return fail(h, SKV_EINVAL, "kernel %d / reps %d out of range", kernel, reps);
   if (!h->ran) return fail(h, SKV_ESTATE, "no decode step has run");
+  if (const int rc = flush_pending(h)) return rc;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   HIPCHK(h, hipEventCreate(&e0));
   HIPCHK(h, hipEventCreate(&e1));
@@ -884,6 +947,7 @@ int skv_dense_decode(void* handle) {
   if (!h) return SKV_ESTATE;
   if (!h->bound) return fail(h, SKV_ESTATE, "bind a query before the dense decode");
   HIPCHK(h, hipSetDevice(h->device));
+  if (const int rc = flush_pending(h)) return rc;
   launch_dense(h->dn, h->stream, 0);
   launch_dense(h->dn, h->stream, 1);
   HIPCHK(h, hipGetLastError());
@@ -896,6 +960,30 @@ int skv_dense_decode(void* handle) {
 // retrieval region are the prefill's).  k, v: [G][n][256] BF16, device
 // pointers when on_device, else host memory staged APPEND_CHUNK tokens at a
 // time.  Work already enqueued keeps the shape it was launched with.
+// device_range_error for the K/V of skv_append_device, remembering the
+// allocations it accepted: a range inside one of the last DEV_OK_SLOTS
+// accepted allocations is not queried again (a decoder appends from the same
+// buffers every step).
+static const char* checked_device_range(Handle* h, const void* ptr, uint64_t bytes) {
+  const uintptr_t lo = (uintptr_t)ptr;
+  for (int i = 0; i < h->dev_ok_n; ++i)
+    if (lo >= h->dev_ok[i].lo && lo < h->dev_ok[i].hi && bytes <= h->dev_ok[i].hi - lo)
+      return nullptr;
+  if (const char* why = device_range_error(ptr, bytes, h->device)) return why;
+  void* base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) == hipSuccess) {
+    DevRange& r = h->dev_ok[h->dev_ok_next];
+    r.lo = (uintptr_t)base;
+    r.hi = (uintptr_t)base + size;
+    h->dev_ok_next = (h->dev_ok_next + 1) % DEV_OK_SLOTS;
+    h->dev_ok_n = std::min(h->dev_ok_n + 1, DEV_OK_SLOTS);
+  } else {
+    (void)hipGetLastError();
+  }
+  return nullptr;
+}
+
 static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n, bool on_device) {
   if (!h) return SKV_ESTATE;
   if (!k || !v) return fail(h, SKV_EINVAL, "NULL K/V");
@@ -906,10 +994,22 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
     return fail(h, SKV_EINVAL, "append of %d tokens: %d of the capacity %d left", n,
                 h->context0 + h->append_capacity - a.T, h->append_capacity);
   HIPCHK(h, hipSetDevice(h->device));
-  if (on_device) {
+  if (const int rc = flush_pending(h)) return rc;  // appends pack in order
+  if (!on_device && n <= APPEND_FUSE && !h->use_graph) {
+    // staged in the next query ring slot; the next bind uploads it with the
+    // query and the next step's k_front packs it
+    const unsigned slot = h->q_next % Q_RING;
+    uint16_t* stage = h->q_host + (size_t)slot * h->q_slot + 16 * D;
+    HIPCHK(h, hipEventSynchronize(h->q_marked[slot / Q_MARK]));
+    memcpy(stage, k, (size_t)G * n * D * 2);
+    memcpy(stage + (size_t)G * n * D, v, (size_t)G * n * D * 2);
+    h->pend_n = n;
+    h->pend_row = a.T;
+    h->pend_host = true;
+  } else if (on_device) {
     const uint64_t bytes = (uint64_t)G * n * D * 2;
     for (const uint16_t* src : {k, v})
-      if (const char* why = device_range_error(src, bytes, h->device))
+      if (const char* why = checked_device_range(h, src, bytes))
         return fail(h, SKV_EINVAL, "device %s of %d tokens (%llu bytes) %s", src == k ? "K" : "V",
                     n, (unsigned long long)bytes, why);
     hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * n * (D / 4) + 255) / 256)), dim3(256),
@@ -1084,6 +1184,8 @@ int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t c
                    int64_t* count_out) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h || !host_out || group < 0 || group >= G || cap < 0) return SKV_EINVAL;
+  if (stage == SKV_STAGE_KV8)
+    if (const int rc = flush_pending(h)) return rc;  // a pending append's records
   HIPCHK(h, hipStreamSynchronize(h->stream));
   const StepArgs& a = h->a;
   int st[ST_WORDS];

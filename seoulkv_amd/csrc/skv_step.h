@@ -81,6 +81,11 @@ struct StepArgs {
                             // the page pool [pages][G][1 << kv_shift][512]
   const int* kv_table;      // paged records: physical page of each logical page (else NULL)
   int kv_shift;             // paged records: log2 tokens per page
+  // a small host append folded into this step: BF16 K [G][app_n][256] at
+  // app_src, V right after it; k_front packs their FP8 records at rows
+  // app_row .. app_row + app_n - 1 (app_n == 0: nothing pending)
+  const uint16_t* app_src;
+  int app_n, app_row;
   // per-step workspace
   QOperand* qop;            // [G][QV_COUNT]
   uint16_t* lower;          // [G][H][nc] ordered BF16
@@ -144,6 +149,11 @@ struct StepWork {
 constexpr int ATTN_WAVES = 16;
 constexpr size_t ATTN_SCRATCH_BYTES = (size_t)ATTN_WAVES * (2 + D) * 4;
 constexpr int DENSE_SLICE_KEYS = ATTN_WAVES * 16;
+
+// Host appends of at most this many tokens are folded into the next step
+// (staged with its query, packed by k_front): 16 tokens x 4 KV heads x 512
+// B of BF16 K and V = 64 KiB per staging slot.
+constexpr int APPEND_FUSE = 16;
 
 // member-bitmap words the top-k kernel keeps in LDS beside its scratch
 constexpr int TOPK_LDS_WORDS = 2048;

@@ -177,3 +177,156 @@ def test_host_append_over_several_staging_chunks():
             np.testing.assert_array_equal(rec[P["context"]:, :256], fp8_bytes(vb[g]))
     finally:
         rt.close()
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_loop_folds_small_host_appends_into_the_step(paged):
+    """A decoder's loop: append the decoded token from the host, bind the next
+    query, enqueue, with no host synchronisation for 12 steps (each step's
+    output copied aside on the instance's stream); every step must equal the
+    oracle's step over exactly the tokens appended before it.  Then the
+    other orders a caller may use: an append followed by a step without a
+    new bind, two appends before a step, the largest folded append (16) and
+    the smallest unfolded one (17), an append followed by the dense decode,
+    by a record readback and by a device-query bind.  FP8 records in pages
+    (a scrambled page table) take the same path through the table."""
+    from seoulkv_amd import KVPagePool
+    from seoulkv_amd.result import _DeviceArray
+
+    index, k, v, qs = case(**P)
+    st = torch.cuda.Stream()
+    kv_pages = None
+    if paged:
+        pool = KVPagePool(64, page_tokens=256, device="cuda:0")
+        pages = pool.allocate(pool.n_pages)
+        import random
+        random.Random(3).shuffle(pages)
+        kv_pages = (pool, pages[: -(-(P["context"] + CAPACITY) // 256)])
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True,
+                      append_capacity=CAPACITY, stream=st.cuda_stream, kv_pages=kv_pages)
+    try:
+        ks, vs = [], []
+        n_loop = 12
+        toks = [new_tokens(qs[i % 2], 1, seed=300 + i) for i in range(n_loop)]
+        out = torch.as_tensor(_DeviceArray(rt.output_device_ptr(), (16, 256), "<i2"),
+                              device="cuda:0")
+        got = torch.zeros((n_loop, 16, 256), dtype=torch.int16, device="cuda:0")
+        torch.cuda.synchronize()
+        print(f"[gpu] decode loop of {n_loop} host appends (paged={paged})", flush=True)
+        with torch.cuda.stream(st):
+            for i, (kn, vn) in enumerate(toks):
+                rt.append(kn, vn)
+                rt.bind_query(qs[i % 2])
+                rt.enqueue()
+                got[i].copy_(out)
+        st.synchronize()
+        got = got.cpu().view(torch.bfloat16).float().numpy()
+        for i, (kn, vn) in enumerate(toks):
+            ks.append(kn)
+            vs.append(vn)
+            _, ref, _, _ = oracle_grown(qs[i % 2], ks, vs)
+            for j in range(16):
+                assert np.abs(got[i][j] - ref[j]).max() <= 2e-2, f"loop step {i} head {j}"
+                assert cosine(got[i][j], ref[j]) >= 0.999, f"loop step {i} head {j}"
+        q = qs[0]
+        rt.bind_query(q)
+        # an append, then a step on the bound query (no new bind)
+        kn, vn = new_tokens(q, 1, seed=401)
+        rt.append(kn, vn)
+        ks.append(kn)
+        vs.append(vn)
+        rt.enqueue()
+        rt.synchronize()
+        _, ref, _, _ = oracle_grown(q, ks, vs)
+        got1 = rt.read_output().float().numpy().reshape(16, 256)
+        for j in range(16):
+            assert cosine(got1[j], ref[j]) >= 0.999, f"append without bind, head {j}"
+        # two appends before a step, the largest folded append, the smallest
+        # unfolded one
+        for step, sizes in enumerate([(3, 2), (16,), (17,)]):
+            for u, n in enumerate(sizes):
+                kn, vn = new_tokens(q, n, seed=500 + 10 * step + u)
+                rt.append(kn, vn)
+                ks.append(kn)
+                vs.append(vn)
+            check_step(rt, q, ks, vs, f"appends {sizes}")
+        # a pending append, then the dense decode over every key
+        kn, vn = new_tokens(q, 4, seed=601)
+        rt.append(kn, vn)
+        ks.append(kn)
+        vs.append(vn)
+        rt.dense_decode()
+        dense = rt.read_dense_output().float().numpy().reshape(16, 256).astype(np.float64)
+        _, _, k8, v8 = oracle_grown(q, ks, vs)
+        qf = arith.bf16_to_f32(bits(q).reshape(16, 256))
+        ids = np.arange(k8.shape[1])
+        for j in range(16):
+            ref = od.sdpa(qf[j], k8[j // 4], v8[j // 4], ids)
+            assert np.abs(dense[j] - ref).max() <= 2e-2, f"dense after append, head {j}"
+        # a pending append, then a record readback
+        kn, vn = new_tokens(q, 2, seed=602)
+        rt.append(kn, vn)
+        ks.append(kn)
+        vs.append(vn)
+        kall, vall = bits(torch.cat(ks, 1)), bits(torch.cat(vs, 1))
+        n_app = kall.shape[1]
+        for g in range(4):
+            rec = rt.read_stage("kv8", g).reshape(-1, 512)
+            assert rec.shape[0] == P["context"] + n_app
+            np.testing.assert_array_equal(rec[P["context"]:, 256:], fp8_bytes(kall[g]))
+            np.testing.assert_array_equal(rec[P["context"]:, :256], fp8_bytes(vall[g]))
+        # a pending append, then a device-query bind
+        kn, vn = new_tokens(q, 5, seed=603)
+        rt.append(kn, vn)
+        ks.append(kn)
+        vs.append(vn)
+        with torch.cuda.stream(st):
+            rt.bind_query_device(qs[1].reshape(16, 256).to("cuda:0"))
+        rt.enqueue()
+        rt.synchronize()
+        _, ref, _, _ = oracle_grown(qs[1], ks, vs)
+        got2 = rt.read_output().float().numpy().reshape(16, 256)
+        for j in range(16):
+            assert cosine(got2[j], ref[j]) >= 0.999, f"device bind after append, head {j}"
+        assert rt.metadata()["appended"] == n_app + 5
+    finally:
+        torch.cuda.synchronize()
+        rt.close()
+
+
+def test_appended_records_match_torch_cast_for_every_bf16_pattern():
+    """The FP8 e4m3fn records of appended tokens equal torch's cast for all
+    65536 BF16 bit patterns (zeros, subnormals, the 448 / 464 rounding edge,
+    infinities, every NaN), through the bulk pack kernel and through the
+    folded append that the next step's first kernel packs."""
+    index, k, v, qs = case(**P)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True,
+                      append_capacity=64 + 16)
+    try:
+        pat = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+        kn = pat.reshape(4, 64, 256)
+        vn = pat.flip(0).reshape(4, 64, 256)  # V sees every pattern too
+        print("[gpu] every BF16 pattern through the record packers", flush=True)
+        rt.append(kn, vn)  # 64 tokens: the bulk pack kernel
+        ks, vs = bits(kn), bits(vn)
+        for g in range(4):
+            rec = rt.read_stage("kv8", g).reshape(-1, 512)[P["context"]:]
+            np.testing.assert_array_equal(rec[:, 256:], fp8_bytes(ks[g]))
+            np.testing.assert_array_equal(rec[:, :256], fp8_bytes(vs[g]))
+        # 16 tokens folded into the next step (their NaN keys make the
+        # output NaN; only the records are checked)
+        sel = torch.randperm(65536, generator=torch.Generator().manual_seed(5))[:4 * 16 * 256]
+        sel[:256] = torch.arange(0x7f80, 0x7f80 + 256)  # +inf and NaNs
+        kf = pat[sel].reshape(4, 16, 256)
+        vf = pat[sel.flip(0)].reshape(4, 16, 256)
+        rt.append(kf, vf)
+        rt.bind_query(qs[0])
+        rt.enqueue()
+        rt.synchronize()
+        kb, vb = bits(kf), bits(vf)
+        for g in range(4):
+            rec = rt.read_stage("kv8", g).reshape(-1, 512)[P["context"] + 64:]
+            np.testing.assert_array_equal(rec[:, 256:], fp8_bytes(kb[g]))
+            np.testing.assert_array_equal(rec[:, :256], fp8_bytes(vb[g]))
+    finally:
+        rt.close()
