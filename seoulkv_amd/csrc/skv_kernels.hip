@@ -418,7 +418,9 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
 // waves score 16-centroid tiles x*FR_WAVES + wave and, when LOOP (more tiles
 // than one pass of the grid covers), every FR_WAVES * gridDim.x tiles after
 // it, with the next tile's loads in flight while one is scored.
-template <bool LOOP>
+// APPEND (the step folds a host append, a.app_n > 0): block 0 of each group
+// also packs the appended tokens' FP8 records.
+template <bool LOOP, bool APPEND>
 __global__ __launch_bounds__(FR_BLOCK) void k_front(const uint16_t* __restrict__ q, StepArgs a) {
   SKV_TSB(4, 0);
   SKV_TS(0, 0);
@@ -440,11 +442,15 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(const uint16_t* __restrict__
   // the query when it packs nothing): a conditional load would make the
   // compiler wait for it where the branches join, here.
   const int app_i = (int)threadIdx.x >> 5, app_w = ((int)threadIdx.x & 31) * 16;
-  const bool app = blockIdx.x == 0 && app_i < a.app_n;
+  const bool app = APPEND && blockIdx.x == 0 && app_i < a.app_n;
+  uint4 app_s0 = make_uint4(0, 0, 0, 0), app_s1 = app_s0;
   const size_t app_off = (app_w < D ? (size_t)G * a.app_n * D : 0) +
                          ((size_t)g * a.app_n + app_i) * D + (app_w < D ? app_w : app_w - D);
-  const uint4* app_p = reinterpret_cast<const uint4*>(app ? a.app_src + app_off : q);
-  const uint4 app_s0 = app_p[0], app_s1 = app_p[1];
+  if (APPEND) {
+    const uint4* app_p = reinterpret_cast<const uint4*>(app ? a.app_src + app_off : q);
+    app_s0 = app_p[0];
+    app_s1 = app_p[1];
+  }
   __shared__ __align__(16) QOperand sq;
   prep_operand(a, g, QV_RAW, &sq, qw);
   SKV_TS(0, 1);
@@ -483,7 +489,7 @@ __global__ __launch_bounds__(FR_BLOCK) void k_front(const uint16_t* __restrict__
     uint32_t* dst = reinterpret_cast<uint32_t*>(&a.qop[g * QV_COUNT + QV_RAW]);
     for (int i = threadIdx.x; i < (int)(sizeof(QOperand) / 4); i += FR_BLOCK) dst[i] = src[i];
   }
-  if (app) {  // the folded append's records (read from the next kernel on)
+  if (APPEND && app) {  // the folded append's records (read from the next kernel on)
     const int row = a.app_row + app_i;
     uint8_t* rec = const_cast<uint8_t*>(a.kv8) +
                    (a.kv_table ? (size_t)kv_row_paged(a.kv_table, a.kv_shift, g, row)
@@ -1629,12 +1635,13 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
   const int tiles_blocks = std::min((a.nc + FR_CENTROIDS - 1) / FR_CENTROIDS, FR_MAX_BLOCKS);
   const size_t bm_lds = (size_t)PL_BM_WORDS * 4;
   switch (k) {
-    case 0:
-      if (tiles_blocks * FR_CENTROIDS >= a.nc)
-        hipLaunchKernelGGL(k_front<false>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a.q, a);
-      else
-        hipLaunchKernelGGL(k_front<true>, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a.q, a);
+    case 0: {
+      const bool loop = tiles_blocks * FR_CENTROIDS < a.nc, app = a.app_n > 0;
+      const auto fn = loop ? (app ? k_front<true, true> : k_front<true, false>)
+                           : (app ? k_front<false, true> : k_front<false, false>);
+      hipLaunchKernelGGL(fn, dim3(tiles_blocks, G), dim3(FR_BLOCK), 0, st, a.q, a);
       break;
+    }
     case 1:
       hipLaunchKernelGGL(a.kv_table ? k_select<true> : k_select<false>,
                          dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
@@ -1679,7 +1686,7 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   const void* fn = nullptr;
   size_t dyn = 0;
   switch (k) {
-    case 0: fn = reinterpret_cast<const void*>(&k_front<true>); break;
+    case 0: fn = reinterpret_cast<const void*>(&k_front<true, true>); break;
     case 1:
       fn = a.kv_table ? reinterpret_cast<const void*>(&k_select<true>)
                       : reinterpret_cast<const void*>(&k_select<false>);
@@ -1701,12 +1708,15 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   const hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return e;
   size_t st = attr.sharedSizeBytes;
-  if (k == 0) {  // both front variants
-    hipFuncAttributes attr2;
-    const hipError_t e2 =
-        hipFuncGetAttributes(&attr2, reinterpret_cast<const void*>(&k_front<false>));
-    if (e2 != hipSuccess) return e2;
-    st = std::max(st, (size_t)attr2.sharedSizeBytes);
+  if (k == 0) {  // every front variant
+    for (const void* f : {reinterpret_cast<const void*>(&k_front<true, false>),
+                          reinterpret_cast<const void*>(&k_front<false, true>),
+                          reinterpret_cast<const void*>(&k_front<false, false>)}) {
+      hipFuncAttributes attr2;
+      const hipError_t e2 = hipFuncGetAttributes(&attr2, f);
+      if (e2 != hipSuccess) return e2;
+      st = std::max(st, (size_t)attr2.sharedSizeBytes);
+    }
   }
   *static_bytes = st;
   *dynamic_bytes = dyn;
