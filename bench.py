@@ -95,18 +95,62 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
     }
 
 
-def kv_gather_bytes(top_ids, p) -> int:
-    """FP8 [V || K] record bytes the sparse SDPA gathers in one step: each KV
-    group's sink and local records once (read for its 4 query heads) plus the
-    distinct top-100 tokens of its heads (a token chosen by several heads of
-    a group is one record)."""
+def kv_gather_bytes(top_ids, p) -> tuple[int, int]:
+    """FP8 [V || K] record bytes the sparse SDPA gathers in one step, as
+    (sink/local, top-100): each KV group's sink and local records once (read
+    for its 4 query heads) and the distinct top-100 tokens of its heads (a
+    token chosen by several heads of a group is one record)."""
     rec = 512
-    total = 0
+    top = 0
     for g in range(4):
         ids = np.unique(np.asarray(top_ids[g]).ravel())
-        ids = ids[ids >= 0]
-        total += (p.sink + p.local + len(ids)) * rec
-    return int(total)
+        top += int((ids >= 0).sum()) * rec
+    return 4 * (p.sink + p.local) * rec, top
+
+
+# The gather's latency bound: an 8 KB read of records nobody touched recently
+# takes one CU 0.64 us from issue to arrival (MI355X, device clock), so the
+# top-100 part (~51 KB per query-head block, 16 blocks) cannot beat ~1 TB/s
+# however it is spread: ~16 % of the HBM peak for ~0.8 MB.
+GATHER_LATENCY_CAP_FRAC = 0.16
+
+
+def gather_phases(k, v, index, q, steps: int):
+    """Record-gather phases of the sparse SDPA from the trace build of the
+    library (same kernels plus per-block device timestamps), or None when it
+    was not built.  Per step: the top-100 gather (k_top100 blocks: record
+    loads issued -> the last wave's records arrived) and the sink/local
+    gather (the attention-slice blocks of k_select, the same two points);
+    `window` = first issue to last arrival over the blocks of the part,
+    `per_block` = the blocks' mean issue -> arrival; medians over steps."""
+    from seoulkv_amd import _hip
+
+    lib = _hip.load_trace_library()
+    if lib is None:
+        return None
+    zones = index.zones
+    slices = -(-(zones.sink + zones.local) // 256)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=False, lib=lib)
+    try:
+        rt.bind_query(q)
+        for _ in range(20):
+            rt.enqueue()
+        rt.synchronize()
+        parts = {"top100": [], "sink_local": []}
+        for _ in range(steps):
+            rt.enqueue()
+            rt.synchronize()
+            bl = rt.trace_blocks().astype(np.int64)
+            for name, rows in (("top100", bl[9][:16]), ("sink_local", bl[5][16:16 + 16 * slices])):
+                issue, arrive = rows[:, 1], rows[:, 2]
+                parts[name].append(((arrive.max() - issue.min()) * 0.01,
+                                    float(np.mean(arrive - issue)) * 0.01))
+    finally:
+        rt.close()
+    return {name: {"window_us": round(statistics.median(w for w, _ in vals), 3),
+                   "per_block_us": round(statistics.median(b for _, b in vals), 3),
+                   "steps": len(vals)}
+            for name, vals in parts.items()}
 
 
 def cpu_model() -> str:
@@ -284,6 +328,42 @@ def index_build(args) -> int:
         "posting_cosine": quality,
     }), flush=True)
     return 0
+
+
+def kv_gather_entry(sl_bytes: int, top_bytes: int, phases, alone_ms: dict) -> dict:
+    """The K/V gather stage: its two parts' bytes over their own gather phase
+    (trace build) and, beside them, over the whole kernel that holds each
+    part (k_select for sink/local, k_top100 for the top-100 records)."""
+    def rate(nbytes, us):
+        if not us:
+            return None, None
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return round(gbs, 1), round(gbs / HBM_PEAK_GBS, 4)
+
+    entry = {"bytes": sl_bytes + top_bytes, "latency_cap_frac": GATHER_LATENCY_CAP_FRAC,
+             "north_star_frac": 0.5}
+    for name, nbytes, kernel in (("top100", top_bytes, "top100_sdpa"),
+                                 ("sink_local", sl_bytes, "select")):
+        part = {"bytes": nbytes, "kernel": kernel,
+                "kernel_us": round(alone_ms[kernel] * 1e3, 2)}
+        part["kernel_GB/s"], part["kernel_frac"] = rate(nbytes, part["kernel_us"])
+        if phases is not None:
+            ph = phases[name]
+            part.update(phase_us=ph["window_us"], per_block_us=ph["per_block_us"])
+            part["GB/s"], part["frac"] = rate(nbytes, ph["window_us"])
+        entry[name] = part
+    if phases is not None:
+        both = phases["top100"]["window_us"] + phases["sink_local"]["window_us"]
+        entry["phase_us"] = round(both, 3)
+        entry["GB/s"], entry["frac"] = rate(sl_bytes + top_bytes, both)
+    entry["note"] = (
+        "unique FP8 [V||K] records of each KV group: sink/local (gathered by the attention-"
+        "slice blocks of the select launch while the centroid selections run) and top-100 "
+        "(gathered by k_top100 after its selection); phase = record loads issued -> last "
+        "wave's records arrived, first block to last (trace build of the same kernels); "
+        "kernel_* = the same bytes over the whole holding kernel alone; latency_cap_frac = "
+        "the fraction a 0.64 us issue-to-arrival floor per block allows for the top-100 part")
+    return entry
 
 
 def time_steps(inst, stream, steps: int, warmup: int) -> float:
@@ -639,8 +719,8 @@ def main() -> int:
                         "grows with the local window); bulk = wall time incl. host sync",
             }
 
-    gather_bytes = kv_gather_bytes(top_gpu, p)
-    gather_us = alone_ms["top100_sdpa"] * 1e3
+    sl_bytes, top_bytes = kv_gather_bytes(top_gpu, p)
+    phases = gather_phases(k, v, index, q, steps=50)
     nbytes = kernel_bytes(status, p, nc)
     total_bytes = sum(nbytes.values())
     dominant = max(alone_ms, key=alone_ms.get)
@@ -714,17 +794,7 @@ def main() -> int:
             "bytes_per_launch": int(nbytes.get(dominant, 0)),
         },
         "kernels": per_kernel,
-        "kv_gather": {
-            "bytes": gather_bytes,
-            "kernel": "top100_sdpa",
-            "us": round(gather_us, 2),
-            "GB/s": round(gather_bytes / (gather_us * 1e-6) / 1e9, 1),
-            "frac": round(gather_bytes / (gather_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "note": "unique sink/local + top-100 FP8 records of each KV group; the "
-                    "sink/local part is gathered by extra blocks of the select launch "
-                    "while the centroid selections run, the top-100 part by k_top100 "
-                    "after its selection; time = k_top100 alone",
-        },
+        "kv_gather": kv_gather_entry(sl_bytes, top_bytes, phases, alone_ms),
         "dense_fp8": {
             "us": round(dn_ms * 1e3, 2),
             "kernel_us": round(dn_kernel_ms * 1e3, 2),

@@ -70,7 +70,10 @@ class KVPagesDesc(ctypes.Structure):
     ]
 
 
+TRACE_LIB_PATH = LIB_PATH.with_name("libseoulkv4_hip_trace.so")
+
 _lib = None
+_trace_lib = None
 
 
 def load_library() -> ctypes.CDLL:
@@ -83,7 +86,25 @@ def load_library() -> ctypes.CDLL:
             f"SeoulKV4 HIP library missing at {LIB_PATH}; build it with "
             "`python -m seoulkv_amd.build` (gfx950)"
         )
-    lib = ctypes.CDLL(str(LIB_PATH))
+    _lib = _bind(ctypes.CDLL(str(LIB_PATH)))
+    return _lib
+
+
+def load_trace_library() -> ctypes.CDLL | None:
+    """The phase-timestamp build of the same sources (``build(trace=True)``),
+    for measurements only, or None when it was not built.  A Runtime opened
+    with ``lib=`` this library runs the same kernels and records per-block
+    device timestamps, read with :meth:`Runtime.trace_blocks`."""
+    global _trace_lib
+    if _trace_lib is None and TRACE_LIB_PATH.exists():
+        lib = _bind(ctypes.CDLL(str(TRACE_LIB_PATH)))
+        lib.skv_trace_blocks.restype = ctypes.c_int32
+        lib.skv_trace_blocks.argtypes = [ctypes.c_void_p]
+        _trace_lib = lib
+    return _trace_lib
+
+
+def _bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     sig = {
         "skv_create": (i32, [ctypes.POINTER(IndexDesc), vp, vp, i32, vp, ctypes.POINTER(vp)]),
@@ -121,7 +142,6 @@ def load_library() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = lib
     return lib
 
 
@@ -212,11 +232,12 @@ class Runtime:
 
     def __init__(self, device: int, k: torch.Tensor, v: torch.Tensor, index, *,
                  pool_min: int, pool_capacity: int | None, debug: bool, stream=None,
-                 append_capacity: int = 0, kv_pages=None):
+                 append_capacity: int = 0, kv_pages=None, lib: ctypes.CDLL | None = None):
         """``kv_pages``: ``(pool, page_table)`` to keep the FP8 records in
         pages of a :class:`seoulkv_amd.paged.KVPagePool` (``skv_create_paged``);
-        ``None`` keeps them contiguous in the instance's own memory."""
-        self.lib = load_library()
+        ``None`` keeps them contiguous in the instance's own memory.  ``lib``:
+        another build of the library (the trace build); default the product."""
+        self.lib = lib or load_library()
         desc, keep = index_desc(index, pool_min=pool_min, pool_capacity=pool_capacity,
                                 debug=debug, append_capacity=append_capacity)
         kb = _np(k, np.uint16)
@@ -286,6 +307,13 @@ class Runtime:
         self._check(self.lib.skv_bind_query_device(self.handle, q_dev.data_ptr(),
                                                    ctypes.c_void_p(producer or None)),
                     "bind_query")
+
+    def trace_blocks(self) -> np.ndarray:
+        """Trace builds: the per-block device timestamps of the last step,
+        uint64 [12 kernel slots][4096 blocks][4 points] in 10 ns ticks."""
+        out = np.zeros((12, 4096, 4), dtype=np.uint64)
+        self._check(self.lib.skv_trace_blocks(_ptr(out)), "trace_blocks")
+        return out
 
     def time_kernel(self, kernel: int, reps: int = 50) -> float:
         """Mean milliseconds of step kernel ``kernel`` launched ``reps`` times

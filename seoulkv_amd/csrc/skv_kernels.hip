@@ -222,11 +222,6 @@ __device__ __forceinline__ void attend_math(const AttnLoads<KPW>& L, const float
   }
 }
 
-__device__ __forceinline__ void wave_attend(const uint8_t* __restrict__ kv, const float q[4],
-                                            int tk, float& m, float& l, float o[4]) {
-  attend_math<SDPA_WAVE_KEYS>(attend_load<SDPA_WAVE_KEYS>(kv, tk), q, m, l, o);
-}
-
 struct AttnScratch {
   float m[SEL_BLOCK / WAVE], l[SEL_BLOCK / WAVE];
   float o[SEL_BLOCK / WAVE][D];
@@ -296,7 +291,13 @@ __device__ void dense_attend(const StepArgs& a, int blk, AttnScratch& s) {
   const int i = r * DENSE_BLOCK_KEYS + wave * SDPA_WAVE_KEYS + lane;
   if (lane < SDPA_WAVE_KEYS && i < ndense) tk = i < a.sink ? i : a.T - a.local + (i - a.sink);
   float m, l, o[4];
-  wave_attend(kv_base<PAGED>(a, g), q, kv_lane_row<PAGED>(a, g, tk), m, l, o);
+  // the slice's record gather (trace builds time it: issue, then arrival)
+  const AttnLoads<SDPA_WAVE_KEYS> L =
+      attend_load<SDPA_WAVE_KEYS>(kv_base<PAGED>(a, g), kv_lane_row<PAGED>(a, g, tk));
+  SKV_TSB(5, 1);
+  SKV_WAIT(L.kw[SDPA_WAVE_KEYS - 1] ^ L.vw[SDPA_WAVE_KEYS - 1]);
+  SKV_TSW(5, 2);
+  attend_math<SDPA_WAVE_KEYS>(L, q, m, l, o);
   stash_wave(s, m, l, o);
   __syncthreads();
   if (threadIdx.x < D) {
@@ -1569,6 +1570,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
   }
   const AttnLoads<TOP_KPW> L =
       attend_load<TOP_KPW>(kv_base<PAGED>(a, g), kv_lane_row<PAGED>(a, g, tk));
+  SKV_TSB(9, 1);  // trace builds: the top-100 record gather is issued
   // the output list, best first (member keys are distinct)
   int* out = a.top + j * TOPK;
   if ((int)threadIdx.x < m) {
@@ -1578,6 +1580,8 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
     out[threadIdx.x] = -1;
   }
   SKV_TS(13, 8);
+  SKV_WAIT(L.kw[TOP_KPW - 1] ^ L.vw[TOP_KPW - 1]);  // trace builds: ... and has arrived
+  SKV_TSW(9, 2);
   float mw, lw, ow[4];
   attend_math<TOP_KPW>(L, q, mw, lw, ow);
   stash_wave(att, mw, lw, ow);

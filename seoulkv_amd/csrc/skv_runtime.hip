@@ -95,6 +95,11 @@ struct Handle {
   // cache append: tokens after the prefill context extend the local window
   int context0 = 0, append_capacity = 0;
   uint16_t* append_stage = nullptr;  // [2][G][APPEND_CHUNK][256] bf16 (host appends)
+  // pinned host staging of long host appends: two [2][G][chunk][256] BF16
+  // slots used in turn, each reused once its upload (event) has left it
+  uint16_t* append_host = nullptr;
+  hipEvent_t append_ev[2] = {};
+  unsigned append_next = 0;
   int n_centroids = 0, np_max = 0;
   int top_u1_lds_items = 0, top_u2_lds_items = 0;  // LDS-resident sizes (select modes 0-2)
   bool dense_ran = false;
@@ -342,6 +347,9 @@ void skv_destroy(void* handle) {
   drop_graph(h);
   if (h->capture_stream) (void)hipStreamDestroy(h->capture_stream);
   if (h->q_host) (void)hipHostFree(h->q_host);
+  if (h->append_host) (void)hipHostFree(h->append_host);
+  for (hipEvent_t e : h->append_ev)
+    if (e) (void)hipEventDestroy(e);
   if (h->static_mem) (void)hipFree(h->static_mem);
   if (h->work_mem) (void)hipFree(h->work_mem);
   if (h->own_stream && h->stream) (void)hipStreamDestroy(h->stream);
@@ -739,6 +747,13 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
   h->pend_dev = cap_app ? const_cast<uint16_t*>(a.q) + 16 * D : nullptr;
   bool ring_ok = hipHostMalloc((void**)&h->q_host, (size_t)Q_RING * h->q_slot * 2,
                                hipHostMallocDefault) == hipSuccess;
+  if (cap_app && ring_ok) {
+    const size_t slot = (size_t)2 * G * std::min(cap_app, APPEND_CHUNK) * D;
+    ring_ok = hipHostMalloc((void**)&h->append_host, 2 * slot * 2, hipHostMallocDefault) ==
+              hipSuccess;
+    for (hipEvent_t& e : h->append_ev)
+      ring_ok = ring_ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
+  }
   for (int i = 0; i < Q_RING / Q_MARK && ring_ok; ++i)
     ring_ok = hipEventCreateWithFlags(&h->q_marked[i], hipEventDisableTiming) == hipSuccess;
   if (!ring_ok ||
@@ -1017,17 +1032,24 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
                        a.kv_table, a.kv_shift);
     HIPCHK(h, hipGetLastError());
   } else {
+    // chunks of the caller's [G][n][D] arrays gathered into a pinned slot as
+    // [K: G][c][D] then [V: G][c][D], one upload per chunk
     const int chunk = std::min(h->append_capacity, APPEND_CHUNK);
     uint16_t* sk = h->append_stage;
-    uint16_t* sv = sk + (size_t)G * chunk * D;
     for (int t0 = 0; t0 < n; t0 += chunk) {
       const int c = std::min(chunk, n - t0);
-      for (int g = 0; g < G; ++g) {  // pageable source: the copy returns once it is staged
-        HIPCHK(h, hipMemcpyAsync(sk + (size_t)g * c * D, k + ((size_t)g * n + t0) * D,
-                                 (size_t)c * D * 2, hipMemcpyHostToDevice, h->stream));
-        HIPCHK(h, hipMemcpyAsync(sv + (size_t)g * c * D, v + ((size_t)g * n + t0) * D,
-                                 (size_t)c * D * 2, hipMemcpyHostToDevice, h->stream));
+      const unsigned slot = h->append_next++ % 2;
+      uint16_t* hk = h->append_host + (size_t)slot * 2 * G * chunk * D;
+      uint16_t* hv = hk + (size_t)G * c * D;
+      HIPCHK(h, hipEventSynchronize(h->append_ev[slot]));
+      for (int g = 0; g < G; ++g) {
+        memcpy(hk + (size_t)g * c * D, k + ((size_t)g * n + t0) * D, (size_t)c * D * 2);
+        memcpy(hv + (size_t)g * c * D, v + ((size_t)g * n + t0) * D, (size_t)c * D * 2);
       }
+      HIPCHK(h, hipMemcpyAsync(sk, hk, (size_t)2 * G * c * D * 2, hipMemcpyHostToDevice,
+                               h->stream));
+      HIPCHK(h, hipEventRecord(h->append_ev[slot], h->stream));
+      const uint16_t* sv = sk + (size_t)G * c * D;
       hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * c * (D / 4) + 255) / 256)),
                          dim3(256), 0, h->stream, sk, sv, c, (size_t)c, a.T + t0, a.kv_rows,
                          (uint8_t*)a.kv8, a.kv_table, a.kv_shift);
