@@ -436,6 +436,51 @@ def reference_profile(k, v, q, dev, stream, steps: int, warmup: int) -> dict:
     return entry, indexes
 
 
+def dense_layouts(args) -> int:
+    """Only the dense FP8 decode over one config's cache in four record
+    layouts: contiguous, and 256-token pages of a pool holding exactly the
+    pages needed or twice that, handed out in order or scrambled.  Two sets
+    of 20 back-to-back calls per layout (skv_time_dense, after a warm-up
+    set); one JSON line.  The layouts the bench's "paged" leg compares, for
+    counter runs."""
+    p, k, v, qs = make_profile(args.config, n_queries=1)
+    index = SeoulKV4Index.build(k, v, sink=p.sink, local=p.local, nprobe=p.nprobe,
+                                n_centroids=p.n_centroids)
+    from seoulkv_amd import _hip
+
+    need = -(-p.context // PAGE_TOKENS)
+    out = {}
+
+    def run(label, pages=None):
+        rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=False,
+                          kv_pages=pages)
+        try:
+            rt.bind_query(qs[0])
+            rt.enqueue()
+            rt.synchronize()
+            rt.dense_decode()
+            rt.read_dense_output()
+            rt.time_dense(reps=5)
+            sets = [rt.time_dense(reps=20) for _ in range(2)]
+        finally:
+            rt.close()
+        out[label] = [{"partials_us": round(a * 1e3, 2), "call_us": round(c * 1e3, 2)}
+                      for a, _, c in sets]
+        log(f"{label}: {out[label]}")
+
+    run("contiguous")
+    for mult in (1, 2):
+        pool = KVPagePool(mult * need, page_tokens=PAGE_TOKENS, device="cuda:0")
+        order = list(range(mult * need))
+        random.Random(5).shuffle(order)
+        run(f"pool_x{mult}_in_order", (pool, list(range(need))))
+        run(f"pool_x{mult}_scrambled", (pool, order[:need]))
+        del pool
+    print(json.dumps({"metric": "dense FP8 decode µs by record layout", "config": args.config,
+                      "page_tokens": PAGE_TOKENS, "layouts": out}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -453,6 +498,9 @@ def main() -> int:
     ap.add_argument("--index-build", action="store_true",
                     help="only time SeoulKV4Index.build on the CPU and the GPU for --config "
                          "and compare the two indexes")
+    ap.add_argument("--dense-layouts", action="store_true",
+                    help="only time the dense FP8 decode in contiguous and paged record "
+                         "layouts (for counter runs)")
     args = ap.parse_args()
     _CONFIG["name"] = args.config
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -472,6 +520,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy)
     if args.index_build:
         return index_build(args)
+    if args.dense_layouts:
+        return dense_layouts(args)
 
     t0 = time.time()
     p, k, v, qs = make_profile(args.config, n_queries=1)
