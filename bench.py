@@ -490,6 +490,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-profile", action="store_true",
                     help="skip the reference's default 128K profile leg (config 2 only)")
+    ap.add_argument("--no-append", action="store_true",
+                    help="skip the cache-append decode loops")
+    ap.add_argument("--no-gather-phases", action="store_true",
+                    help="skip the K/V gather phase timing (trace build of the library)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--build-device", default="cpu")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -682,7 +686,7 @@ def main() -> int:
         # and enqueues the step, with no host synchronisation; device time of
         # `loop_steps` such iterations against the same loop without appends.
         append = None
-        if n_append >= 2 * loop_steps + 2 * APPEND_BULK:
+        if not args.no_append and n_append >= 2 * loop_steps + 2 * APPEND_BULK:
             rt = attn._state
             kn = k[:, -n_append:].clone()
             vn = v[:, -n_append:].clone()
@@ -770,7 +774,7 @@ def main() -> int:
             }
 
     sl_bytes, top_bytes = kv_gather_bytes(top_gpu, p)
-    phases = gather_phases(k, v, index, q, steps=50)
+    phases = None if args.no_gather_phases else gather_phases(k, v, index, q, steps=50)
     nbytes = kernel_bytes(status, p, nc)
     total_bytes = sum(nbytes.values())
     dominant = max(alone_ms, key=alone_ms.get)
