@@ -1135,6 +1135,12 @@ size_t topk_dynamic_lds(int lds_items) {
 // The leading arguments repeat the fields of t that the first loads need
 // (preloaded into scalar registers at dispatch, so those loads do not wait
 // for the argument block).
+// OCT2: rows of up to 2 x OCT_ITEMS items are selected in registers too (two
+// octets per thread), which a top-1600 over pools of 8K-16K keys gains from;
+// the extra path costs the other selections some speed when it is compiled
+// into their instance, so the runtime launches it only while the pools are
+// that small (TopkArgs::regs2).  Both instances select the same members.
+template <bool OCT2>
 __global__ __launch_bounds__(SEL_BLOCK) void k_topk(const int* count_word, const uint16_t* scores,
                                                     int stride, int exact_select,
                                                     const uint16_t* tile_max, int words,
@@ -1155,6 +1161,17 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_topk(const int* count_word, const
                                                  *reinterpret_cast<FastScratch*>(dyn), ts);
     if (r.ok) {
       write_member_words(r.mine, n, bm);
+      SKV_TS(ts, 15);
+      SKV_TSE((t.count_slot == ST_POOL ? 6 : 7));
+      return;
+    }
+  } else if (OCT2 && exact_select == 0 && n <= 2 * OCT_ITEMS) {  // two octets per thread
+    const uint4 w2[2] = {load_oct(sc, n), load_oct(sc + OCT_ITEMS, n - OCT_ITEMS)};
+    const OctResult r = octn_select<2, false, false>(w2, t.k, id,
+                                                     *reinterpret_cast<FastScratch*>(dyn), ts);
+    if (r.ok) {
+      write_member_words(r.mine & 0xffu, OCT_ITEMS, bm);
+      write_member_words(r.mine >> 8, n - OCT_ITEMS, bm + OCT_ITEMS / 64);
       SKV_TS(ts, 15);
       SKV_TSE((t.count_slot == ST_POOL ? 6 : 7));
       return;
@@ -1628,7 +1645,8 @@ const char* const kKernelNames[N_STEP_KERNELS] = {
     "front", "select", "pool", "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
 
 static void launch_topk(const TopkArgs& t, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL(k_topk, dim3(G * H), dim3(SEL_BLOCK), lds, st, t.status + t.count_slot,
+  hipLaunchKernelGGL(t.regs2 ? k_topk<true> : k_topk<false>, dim3(G * H), dim3(SEL_BLOCK), lds,
+                     st, t.status + t.count_slot,
                      t.scores, t.stride, t.exact_select, t.tile_max, t.words, t);
 }
 
@@ -1697,9 +1715,9 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
       dyn = w.select_lds;
       break;
     case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)PL_BM_WORDS * 4; break;
-    case 3: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u1_lds; break;
+    case 3: fn = reinterpret_cast<const void*>(&k_topk<true>); dyn = w.top_u1_lds; break;
     case 4: fn = reinterpret_cast<const void*>(&k_union_score<4>); break;
-    case 5: fn = reinterpret_cast<const void*>(&k_topk); dyn = w.top_u2_lds; break;
+    case 5: fn = reinterpret_cast<const void*>(&k_topk<false>); dyn = w.top_u2_lds; break;
     case 6: fn = reinterpret_cast<const void*>(&k_union_score<8>); break;
     case 7:
       fn = a.kv_table ? reinterpret_cast<const void*>(&k_top100<true>)
@@ -1712,6 +1730,12 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   const hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return e;
   size_t st = attr.sharedSizeBytes;
+  if (k == 3) {  // both top-k instances
+    hipFuncAttributes attr2;
+    const hipError_t e2 = hipFuncGetAttributes(&attr2, reinterpret_cast<const void*>(&k_topk<false>));
+    if (e2 != hipSuccess) return e2;
+    st = std::max(st, (size_t)attr2.sharedSizeBytes);
+  }
   if (k == 0) {  // every front variant
     for (const void* f : {reinterpret_cast<const void*>(&k_front<true, false>),
                           reinterpret_cast<const void*>(&k_front<false, true>),

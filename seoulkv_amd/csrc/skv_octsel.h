@@ -78,13 +78,18 @@ __device__ __forceinline__ uint64_t rank_ties(uint64_t eq, int ties, int need, P
 
 struct OctResult {
   Selection sel;  // v (k-th best score), above (count scoring > v), all
-  uint32_t mine;  // member bits of this thread's 8 items (bit e = item 8t + e)
+  uint32_t mine;  // member bits of this thread's items (bit 8o + e = item e of octet o)
   bool ok;        // false: too many ties at v to rank here (use the full path)
 };
 
-template <bool VALUE_ONLY, bool POS_IDS, typename IdFn>
-__device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s,
-                                                int ts = -1) {
+// NO octets per thread: octet o of thread t holds items 8 (t + o SEL_BLOCK) ..
+// +7 (NO = 2: the row's first 8 SEL_BLOCK items, then the rest, in the same
+// layout).  POS_IDS ranks ties by a block scan in thread order, which is
+// position order only for one octet per thread.
+template <int NO, bool VALUE_ONLY, bool POS_IDS, typename IdFn>
+__device__ __forceinline__ OctResult octn_select(const uint4 (&w)[NO], int k, IdFn id,
+                                                 FastScratch& s, int ts = -1) {
+  static_assert(NO >= 1 && NO <= 4 && !(POS_IDS && NO > 1), "octets per thread");
   OctResult res;
   res.ok = true;
   res.mine = 0;
@@ -92,7 +97,9 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
   res.sel.idcut = 0xffffffffu;
   res.sel.above = 0;
   res.sel.all = false;
-  const u32x4 wv = {w.x, w.y, w.z, w.w};
+  u32x4 wv[NO];
+#pragma unroll
+  for (int o = 0; o < NO; ++o) wv[o] = u32x4{w[o].x, w[o].y, w[o].z, w[o].w};
   for (int i = threadIdx.x; i < 4096; i += SEL_BLOCK) s.hist[i] = 0;
   if (threadIdx.x < 16) s.hist4[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
@@ -103,13 +110,15 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
   __syncthreads();
   uint32_t valid = 0;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t o = oct_half(wv, e);
-    if (o) {
-      atomicAdd(&s.hist[o >> 4], 1u);
-      valid |= 1u << e;
+  for (int o = 0; o < NO; ++o)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t x = oct_half(wv[o], e);
+      if (x) {
+        atomicAdd(&s.hist[x >> 4], 1u);
+        valid |= 1u << (8 * o + e);
+      }
     }
-  }
   __syncthreads();
   SKV_TS(ts, 1);
   fs_rank_bin(s, k);
@@ -126,10 +135,12 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
     return res;
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t o = oct_half(wv, e);
-    if (o && (int)(o >> 4) == b1) atomicAdd(&s.hist4[o & 15], 1u);
-  }
+  for (int o = 0; o < NO; ++o)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t x = oct_half(wv[o], e);
+      if (x && (int)(x >> 4) == b1) atomicAdd(&s.hist4[x & 15], 1u);
+    }
   __syncthreads();
   fs_rank_digit(s, k, acc1);
   __syncthreads();
@@ -143,11 +154,13 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
   if (VALUE_ONLY) return res;
   uint32_t gt = 0, eq = 0;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t o = oct_half(wv, e);
-    gt |= (uint32_t)(o > v) << e;
-    eq |= (uint32_t)(o == v) << e;
-  }
+  for (int o = 0; o < NO; ++o)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t x = oct_half(wv[o], e);
+      gt |= (uint32_t)(x > v) << (8 * o + e);
+      eq |= (uint32_t)(x == v) << (8 * o + e);
+    }
   const int need = k - above;  // 1 <= need <= ties
   if (need >= ties) {
     res.mine = gt | eq;
@@ -171,8 +184,17 @@ __device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, F
     return res;
   }
   res.mine = gt | (uint32_t)rank_ties(
-                       eq, ties, need, [](int b) { return 8 * (int)threadIdx.x + b; }, id, s);
+                       eq, ties, need,
+                       [](int b) { return 8 * ((int)threadIdx.x + (b >> 3) * SEL_BLOCK) + (b & 7); },
+                       id, s);
   return res;
+}
+
+template <bool VALUE_ONLY, bool POS_IDS, typename IdFn>
+__device__ __forceinline__ OctResult oct_select(const uint4 w, int k, IdFn id, FastScratch& s,
+                                                int ts = -1) {
+  const uint4 w1[1] = {w};
+  return octn_select<1, VALUE_ONLY, POS_IDS>(w1, k, id, s, ts);
 }
 
 }  // namespace skv

@@ -27,6 +27,7 @@
 #include "skv_dense.h"
 #include "skv_device.h"
 #include "skv_fastsel.h"
+#include "skv_octsel.h"
 #include "skv_select.h"
 #include "skv_step.h"
 
@@ -716,9 +717,9 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     return bail(SKV_EINVAL);
   }
   w.top_u1 = TopkArgs{a.s2, a.pool_tok, a.cap, M15, a.bm_u1, words1, a.status, ST_POOL,
-                      std::min(lds_items, a.cap), 0, FS_TOP1600, a.s2_tmax, a.cap / 16};
+                      std::min(lds_items, a.cap), 0, FS_TOP1600, a.s2_tmax, a.cap / 16, 0};
   w.top_u2 = TopkArgs{a.s4, a.u1_tok, U1_MAX, M16, a.bm_u2, words2, a.status, ST_U1, U1_MAX,
-                      0, FS_TOP256, nullptr, 0};
+                      0, FS_TOP256, nullptr, 0, 0};
   h->top_u1_lds_items = w.top_u1.lds_items;
   h->top_u2_lds_items = w.top_u2.lds_items;
   // Dynamic LDS of the selection kernels: the sampled-cut scratch, or the
@@ -1166,7 +1167,19 @@ int skv_sync(void* handle, int32_t* status) {
   Handle* h = static_cast<Handle*>(handle);
   if (!h) return SKV_ESTATE;
   HIPCHK(h, hipStreamSynchronize(h->stream));
-  if (status) HIPCHK(h, hipMemcpy(status, h->a.status, G * ST_WORDS * 4, hipMemcpyDeviceToHost));
+  if (status) {
+    HIPCHK(h, hipMemcpy(status, h->a.status, G * ST_WORDS * 4, hipMemcpyDeviceToHost));
+    // the top-1600 instance for the pool sizes just seen: pools of OCT_ITEMS
+    // to 2 x OCT_ITEMS keys are selected in registers by the instance that
+    // carries that path (a speed choice only: both select the same members)
+    int pmax = 0;
+    for (int g = 0; g < G; ++g) pmax = std::max(pmax, (int)status[g * ST_WORDS + ST_POOL]);
+    const int regs2 = pmax > OCT_ITEMS && pmax <= 2 * OCT_ITEMS;
+    if (regs2 != h->w.top_u1.regs2) {
+      h->w.top_u1.regs2 = regs2;
+      drop_graph(h);  // the captured step holds the other instance
+    }
+  }
   return SKV_OK;
 }
 

@@ -135,6 +135,8 @@ struct TopkArgs {
   int fullsel_bit;          // FS_* bit recorded when the full selection runs
   const uint16_t* tile_max; // [G][H][tile_stride] max of every 16-item tile (or NULL)
   int tile_stride;
+  int regs2;                // launch choice: the instance that also selects rows of up to
+                            // 2 x OCT_ITEMS items in registers (same members either way)
 };
 
 
