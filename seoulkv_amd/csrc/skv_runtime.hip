@@ -137,12 +137,13 @@ void build_meta(Handle* h) {
            "\"static_device_bytes\": %zu, \"workspace_device_bytes\": %zu, "
            "\"kernels_per_step\": %d, \"lds_per_block\": %zu, \"pool_lds_items\": %d, "
            "\"prefill_context\": %d, \"appended\": %d, \"append_capacity\": %d, "
-           "\"kv_page_tokens\": %d}",
+           "\"kv_page_tokens\": %d, \"top1600_in_registers_to\": %d}",
            json_escape(prop.name).c_str(), json_escape(prop.gcnArchName).c_str(), a.T, a.sink,
            a.local, h->n_centroids, a.P[0], a.P[1], a.P[2], a.P[3], a.cap, a.pool_min,
            a.pool_capacity, h->np_max, h->static_bytes, h->work_bytes, N_STEP_KERNELS,
            h->lds_per_block, h->w.top_u1.lds_items, h->context0, a.T - h->context0,
-           h->append_capacity, a.kv_table ? 1 << a.kv_shift : 0);
+           h->append_capacity, a.kv_table ? 1 << a.kv_shift : 0,
+           h->w.top_u1.regs2 ? 2 * OCT_ITEMS : OCT_ITEMS);
   h->meta = buf;
 }
 
@@ -1178,6 +1179,7 @@ int skv_sync(void* handle, int32_t* status) {
     if (regs2 != h->w.top_u1.regs2) {
       h->w.top_u1.regs2 = regs2;
       drop_graph(h);  // the captured step holds the other instance
+      build_meta(h);
     }
   }
   return SKV_OK;

@@ -72,6 +72,10 @@ def _stages(index, k, v, qs, inputs, label):
     bounds (minimum 2048, capacity 13056)."""
     rt = _hip.Runtime(0, k, v, index, pool_min=2048, pool_capacity=REF_CAPACITY, debug=True)
     try:
+        # the first step runs the top-k instance without the two-octet register
+        # path; its synchronisation sees pools of 8K-16K keys, so the next
+        # step runs the other instance: both are checked below
+        assert rt.metadata()["top1600_in_registers_to"] == 8192
         for qi, q in enumerate(qs):
             traces, ref = _oracle(index, inputs, q)
             print(f"[gpu] {label}: device step q{qi}", flush=True)
@@ -87,6 +91,8 @@ def _stages(index, k, v, qs, inputs, label):
                 np.testing.assert_array_equal(rt.read_stage("u2", g), tr.u2)
                 np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100)
             _check_output(rt.read_output(), ref)
+            if max(status["pool"]) > 8192:
+                assert rt.metadata()["top1600_in_registers_to"] == 16384
     finally:
         rt.close()
 
