@@ -266,11 +266,12 @@ def calibrate_copy(mib: int) -> int:
     return 0
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` from the committed counter summary
-    (``profiles/hbm_traffic_cfg2.txt``: lines ``traffic <kernel> <bytes>``),
-    or None when that kernel was not measured."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic_cfg2.txt")
+def measured_traffic(kernel: str, config: str):
+    """HBM bytes per launch of ``kernel`` on ``config`` from the committed
+    counter summary of that config (``profiles/hbm_traffic_<config>.txt``:
+    lines ``traffic <kernel> <bytes>``), or None when that kernel was not
+    measured on it."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config}.txt")
     try:
         with open(path) as f:
             for line in f:
@@ -843,7 +844,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(dominant),
+            "traffic": measured_traffic(dominant, args.config),
             "kernel_us": round(dom_us, 2),
             "bytes_per_launch": int(nbytes.get(dominant, 0)),
         },
@@ -856,7 +857,7 @@ def main() -> int:
             "bytes": int(dense_bytes),
             "GB/s": round(dense_bytes / (dn_kernel_ms * 1e-3) / 1e9, 1),
             "frac": round(dense_bytes / (dn_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("dense_fp8"),
+            "traffic": measured_traffic("dense_fp8", args.config),
             "max_abs_vs_oracle": dense_err,
             "sparse_over_dense": round(ms_per_step / dn_ms, 3),
         },
