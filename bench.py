@@ -40,6 +40,7 @@ from seoulkv_amd.synthetic import PROFILES, make_profile  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 G_KV = 4  # KV heads of the layer
 APPEND_BULK = 64  # tokens of the bulk host and device appends after the measured steps
+APPEND_BULK_REPS = 3  # bulk appends of each kind (median reported)
 N_COLD = 10  # independent instances the cold-cache steps rotate over
 PAGE_TOKENS = 256  # tokens per page of the paged-records measurement
 METRIC = "µs/layer decode step at T=128K (1 GPU); achieved HBM GB/s; top-100 ID match"
@@ -59,7 +60,6 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
     scanned = sum(status["scanned"])
     pool = sum(status["pool"])
     u1 = sum(status["u1"])
-    u2 = sum(status["u2"])
     bm_pool = H * sum((n + 63) // 64 * 8 for n in status["pool"])  # top-1600 members
     bm_u1 = H * sum((n + 63) // 64 * 8 for n in status["u1"])      # top-256 members
     return {
@@ -81,16 +81,14 @@ def kernel_bytes(status: dict, p, nc: int) -> dict:
         + pool * (64 + H * 2) + H * pool // 16 * 2,
         # pool scores in; member bitmaps out
         "top1600": pool * H * 2 + bm_pool,
-        # member bitmaps + pool tokens in; U1 tokens, their 128 B (prefix |
-        # residual-2) key rows in; U1 tokens and 4-bit scores out
-        "union_score4": bm_pool + u1 * (4 + 4 + 128 + H * 2),
+        # member bitmaps + pool tokens in; U1 tokens, their full 256 B key
+        # records in; U1 tokens, 4-bit and 8-bit scores out
+        "union_score": bm_pool + u1 * (4 + 4 + 256 + H * 4),
         "top256": u1 * (4 + H * 2) + bm_u1,
-        # member bitmaps + U1 tokens in; full 256 B key records in; U2 tokens
-        # and 8-bit scores out
-        "union_score8": bm_u1 + u2 * (4 + 4 + 256 + H * 2),
-        # U2 scores + tokens in, top-100 IDs out; the 100 FP8 [V||K] records of
-        # each head, the sink/local slice partials in; BF16 output out
-        "top100_sdpa": u2 * (4 + H * 2) + 16 * 100 * 4 + 16 * 100 * 512
+        # per head: U1 8-bit scores and tokens, the 4 heads' top-256 bitmaps
+        # in, top-100 IDs out; the 100 FP8 [V||K] records of each head, the
+        # sink/local slice partials in; BF16 output out
+        "top100_sdpa": H * u1 * (4 + 2) + H * bm_u1 + 16 * 100 * 4 + 16 * 100 * 512
         + 16 * ((p.sink + p.local + 255) // 256) * 258 * 4 + 16 * 256 * 2,
     }
 
@@ -544,7 +542,7 @@ def main() -> int:
     # the decode loops append one token per step (host, then device), then
     # two bulk appends; token IDs stay below 2^20, so config 4 has no room
     loop_steps = max(args.steps, 200)
-    n_append = min(2 * loop_steps + 2 * APPEND_BULK, (1 << 20) - p.context)
+    n_append = min(2 * loop_steps + 2 * APPEND_BULK_REPS * APPEND_BULK, (1 << 20) - p.context)
     config = SeoulKV4Config(stage15_capacity=None, debug=True, append_capacity=n_append)
     with torch.cuda.stream(stream):
         attn = SeoulKV4(device=dev, k=k, v=v, index=index, config=config)
@@ -687,7 +685,7 @@ def main() -> int:
         # and enqueues the step, with no host synchronisation; device time of
         # `loop_steps` such iterations against the same loop without appends.
         append = None
-        if not args.no_append and n_append >= 2 * loop_steps + 2 * APPEND_BULK:
+        if not args.no_append and n_append >= 2 * loop_steps + 2 * APPEND_BULK_REPS * APPEND_BULK:
             rt = attn._state
             kn = k[:, -n_append:].clone()
             vn = v[:, -n_append:].clone()
@@ -733,18 +731,24 @@ def main() -> int:
             dev_us_, dev_call_us = loop(dev_one)
             used += loop_steps
             after_us, _ = loop(None)
-            # bulk appends (wall time including the host sync)
+            # bulk appends (wall time including the host sync), median of
+            # APPEND_BULK_REPS each
             attn.synchronize()
-            t = time.perf_counter()
-            attn.append(kn[:, used:used + APPEND_BULK], vn[:, used:used + APPEND_BULK])
-            attn.synchronize()
-            bulk_host_us = (time.perf_counter() - t) * 1e6
-            used += APPEND_BULK
-            t = time.perf_counter()
-            attn.append(kd[:, used:used + APPEND_BULK], vd[:, used:used + APPEND_BULK])
-            attn.synchronize()
-            bulk_dev_us = (time.perf_counter() - t) * 1e6
-            used += APPEND_BULK
+
+            def bulk(kk, vv) -> float:
+                nonlocal used
+                times = []
+                for _ in range(APPEND_BULK_REPS):
+                    ks, vs = kk[:, used:used + APPEND_BULK], vv[:, used:used + APPEND_BULK]
+                    t = time.perf_counter()
+                    attn.append(ks, vs)
+                    attn.synchronize()
+                    times.append((time.perf_counter() - t) * 1e6)
+                    used += APPEND_BULK
+                return float(np.median(times))
+
+            bulk_host_us = bulk(kn, vn)
+            bulk_dev_us = bulk(kd, vd)
             host_ref, dev_ref = (base_us + mid_us) / 2, (mid_us + after_us) / 2
             log(f"decode loop: step {base_us:.1f} / {mid_us:.1f} / {after_us:.1f} µs (local "
                 f"window {p.local} / +{loop_steps} / +{2 * loop_steps}); with a 1-token host "
@@ -771,7 +775,8 @@ def main() -> int:
                         "it), enqueue the step; device time between HIP events over "
                         "loop_steps iterations, no host sync; *_over_step = against the mean "
                         "of the same loop without appends just before and after (the step "
-                        "grows with the local window); bulk = wall time incl. host sync",
+                        "grows with the local window); bulk = median wall time of 3 appends of "
+                        "bulk_tokens, incl. host sync",
             }
 
     sl_bytes, top_bytes = kv_gather_bytes(top_gpu, p)

@@ -14,11 +14,13 @@
 //               decoupled look-back over the centroid ranges) and the 2-bit
 //               scores of the pool keys
 //   top1600     per head: top-1600 of the pool -> membership bitmap
-//   union_score4  U1 = union over heads in pool order + 4-bit scores of U1
+//   union_score U1 = union over heads in pool order + 4-bit and 8-bit scores
+//               of U1
 //   top256      per head: top-256 of U1 -> membership bitmap
-//   union_score8  U2 = union over heads in U1 order + 8-bit scores of U2
-//   top100      per head: best-first top-100 token IDs, then FP8 attention over
-//               them merged with the sink/local attention slices
+//   top100      per head: best-first top-100 token IDs of U2 (the union of
+//               the heads' top-256, read as a mask over U1) by 8-bit score,
+//               then FP8 attention over them merged with the sink/local
+//               attention slices
 // Reference stages: see the table in skv_step.h.
 //
 // Selection keys are (ordered BF16 score, lowest ID first); all score dots
@@ -1264,34 +1266,32 @@ __device__ __forceinline__ void load_code4(const uint8_t* rec, int kb, uint32_t 
   }
 }
 
-// ============================================================ unions + scores
-// U1 (STAGE 4) / U2 (STAGE 8): the union of the four heads' member bitmaps
-// over the input items (pool positions / U1 positions), compacted in input
-// order, and the union members' 4-bit / 8-bit scores.  Block b of a group
-// owns a contiguous span of bitmap words: it counts the members in all
-// earlier words (its output base), lists its own members in LDS, copies
-// their tokens to the output list and scores them 16 keys per MFMA tile.
-// U1: 64 blocks of 1024 threads per group, one per CU across the 4 groups,
-// each listing up to 16 words per pass (config 2: one pass); U2: 16 blocks
-// of 512 threads per group over at most 100 words.
-constexpr int us_block(int stage) { return stage == 4 ? 1024 : 512; }
-constexpr int US_GRID_U1 = 64;  // blocks per group over the pool
-constexpr int US_GRID_U2 = 32;  // blocks per group over U1 (<= 100 words; spans of >= US_CHUNK)
+// ============================================================ union + scores
+// U1: the union of the four heads' top-1600 member bitmaps over the pool,
+// compacted in pool order, with every member's 4-bit and 8-bit scores.  The
+// 8-bit dot is 16 x (the 4-bit code dot) + (the residual-4 dot), so one pass
+// over a key's record gives both; the top-256 ranks the 4-bit scores and the
+// top-100 the 8-bit scores of the top-256 union (U2), read from this list by
+// U1 position.  Block b of a group owns a contiguous span of bitmap words:
+// it counts the members in all earlier words (its output base), lists its
+// own members in LDS, copies their tokens to the output list and scores
+// them 16 keys per MFMA tile.  64 blocks of 1024 threads per group, one per
+// CU across the 4 groups, each listing up to 16 words per pass (config 2:
+// one pass).
+constexpr int US_BLOCK = 1024;
+constexpr int US_GRID = 64;  // blocks per group over the pool
 
-// The leading arguments are the input count word (status + slot), the input
-// member bitmaps, the input token list, bitmap words per head and the token
-// list's stride per group: the fields the first loads need, preloaded into
-// scalar registers at dispatch.
-template <int STAGE>
-__global__ __launch_bounds__(us_block(STAGE)) void k_union_score(const int* count_word,
-                                                                 const uint64_t* bm_in,
-                                                                 const int* tok_base, int W,
-                                                                 int tok_stride, StepArgs a) {
-  constexpr bool U1 = STAGE == 4;
-  constexpr int US_BLOCK = us_block(STAGE);
+// The leading arguments are the pool size word, the top-1600 member bitmaps,
+// the pool's token list, bitmap words per head and the token list's stride
+// per group: the fields the first loads need, preloaded into scalar
+// registers at dispatch.
+__global__ __launch_bounds__(US_BLOCK) void k_union_score(const int* count_word,
+                                                          const uint64_t* bm_in,
+                                                          const int* tok_base, int W,
+                                                          int tok_stride, StepArgs a) {
   constexpr int US_CHUNK = US_BLOCK / 64;  // bitmap words listed per pass (1 item per thread)
-  SKV_TSB((U1 ? 3 : 8), 0);
-  const int ts = U1 ? 8 : 11;
+  SKV_TSB(3, 0);
+  const int ts = 8;
   SKV_TS(ts, 0);
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1299,11 +1299,8 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(const int* coun
   const int words_in = (n_in + 63) / 64;
   const uint64_t* __restrict__ bm = bm_in + (size_t)g * H * W;
   const int* __restrict__ tok_in = tok_base + (size_t)g * tok_stride;
-  const int cap_out = U1 ? U1_MAX : U2_MAX;
-  int* __restrict__ tok_out = (U1 ? a.u1_tok : a.u2_tok) + (size_t)g * cap_out;
-  uint16_t* __restrict__ s_out = U1 ? a.s4 : a.s8;
-  const int slot_out = U1 ? ST_U1 : ST_U2;
-  if (U1 && blockIdx.x == 0 && wave == 0) {  // diagnostic: postings the pool ranges walked
+  int* __restrict__ tok_out = a.u1_tok + (size_t)g * U1_MAX;
+  if (blockIdx.x == 0 && wave == 0) {  // diagnostic: postings the pool ranges walked
     const int nb = (a.nc + a.pool_range - 1) / a.pool_range;
     int sc = 0;
     for (int i = lane; i < nb; i += WAVE) sc += a.pool_scan[g * a.pool_blocks + i];
@@ -1311,14 +1308,14 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(const int* coun
     if (lane == 0) a.status[g * ST_WORDS + ST_SCANNED] = sc;
   }
   if (n_in == 0) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = 0;
-    SKV_TSE((U1 ? 3 : 8));
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.status[g * ST_WORDS + ST_U1] = 0;
+    SKV_TSE(3);
     return;
   }
   const int span = max(US_CHUNK, (words_in + (int)gridDim.x - 1) / (int)gridDim.x);
   const int w_lo = blockIdx.x * span;
   if (w_lo >= words_in) {
-    SKV_TSE((U1 ? 3 : 8));
+    SKV_TSE(3);
     return;
   }
   const int w_hi = min(words_in, w_lo + span);
@@ -1364,8 +1361,9 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(const int* coun
   // lane l converts key l % 16 of a tile for head l / 16:
   // 4-bit (2 dq - 15 S) 2^(fx + 4), 8-bit (2 dq - 255 S) 2^fx
   const int hq = lane >> 4;
-  const LimbScale ls(q->fx[hq] + (U1 ? 4 : 0), 1);
-  const double lc = LimbScale::offset((U1 ? -15 : -255) * q->sum[hq], q->fx[hq] + (U1 ? 4 : 0));
+  const LimbScale ls4(q->fx[hq] + 4, 1), ls8(q->fx[hq], 1);
+  const double lc4 = LimbScale::offset(-15 * q->sum[hq], q->fx[hq] + 4);
+  const double lc8 = LimbScale::offset(-255 * q->sum[hq], q->fx[hq]);
   for (int c0 = w_lo; c0 < w_hi; c0 += US_CHUNK) {
     const int nw = min(US_CHUNK, w_hi - c0);
     const bool first = c0 == w_lo;
@@ -1391,66 +1389,96 @@ __global__ __launch_bounds__(us_block(STAGE)) void k_union_score(const int* coun
         const int r = s_wbase[j] + __popcll(m & ((1ull << bit) - 1));
         const int t = first ? tok0 : tok_in[64 * (c0 + j) + bit];
         s_tok[r] = t;
-        if (base + r < cap_out) tok_out[base + r] = t;
+        if (base + r < U1_MAX) tok_out[base + r] = t;
       }
     }
     __syncthreads();
     // scores of the listed members, one 16-key tile per wave at a time
     for (int tile = wave; tile * 16 < nloc; tile += US_BLOCK / WAVE) {
       const int i_in = tile * 16 + row;
-      v4i acc = {0, 0, 0, 0};
-      if (U1) {
-        uint32_t av[4][4] = {};
-        if (i_in < nloc) load_code4(a.keyrec + ((size_t)g * a.rec_rows + s_tok[i_in]) * 256, kb, av);
+      uint32_t hi[4][4] = {}, lo[4][4] = {};
+      if (i_in < nloc) {
+        const uint8_t* rec = a.keyrec + ((size_t)g * a.rec_rows + s_tok[i_in]) * 256;
+        load_code4(rec, kb, hi);
+        const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
+        const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
+        const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) acc = mfma_i8(b[kc], av[kc], acc);
-      } else {
-        uint32_t hi[4][4] = {}, lo[4][4] = {};
-        if (i_in < nloc) {
-          const uint8_t* rec = a.keyrec + ((size_t)g * a.rec_rows + s_tok[i_in]) * 256;
-          load_code4(rec, kb, hi);
-          const uint4 r0 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32);
-          const uint4 r1 = *reinterpret_cast<const uint4*>(rec + 128 + kb * 32 + 16);
-          const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-          for (int kc = 0; kc < 4; ++kc) expand4t(rw[2 * kc], rw[2 * kc + 1], lo[kc]);
-        }
-        v4i acc_lo = {0, 0, 0, 0};
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-          acc = mfma_i8(b[kc], hi[kc], acc);
-          acc_lo = mfma_i8(b[kc], lo[kc], acc_lo);
-        }
-        // 8-bit dot = 16 x (code4 dot) + (residual-4 dot), limb by limb
-        // (|16 hi + lo| < 2^23 per limb)
-        acc = acc * 16 + acc_lo;
+        for (int kc = 0; kc < 4; ++kc) expand4t(rw[2 * kc], rw[2 * kc + 1], lo[kc]);
       }
+      v4i acc = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        acc = mfma_i8(b[kc], hi[kc], acc);
+        acc_lo = mfma_i8(b[kc], lo[kc], acc_lo);
+      }
+      // 8-bit dot = 16 x (code4 dot) + (residual-4 dot), limb by limb
+      // (|16 hi + lo| < 2^23 per limb)
+      const v4i acc8 = acc * 16 + acc_lo;
       const int i = tile * 16 + row, o = base + i;
-      if (i < nloc && o < cap_out)
-        s_out[((size_t)g * H + hq) * cap_out + o] =
-            (uint16_t)ordered16(bf16_rne(ls(acc[0], acc[1], acc[2], lc)));
+      if (i < nloc && o < U1_MAX) {
+        const size_t at = ((size_t)g * H + hq) * U1_MAX + o;
+        a.s4[at] = (uint16_t)ordered16(bf16_rne(ls4(acc[0], acc[1], acc[2], lc4)));
+        a.s8[at] = (uint16_t)ordered16(bf16_rne(ls8(acc8[0], acc8[1], acc8[2], lc8)));
+      }
     }
     base += nloc;
     __syncthreads();
   }
-  if (w_hi == words_in && threadIdx.x == 0) a.status[g * ST_WORDS + slot_out] = min(base, cap_out);
+  if (w_hi == words_in && threadIdx.x == 0) a.status[g * ST_WORDS + ST_U1] = min(base, U1_MAX);
   SKV_TS(ts, 15);
-  SKV_TSE((U1 ? 3 : 8));
+  SKV_TSE(3);
 }
 
 // ============================================================ final top-100
-// Per (group, head): the 100 best of U2, written best first (the rank of a
-// member is the number of members with a larger (score, -token) key), then
-// the head's attention over them merged with its sink/local slices.
+// Per (group, head): the 100 best of U2 (the union of the four heads'
+// top-256 over U1) by 8-bit score, written best first (the rank of a member
+// is the number of members with a larger (score, -token) key), then the
+// head's attention over them merged with its sink/local slices.  U2 is not
+// listed: the block reads the U1-indexed 8-bit scores and keeps those whose
+// U1 position is set in any head's top-256 bitmap, so the members come out
+// in U1 order, which is U2's list order.
 constexpr int TOP_KPW = (TOPK + ATTN_WAVES - 1) / ATTN_WAVES;  // selected keys per wave
 constexpr int DENSE_PREF = 2;  // sink/local partials prefetched per merge thread
+
+// Bits 8o .. 8o + 7 of the union of 4 bitmap rows of W words (octet o).
+__device__ __forceinline__ uint32_t union_octet(const uint64_t* __restrict__ bm, int W, int o) {
+  const int w = o >> 3;
+  const uint64_t u = bm[w] | bm[W + w] | bm[2 * W + w] | bm[3 * W + w];
+  return (uint32_t)(u >> (8 * (o & 7))) & 0xffu;
+}
+
+// The packed scores of octet w whose bit in `bits` is set; the rest 0.
+__device__ __forceinline__ uint4 keep_octet(uint4 w, uint32_t bits) {
+  auto keep = [bits](uint32_t word, int q) {
+    const uint32_t b = bits >> (2 * q);
+    return word & (((b & 1u) ? 0xffffu : 0u) | ((b & 2u) ? 0xffff0000u : 0u));
+  };
+  return make_uint4(keep(w.x, 0), keep(w.y, 1), keep(w.z, 2), keep(w.w, 3));
+}
+
+// 8-bit scores of U2 members by U1 position (0 elsewhere): a fast_select source.
+struct UnionScores {
+  static constexpr int PRE = 4;
+  const uint16_t* __restrict__ score;
+  const uint64_t* __restrict__ bm;  // 4 rows of W words
+  int W;
+  __device__ uint32_t at(int i) const {
+    const uint32_t sv = score[i];
+    return (union_octet(bm, W, i >> 3) >> (i & 7)) & 1u ? sv : 0u;
+  }
+  __device__ uint4 oct(int o) const {
+    return keep_octet(reinterpret_cast<const uint4*>(score)[o], union_octet(bm, W, o));
+  }
+};
 
 // The leading arguments repeat the fields of a that the first loads need
 // (preloaded into scalar registers at dispatch).  PAGED: the selected records
 // are read through the page table.
 template <bool PAGED>
 __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const uint16_t* s8,
-                                                      const int* u2_tok, const uint16_t* q_in,
+                                                      const int* u1_tok, const uint64_t* bm_u2,
+                                                      int W, const uint16_t* q_in,
                                                       const float* dense_part, int dense_slices,
                                                       int exact_select, StepArgs a) {
   SKV_TSB(9, 0);
@@ -1459,14 +1487,22 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ SelectScratch s;
   __shared__ __align__(16) uint64_t s_key[TOPK];
-  __shared__ __align__(16) uint32_t s_pos[TOPK];  // U2 positions (atomic-order paths)
+  __shared__ __align__(16) uint32_t s_pos[TOPK];  // U1 positions (atomic-order paths)
   __shared__ int s_cnt;
+  __shared__ int s_u2[SEL_WAVES];  // U2 members per wave's octets
   __shared__ AttnScratch att;
-  const int n = status[g * ST_WORDS + ST_U2];
-  const uint16_t* sc = s8 + (size_t)j * U2_MAX;
-  const int* tok = u2_tok + (size_t)g * U2_MAX;
+  const int n = status[g * ST_WORDS + ST_U1];
+  const uint16_t* sc = s8 + (size_t)j * U1_MAX;
+  const int* tok = u1_tok + (size_t)g * U1_MAX;
+  const uint64_t* bmg = bm_u2 + (size_t)g * H * W;
   auto id = [tok](int i) { return (uint32_t)tok[i]; };
   extern __shared__ __align__(16) unsigned char dyn[];
+  // this thread's octet of U1 positions: union bits (n <= U1_MAX <= 8 x SEL_BLOCK)
+  const uint32_t ubits = 8 * (int)threadIdx.x < n ? union_octet(bmg, W, threadIdx.x) : 0u;
+  {
+    const int c = wave_sum(__popc(ubits));
+    if (lane == 0) s_u2[wave] = c;  // read after a later barrier
+  }
   // loads independent of the selection, issued first: the query and the
   // sink/local partials (consumed only by the final merge)
   float q[4];
@@ -1487,17 +1523,17 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
   }
   if (threadIdx.x == 0) s_cnt = 0;
   bool done = false, listed = false;  // listed: s_key is in U2 list order
-  if (exact_select == 0) {  // n <= U2_MAX <= OCT_ITEMS: scores and IDs in registers
-    const uint4 w = load_oct(sc, n);
+  if (exact_select == 0) {  // n <= U1_MAX <= OCT_ITEMS: scores and IDs in registers
+    const uint4 w = keep_octet(load_oct(sc, n), ubits);
     uint4 t0 = make_uint4(0, 0, 0, 0), t1 = t0;
-    if (8 * (int)threadIdx.x < n) {  // rows hold U2_MAX (a multiple of 8) entries
+    if (8 * (int)threadIdx.x < n) {  // rows hold U1_MAX (a multiple of 8) entries
       t0 = reinterpret_cast<const uint4*>(tok)[2 * threadIdx.x];
       t1 = reinterpret_cast<const uint4*>(tok)[2 * threadIdx.x + 1];
     }
     // the octet's tokens in LDS for the tie ranking (ordered before their
     // reads by the selection's first barrier)
-    __shared__ __align__(16) uint32_t s_tok[U2_MAX];
-    if (8 * (int)threadIdx.x < U2_MAX) {
+    __shared__ __align__(16) uint32_t s_tok[U1_MAX];
+    if (8 * (int)threadIdx.x < U1_MAX) {
       reinterpret_cast<uint4*>(s_tok)[2 * threadIdx.x] = t0;
       reinterpret_cast<uint4*>(s_tok)[2 * threadIdx.x + 1] = t1;
     }
@@ -1522,9 +1558,10 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
       done = listed = true;
     }
   }
-  if (!done && exact_select != 1) {  // n <= U2_MAX <= FS_SAMPLE: the cut is exact
+  const UnionScores src{sc, bmg, W};
+  if (!done && exact_select != 1) {
     FastScratch& fs = *reinterpret_cast<FastScratch*>(dyn);
-    const FastResult r = fast_select(RowScores{sc}, n, TOPK, id, fs, exact_select == 2, 13);
+    const FastResult r = fast_select(src, n, TOPK, id, fs, exact_select == 2, 13);
     if (r.ok) {
       SKV_TS(13, 6);
       for (int c = threadIdx.x; c < r.ncand; c += SEL_BLOCK) {
@@ -1545,8 +1582,9 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
     }
   }
   if (!done) {
-    __shared__ __align__(16) uint16_t so[U2_MAX];
-    load_lds_scores(so, sc, n, same16);
+    __shared__ __align__(16) uint16_t so[U1_MAX];
+    if (8 * (int)threadIdx.x < n)  // n <= U1_MAX <= 8 x SEL_BLOCK: one octet per thread
+      reinterpret_cast<uint4*>(so)[threadIdx.x] = keep_octet(load_oct(sc, n), ubits);
     __syncthreads();
     const Selection sel = block_select(so, n, TOPK, id, s);
     for_scores(so, n, [&](int i, uint32_t o) {
@@ -1565,7 +1603,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
   SKV_TS(13, 7);
   const int m = min(s_cnt, TOPK);
   if (!listed) {  // block-uniform
-    // members listed in atomic order: put them in U2 list order, as the
+    // members listed in atomic order: put them in U1 (= U2 list) order, as the
     // register path lists them, so that the attention sums run in the same
     // order on every selection path (bit-identical, reproducible outputs)
     uint64_t key = 0;
@@ -1604,6 +1642,12 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
   stash_wave(att, mw, lw, ow);
   __syncthreads();
   SKV_TS(13, 9);
+  if (h == 0 && threadIdx.x == 0) {  // |U2|
+    int u2 = 0;
+#pragma unroll
+    for (int i = 0; i < SEL_WAVES; ++i) u2 += s_u2[i];
+    a.status[g * ST_WORDS + ST_U2] = u2;
+  }
   // merge with the sink/local slices
   if (threadIdx.x < D) {
     float M, Ls, O;
@@ -1642,7 +1686,7 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
 
 // ============================================================ launcher
 const char* const kKernelNames[N_STEP_KERNELS] = {
-    "front", "select", "pool", "top1600", "union_score4", "top256", "union_score8", "top100_sdpa"};
+    "front", "select", "pool", "top1600", "union_score", "top256", "top100_sdpa"};
 
 static void launch_topk(const TopkArgs& t, size_t lds, hipStream_t st) {
   hipLaunchKernelGGL(t.regs2 ? k_topk<true> : k_topk<false>, dim3(G * H), dim3(SEL_BLOCK), lds,
@@ -1680,7 +1724,7 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
       launch_topk(w.top_u1, w.top_u1_lds, st);
       break;
     case 4:
-      hipLaunchKernelGGL(k_union_score<4>, dim3(US_GRID_U1, G), dim3(us_block(4)), 0, st,
+      hipLaunchKernelGGL(k_union_score, dim3(US_GRID, G), dim3(US_BLOCK), 0, st,
                          (const int*)a.status + ST_POOL, (const uint64_t*)a.bm_u1,
                          (const int*)a.pool_tok, a.words_u1, a.cap, a);
       break;
@@ -1688,15 +1732,11 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
       launch_topk(w.top_u2, w.top_u2_lds, st);
       break;
     case 6:
-      hipLaunchKernelGGL(k_union_score<8>, dim3(US_GRID_U2, G), dim3(us_block(8)), 0, st,
-                         (const int*)a.status + ST_U1, (const uint64_t*)a.bm_u2,
-                         (const int*)a.u1_tok, a.words_u2, U1_MAX, a);
-      break;
-    case 7:
       hipLaunchKernelGGL(a.kv_table ? k_top100<true> : k_top100<false>, dim3(G * H),
                          dim3(SEL_BLOCK), sizeof(FastScratch), st,
-                         (const int*)a.status, (const uint16_t*)a.s8, (const int*)a.u2_tok, a.q,
-                         (const float*)a.dense_part, a.dense_slices, a.exact_select, a);
+                         (const int*)a.status, (const uint16_t*)a.s8, (const int*)a.u1_tok,
+                         (const uint64_t*)a.bm_u2, a.words_u2, a.q, (const float*)a.dense_part,
+                         a.dense_slices, a.exact_select, a);
       break;
     default:
       break;
@@ -1716,10 +1756,9 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
       break;
     case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)PL_BM_WORDS * 4; break;
     case 3: fn = reinterpret_cast<const void*>(&k_topk<true>); dyn = w.top_u1_lds; break;
-    case 4: fn = reinterpret_cast<const void*>(&k_union_score<4>); break;
+    case 4: fn = reinterpret_cast<const void*>(&k_union_score); break;
     case 5: fn = reinterpret_cast<const void*>(&k_topk<false>); dyn = w.top_u2_lds; break;
-    case 6: fn = reinterpret_cast<const void*>(&k_union_score<8>); break;
-    case 7:
+    case 6:
       fn = a.kv_table ? reinterpret_cast<const void*>(&k_top100<true>)
                       : reinterpret_cast<const void*>(&k_top100<false>);
       dyn = sizeof(FastScratch);

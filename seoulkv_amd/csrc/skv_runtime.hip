@@ -596,8 +596,7 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     a.selbm = (uint32_t*)ar.take((size_t)G * (nc / 32) * 4);  // cleared by k_front
     a.u1_tok = (int*)ar.take((size_t)G * U1_MAX * 4);
     a.s4 = (uint16_t*)ar.take((size_t)G * H * U1_MAX * 2);
-    a.u2_tok = (int*)ar.take((size_t)G * U2_MAX * 4);
-    a.s8 = (uint16_t*)ar.take((size_t)G * H * U2_MAX * 2);
+    a.s8 = (uint16_t*)ar.take((size_t)G * H * U1_MAX * 2);
     a.top = (int*)ar.take(G * H * TOPK * 4);
     a.status = (int*)ar.take(G * ST_WORDS * 4);
     a.out = (uint16_t*)ar.take(16 * D * 2);
@@ -1277,9 +1276,43 @@ int skv_read_stage(void* handle, int stage, int group, void* host_out, int64_t c
     case SKV_STAGE_S4:
       return copy_rows(a.s4 + (size_t)group * H * U1_MAX, U1_MAX, 2, st[ST_U1], H);
     case SKV_STAGE_U2:
-      return copy_rows(a.u2_tok + (size_t)group * U2_MAX, 0, 4, st[ST_U2], 1);
-    case SKV_STAGE_S8:
-      return copy_rows(a.s8 + (size_t)group * H * U2_MAX, U2_MAX, 2, st[ST_U2], H);
+    case SKV_STAGE_S8: {
+      // U2 is not listed on the device: its members are the U1 positions set
+      // in any head's top-256 bitmap, in U1 order, and their 8-bit scores sit
+      // at those positions of the U1-indexed score rows
+      const int n1 = st[ST_U1], W = a.words_u2;
+      std::vector<uint64_t> bm((size_t)H * W);
+      HIPCHK(h, hipMemcpy(bm.data(), a.bm_u2 + (size_t)group * H * W, bm.size() * 8,
+                          hipMemcpyDeviceToHost));
+      std::vector<int> pos;
+      for (int i = 0; i < n1; ++i) {
+        const int w = i >> 6;
+        if (((bm[w] | bm[W + w] | bm[2 * W + w] | bm[3 * W + w]) >> (i & 63)) & 1u) pos.push_back(i);
+      }
+      const int64_t n2 = (int64_t)pos.size();
+      if (n2 != st[ST_U2])
+        return fail(h, SKV_EINVAL, "U2 count word %d differs from the bitmaps' %lld", st[ST_U2],
+                    (long long)n2);
+      const bool toks = stage == SKV_STAGE_U2;
+      if ((toks ? 1 : H) * n2 > cap) return fail(h, SKV_EINVAL, "stage buffer too small");
+      if (toks) {
+        std::vector<int> u1(std::max(n1, 1));
+        HIPCHK(h, hipMemcpy(u1.data(), a.u1_tok + (size_t)group * U1_MAX, (size_t)n1 * 4,
+                            hipMemcpyDeviceToHost));
+        int* o = static_cast<int*>(host_out);
+        for (int64_t k = 0; k < n2; ++k) o[k] = u1[pos[k]];
+      } else {
+        std::vector<uint16_t> row(std::max(n1, 1));
+        uint16_t* o = static_cast<uint16_t*>(host_out);
+        for (int hh = 0; hh < H; ++hh) {
+          HIPCHK(h, hipMemcpy(row.data(), a.s8 + ((size_t)group * H + hh) * U1_MAX, (size_t)n1 * 2,
+                              hipMemcpyDeviceToHost));
+          for (int64_t k = 0; k < n2; ++k) o[hh * n2 + k] = row[pos[k]];
+        }
+      }
+      if (count_out) *count_out = n2;
+      return SKV_OK;
+    }
     case SKV_STAGE_TOP:
       return copy_rows(a.top + group * H * TOPK, 0, 4, H * TOPK, 1);
     case SKV_STAGE_QPREP: {

@@ -11,12 +11,13 @@
 //                    masks); codegen/stage15.py:275-345 (mate-ownership dedup,
 //                    encounter-order pool); codegen/stage15.py:886-995 (2-bit scores)
 //   k_top1600        codegen/stage15.py:1027-1180 (top-2048, first 1600 used)
-//   k_union_score<4> codegen/stage15.py:1519-1597 (U1) +
-//                    _kernels/stage16/seoulkv4_stage16_matrix.py:21-60 (4-bit scores)
+//   k_union_score    codegen/stage15.py:1519-1597 (U1) +
+//                    _kernels/stage16/seoulkv4_stage16_matrix.py:21-60 (4-bit scores) +
+//                    _kernels/stage16/seoulkv4_union_matrix.py:58-139 (8-bit scores,
+//                    here of every U1 key)
 //   k_top256         codegen/refinement_fusion.py:263-266,402-455
-//   k_union_score<8> codegen/refinement_fusion.py:142-186 (U2) +
-//                    _kernels/stage16/seoulkv4_union_matrix.py:58-139 (8-bit scores)
-//   k_top100         codegen/refinement_fusion.py:296-300,495-531
+//   k_top100         codegen/refinement_fusion.py:142-186 (U2, as a mask over U1) +
+//                    codegen/refinement_fusion.py:296-300,495-531
 //   k_select, k_top100  sparse SDPA: codegen/attention.py:35-201 (+ TTNN sparse_sdpa)
 #pragma once
 
@@ -110,9 +111,8 @@ struct StepArgs {
   float* dense_part;        // [16][dense_slices][D + 2] sink/local partial (o, max, sum)
   uint32_t* selbm;          // [G][nc/32] selected-cluster bitmap (cleared each step)
   int* u1_tok;              // [G][U1_MAX]
-  uint16_t* s4;             // [G][H][U1_MAX] ordered
-  int* u2_tok;              // [G][U2_MAX]
-  uint16_t* s8;             // [G][H][U2_MAX] ordered
+  uint16_t* s4;             // [G][H][U1_MAX] ordered 4-bit scores of U1
+  uint16_t* s8;             // [G][H][U1_MAX] ordered 8-bit scores of U1 (U2 members read)
   int* top;                 // [G][H][TOPK]
   int* status;              // [G][ST_WORDS]
   uint16_t* out;            // [16][256] bf16
@@ -160,7 +160,7 @@ constexpr int APPEND_FUSE = 16;
 // member-bitmap words the top-k kernel keeps in LDS beside its scratch
 constexpr int TOPK_LDS_WORDS = 2048;
 
-constexpr int N_STEP_KERNELS = 8;
+constexpr int N_STEP_KERNELS = 7;
 extern const char* const kKernelNames[N_STEP_KERNELS];
 
 // Dynamic LDS bytes of a top-k launch whose full selection holds lds_items

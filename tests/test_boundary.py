@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol(lib):
     for name in declared:
         assert hasattr(lib, name), name
     assert lib.skv_version().decode().startswith("seoulkv4-hip")
-    assert lib.skv_kernel_count() == 8
+    assert lib.skv_kernel_count() == 7
     names = [lib.skv_kernel_name(i).decode() for i in range(lib.skv_kernel_count())]
     assert names[0] == "front" and names[-1] == "top100_sdpa"
     assert not lib.skv_kernel_name(99)  # out of range: empty name

@@ -27,7 +27,7 @@ int main(void) {
   memset(&ix, 0, sizeof ix);
   memset(&pages, 0, sizeof pages);
   if (strncmp(skv_version(), "seoulkv4-hip", 12) != 0) return 10;
-  if (skv_kernel_count() != 8) return 11;
+  if (skv_kernel_count() != 7) return 11;
   /* NULL index: rejected before any device work, handle cleared */
   code = skv_create(NULL, NULL, NULL, 0, NULL, &h);
   if (code != SKV_EINVAL || h != NULL) return 12;

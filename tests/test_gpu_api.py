@@ -65,7 +65,7 @@ def test_lifecycle_and_borrowed_results():
         _check_output(r1.to_torch(), ref)
         assert torch.equal(skv.debug_snapshot()["selected_ids"], _top100(traces))
         meta = skv.metadata()
-        assert meta["initialized"] and meta["runtime"]["kernels_per_step"] == 8
+        assert meta["initialized"] and meta["runtime"]["kernels_per_step"] == 7
     with pytest.raises(RuntimeError):
         r1.to_torch()  # closed
     with pytest.raises(RuntimeError):
