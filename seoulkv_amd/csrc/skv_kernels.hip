@@ -546,10 +546,56 @@ __device__ void select_in_registers(const StepArgs& a, const uint16_t* lower,
   SKV_TS(2, 15);
 }
 
+// The same for nc <= NO x 8 x SEL_BLOCK centroids held as NO octets per
+// thread (octet o of thread t: centroids 8 (t + o SEL_BLOCK) ..): all three
+// rows are loaded at once, the threshold and the fine selection each run in
+// registers, so the longer lists need no tile maxima and no second load
+// round.  The fine selection ranks ties by centroid ID as IDs (octet order is
+// not position order); with more ties at its P-th score than that ranking
+// holds it returns false (the threshold is written) and the caller runs the
+// fine selection another way.
+template <int NO>
+__device__ __forceinline__ bool select_in_registers_n(const StepArgs& a, const uint16_t* lower,
+                                      const uint16_t* upper, const uint16_t* fine, int nc, int g,
+                                      int h, FastScratch& fs, uint32_t* thr_out) {
+  const int t = threadIdx.x;
+  const size_t row = ((size_t)g * H + h) * nc;
+  uint4 wl[NO], wu[NO], wf[NO];
+#pragma unroll
+  for (int o = 0; o < NO; ++o) {
+    wl[o] = load_oct(lower + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
+    wu[o] = load_oct(upper + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
+    wf[o] = load_oct(fine + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
+  }
+  auto cid = [](int i) { return (uint32_t)i; };
+  const OctResult r1 = octn_select<NO, true, false>(wl, a.P[g], cid, fs, 2);
+  const uint32_t thr = r1.sel.all ? 0u : r1.sel.v;
+  if (t == 0) a.thr[g * H + h] = thr;
+  *thr_out = thr;
+  SKV_TS(2, 6);
+  uint4 wm[NO];
+#pragma unroll
+  for (int o = 0; o < NO; ++o) wm[o] = MaskedScores::pick4(wf[o], wu[o], thr);
+  const OctResult r2 = octn_select<NO, false, false>(wm, a.P[g], cid, fs, 4);
+  if (!r2.ok) return false;  // block-uniform
+  // items 8u .. 8u+7 (u = t + o SEL_BLOCK) are byte u & 3 of bitmap word u >> 2
+#pragma unroll
+  for (int o = 0; o < NO; ++o) {
+    uint32_t m = ((r2.mine >> (8 * o)) & 0xffu) << (8 * (t & 3));
+    m |= __shfl_xor(m, 1);
+    m |= __shfl_xor(m, 2);
+    if ((t & 3) == 0 && m) atomicOr(&a.selbm[(size_t)g * (nc / 32) + ((t + o * SEL_BLOCK) >> 2)], m);
+  }
+  SKV_TS(2, 15);
+  return true;
+}
+
 // The leading arguments repeat the fields of a that the selection blocks'
 // first loads need (preloaded into scalar registers at dispatch).  PAGED: the
-// sink/local records are read through the page table.
-template <bool PAGED>
+// sink/local records are read through the page table.  NO > 1: the instance
+// for nc in (8 x SEL_BLOCK, NO x 8 x SEL_BLOCK], selecting in registers
+// (select_in_registers_n); NO = 1 for every other nc.
+template <bool PAGED, int NO>
 __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint16_t* lower, const uint16_t* upper,
                                                       const uint16_t* fine, int nc_arg,
                                                       int exact_select, int dense_slices,
@@ -576,12 +622,31 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_select(const uint16_t* lower, con
     return;
   }
   const int g = blockIdx.x / H, h = blockIdx.x % H, nc = nc_arg;
-  if (exact_select == 0 && nc <= OCT_ITEMS) {
+  if (NO == 1 && exact_select == 0 && nc <= OCT_ITEMS) {
     select_in_registers(a, lower, upper, fine, nc, g, h, *reinterpret_cast<FastScratch*>(dyn));
     SKV_TSE(5);
     return;
   }
   __shared__ SelectScratch s;
+  if constexpr (NO > 1) {  // launched for exact_select == 0 and nc <= NO x OCT_ITEMS only
+    uint32_t thr;
+    if (!select_in_registers_n<NO>(a, lower, upper, fine, nc, g, h,
+                                   *reinterpret_cast<FastScratch*>(dyn), &thr)) {
+      // more ties at the P-th fine score than the register ranking holds:
+      // the full selection over the LDS copy of the eligible fine scores
+      const size_t row = ((size_t)g * H + h) * nc;
+      uint16_t* so = reinterpret_cast<uint16_t*>(dyn);
+      load_lds_masked(so, fine + row, upper + row, thr, nc);
+      __syncthreads();
+      const Selection sel = block_select(so, nc, a.P[g], [](int i) { return (uint32_t)i; }, s);
+      uint32_t* selbm = a.selbm + (size_t)g * (nc / 32);
+      for_scores(so, nc, [&](int c, uint32_t o) {
+        if (sel.member(o, (uint32_t)c)) atomicOr(&selbm[c >> 5], 1u << (c & 31));
+      });
+    }
+    SKV_TSE(5);
+    return;
+  }
   __shared__ uint32_t s_thr;
   const size_t row = ((size_t)g * H + h) * nc;
   const uint16_t* lo = a.lower + row;  // ordered; never 0 (the "excluded" mark)
@@ -1688,6 +1753,20 @@ __global__ __launch_bounds__(SEL_BLOCK) void k_top100(const int* status, const u
 const char* const kKernelNames[N_STEP_KERNELS] = {
     "front", "select", "pool", "top1600", "union_score", "top256", "top100_sdpa"};
 
+// The select instance for the centroid count: rows of up to 2 or 4 x
+// OCT_ITEMS centroids selected in registers, every other count by the
+// one-octet instance (its register path, tile maxima or sampled cuts).
+using SelectFn = void (*)(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int,
+                          StepArgs);
+static SelectFn select_kernel(const StepArgs& a) {
+  const int no = a.exact_select != 0 || a.nc <= OCT_ITEMS ? 1
+                 : a.nc <= 2 * OCT_ITEMS                  ? 2
+                 : a.nc <= 4 * OCT_ITEMS                  ? 4
+                                                          : 1;
+  if (a.kv_table) return no == 2 ? k_select<true, 2> : no == 4 ? k_select<true, 4> : k_select<true, 1>;
+  return no == 2 ? k_select<false, 2> : no == 4 ? k_select<false, 4> : k_select<false, 1>;
+}
+
 static void launch_topk(const TopkArgs& t, size_t lds, hipStream_t st) {
   hipLaunchKernelGGL(t.regs2 ? k_topk<true> : k_topk<false>, dim3(G * H), dim3(SEL_BLOCK), lds,
                      st, t.status + t.count_slot,
@@ -1709,7 +1788,7 @@ void launch_kernel(const StepArgs& a, const StepWork& w, hipStream_t st, int k) 
       break;
     }
     case 1:
-      hipLaunchKernelGGL(a.kv_table ? k_select<true> : k_select<false>,
+      hipLaunchKernelGGL(select_kernel(a),
                          dim3(G * H * (1 + a.dense_slices) + 2 * G), dim3(SEL_BLOCK),
                          w.select_lds, st, (const uint16_t*)a.lower, (const uint16_t*)a.upper,
                          (const uint16_t*)a.fine_ord, a.nc, a.exact_select, a.dense_slices, a);
@@ -1750,8 +1829,7 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   switch (k) {
     case 0: fn = reinterpret_cast<const void*>(&k_front<true, true>); break;
     case 1:
-      fn = a.kv_table ? reinterpret_cast<const void*>(&k_select<true>)
-                      : reinterpret_cast<const void*>(&k_select<false>);
+      fn = reinterpret_cast<const void*>(select_kernel(a));
       dyn = w.select_lds;
       break;
     case 2: fn = reinterpret_cast<const void*>(&k_pool); dyn = (size_t)PL_BM_WORDS * 4; break;
@@ -1769,6 +1847,14 @@ hipError_t step_kernel_lds(const StepArgs& a, const StepWork& w, int k, size_t* 
   const hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return e;
   size_t st = attr.sharedSizeBytes;
+  if (k == 1) {  // the one-octet instance too (the selection-path test modes launch it)
+    hipFuncAttributes a1;
+    const hipError_t e1 = hipFuncGetAttributes(
+        &a1, a.kv_table ? reinterpret_cast<const void*>(&k_select<true, 1>)
+                        : reinterpret_cast<const void*>(&k_select<false, 1>));
+    if (e1 != hipSuccess) return e1;
+    st = std::max(st, (size_t)a1.sharedSizeBytes);
+  }
   if (k == 3) {  // both top-k instances
     hipFuncAttributes attr2;
     const hipError_t e2 = hipFuncGetAttributes(&attr2, reinterpret_cast<const void*>(&k_topk<false>));

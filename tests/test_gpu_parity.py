@@ -260,3 +260,40 @@ def test_degenerate_queries_match_the_oracle(runtimes, kind):
         assert np.abs(got[j] - out[j]).max() <= 2e-2, f"head {j} max-abs"
         if np.linalg.norm(out[j]) > 0:
             assert cosine(got[j], out[j]) >= 0.999, f"head {j} cosine"
+
+
+# Long centroid lists selected in registers (two and four octets per thread,
+# about four keys per centroid as in the reference's default index): a real
+# query, and the zero query, whose fine scores all tie (far more ties at the
+# P-th score than the register ranking holds, so the full selection over LDS
+# runs), and the one-hot query.
+LONG_NC_CASES = {
+    "t40960_nc10240": dict(context=40960, components=1024, nc=10240, nprobe=256, seed_shift=5),
+    "t98304_nc24576": dict(context=98304, components=2048, nc=24576, nprobe=256, seed_shift=9),
+}
+
+
+@pytest.mark.parametrize("name", list(LONG_NC_CASES))
+def test_long_centroid_lists_in_registers(runtimes, name):
+    p = LONG_NC_CASES[name]
+    index, k, v, qs = case(**p)
+    print(f"[gpu] create runtime {name}", flush=True)
+    rt = runtimes[name] = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True)
+    queries = {"real": qs[0], **{k_: q for k_, q in degenerate_queries(qs[0]).items()
+                                 if k_ in ("zero", "onehot")}}
+    for kind, q in queries.items():
+        print(f"[gpu] {name} query {kind}", flush=True)
+        rt.bind_query(q)
+        rt.enqueue()
+        status = rt.synchronize()
+        assert status["err"] == [0, 0, 0, 0]
+        traces, out = oracle_step(p, q)
+        for g, tr in enumerate(traces):
+            np.testing.assert_array_equal(rt.read_stage("thresh", g), tr.thr, err_msg=f"{kind} g{g}")
+            np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected,
+                                          err_msg=f"{kind} g{g}")
+            np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool, err_msg=f"{kind} g{g}")
+            np.testing.assert_array_equal(rt.read_stage("top", g), tr.top100, err_msg=f"{kind} g{g}")
+        got = rt.read_output().float().numpy().reshape(16, 256)
+        for j in range(16):
+            assert np.abs(got[j] - out[j]).max() <= 2e-2, f"{kind} head {j} max-abs"
