@@ -556,14 +556,18 @@ __device__ void select_in_registers(const StepArgs& a, const uint16_t* lower,
 // fine selection another way.
 template <int NO>
 __device__ __forceinline__ bool select_in_registers_n(const StepArgs& a, const uint16_t* lower,
-                                      const uint16_t* upper, const uint16_t* fine, int nc, int g,
-                                      int h, FastScratch& fs, uint32_t* thr_out) {
+                                                      const uint16_t* upper, const uint16_t* fine,
+                                                      int nc, int g, int h, FastScratch& fs,
+                                                      uint32_t* thr_out) {
   const int t = threadIdx.x;
   const size_t row = ((size_t)g * H + h) * nc;
+  // the lower bounds first: the threshold waits for them alone (the waits
+  // count loads in issue order), the rest arrive during its selection
   uint4 wl[NO], wu[NO], wf[NO];
 #pragma unroll
+  for (int o = 0; o < NO; ++o) wl[o] = load_oct(lower + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
+#pragma unroll
   for (int o = 0; o < NO; ++o) {
-    wl[o] = load_oct(lower + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
     wu[o] = load_oct(upper + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
     wf[o] = load_oct(fine + row + o * OCT_ITEMS, nc - o * OCT_ITEMS);
   }
