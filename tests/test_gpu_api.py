@@ -271,6 +271,7 @@ def _full_size_parity(name, *, nprobe=None, clustered=True, pool_min=2048, queri
             assert status["err"] == [0, 0, 0, 0]
             for g, tr in enumerate(traces):
                 assert status["pool"][g] == len(tr.pool)
+                np.testing.assert_array_equal(rt.read_stage("thresh", g), tr.thr)
                 np.testing.assert_array_equal(rt.read_stage("selected", g), tr.selected)
                 np.testing.assert_array_equal(rt.read_stage("pool", g), tr.pool)
                 np.testing.assert_array_equal(rt.read_stage("u1", g), tr.u1)
@@ -311,9 +312,17 @@ def test_full_size_parity_config3_nprobe_sweep(nprobe, clustered):
 
 
 @pytest.mark.slow
+def test_full_size_parity_config1():
+    """T = 32768; every stage for two queries (the
+    pool sized in HBM: the reference's capacity rejects this config, see
+    test_capacity_error_then_hbm_sized_pool_at_config1)."""
+    _full_size_parity("cfg1", queries=(0, 1), n_queries=2)
+
+
+@pytest.mark.slow
 def test_full_size_parity_config4():
-    """T = 1048576, nc = 65536, P = 512."""
-    _full_size_parity("cfg4")
+    """T = 1048576, nc = 65536, P = 512; two queries."""
+    _full_size_parity("cfg4", queries=(0, 1), n_queries=2)
 
 
 def test_time_kernel_keeps_the_step_consistent():
