@@ -400,7 +400,9 @@ __device__ __forceinline__ void fr_score(const StepArgs& a, int g, int tile, int
   const uint32_t fo = ordered16(fb);
   a.fine_ord[o] = (uint16_t)fo;
   if (a.debug) a.fine_bits[o] = (uint16_t)fb;
-  if (a.tmax_lo) {
+  // tile maxima: read by the one-octet select instance only (centroid
+  // lists past the register instances, or the selection-path test modes)
+  if (a.tmax_lo && (a.exact_select != 0 || a.nc > 4 * OCT_ITEMS)) {
     // 8-centroid tile maxima: within each quad, then the two quads of each
     // half row (half-row mirror); the fine-score maximum of the whole row
     uint32_t lmax = lo16, fmax = fo;
