@@ -95,10 +95,11 @@ struct Handle {
   DenseArgs dn{};  // dense FP8 decode over every key (comparison path)
   // cache append: tokens after the prefill context extend the local window
   int context0 = 0, append_capacity = 0;
-  uint16_t* append_stage = nullptr;  // [2][G][APPEND_CHUNK][256] bf16 (host appends)
   // pinned host staging of long host appends: two [2][G][chunk][256] BF16
-  // slots used in turn, each reused once its upload (event) has left it
+  // slots used in turn, each reused once the pack kernel that reads it over
+  // the bus (through append_host_dev, its device address) has finished
   uint16_t* append_host = nullptr;
+  const uint16_t* append_host_dev = nullptr;
   hipEvent_t append_ev[2] = {};
   unsigned append_next = 0;
   int n_centroids = 0, np_max = 0;
@@ -605,9 +606,6 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     a.bm_u2 = (uint64_t*)ar.take((size_t)G * H * words2 * 8);
     h->dn.part = (float*)ar.take((size_t)G * DN_TARGET_BLOCKS * H * (D + 2) * 4);  // any T
     h->dn.out = (uint16_t*)ar.take(16 * D * 2);
-    h->append_stage =
-        cap_app ? (uint16_t*)ar.take((size_t)2 * G * std::min(cap_app, APPEND_CHUNK) * D * 2)
-                : nullptr;
   };
   plan_work(wk);
   h->work_bytes = wk.used;
@@ -751,7 +749,9 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
   if (cap_app && ring_ok) {
     const size_t slot = (size_t)2 * G * std::min(cap_app, APPEND_CHUNK) * D;
     ring_ok = hipHostMalloc((void**)&h->append_host, 2 * slot * 2, hipHostMallocDefault) ==
-              hipSuccess;
+                  hipSuccess &&
+              hipHostGetDevicePointer((void**)&h->append_host_dev, h->append_host, 0) ==
+                  hipSuccess;
     for (hipEvent_t& e : h->append_ev)
       ring_ok = ring_ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
   }
@@ -1034,27 +1034,27 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
     HIPCHK(h, hipGetLastError());
   } else {
     // chunks of the caller's [G][n][D] arrays gathered into a pinned slot as
-    // [K: G][c][D] then [V: G][c][D], one upload per chunk
+    // [K: G][c][D] then [V: G][c][D]; the pack kernel reads the slot over
+    // the bus (no copy engine: its latency varied by milliseconds between
+    // machines), and the slot is reused once that kernel has finished
     const int chunk = std::min(h->append_capacity, APPEND_CHUNK);
-    uint16_t* sk = h->append_stage;
     for (int t0 = 0; t0 < n; t0 += chunk) {
       const int c = std::min(chunk, n - t0);
       const unsigned slot = h->append_next++ % 2;
-      uint16_t* hk = h->append_host + (size_t)slot * 2 * G * chunk * D;
+      const size_t off = (size_t)slot * 2 * G * chunk * D;
+      uint16_t* hk = h->append_host + off;
       uint16_t* hv = hk + (size_t)G * c * D;
       HIPCHK(h, hipEventSynchronize(h->append_ev[slot]));
       for (int g = 0; g < G; ++g) {
         memcpy(hk + (size_t)g * c * D, k + ((size_t)g * n + t0) * D, (size_t)c * D * 2);
         memcpy(hv + (size_t)g * c * D, v + ((size_t)g * n + t0) * D, (size_t)c * D * 2);
       }
-      HIPCHK(h, hipMemcpyAsync(sk, hk, (size_t)2 * G * c * D * 2, hipMemcpyHostToDevice,
-                               h->stream));
-      HIPCHK(h, hipEventRecord(h->append_ev[slot], h->stream));
-      const uint16_t* sv = sk + (size_t)G * c * D;
+      const uint16_t* dk = h->append_host_dev + off;
       hipLaunchKernelGGL(k_pack_kv8, dim3(std::min(1024, (G * c * (D / 4) + 255) / 256)),
-                         dim3(256), 0, h->stream, sk, sv, c, (size_t)c, a.T + t0, a.kv_rows,
-                         (uint8_t*)a.kv8, a.kv_table, a.kv_shift);
+                         dim3(256), 0, h->stream, dk, dk + (size_t)G * c * D, c, (size_t)c,
+                         a.T + t0, a.kv_rows, (uint8_t*)a.kv8, a.kv_table, a.kv_shift);
       HIPCHK(h, hipGetLastError());
+      HIPCHK(h, hipEventRecord(h->append_ev[slot], h->stream));
     }
   }
   a.T += n;
