@@ -735,20 +735,25 @@ def main() -> int:
             # APPEND_BULK_REPS each
             attn.synchronize()
 
-            def bulk(kk, vv) -> float:
+            def bulk(kk, vv) -> tuple[float, list, list]:
+                # (median wall time, each append's wall time, each append
+                # call's own time before the host sync), µs
                 nonlocal used
-                times = []
+                times, calls = [], []
                 for _ in range(APPEND_BULK_REPS):
                     ks, vs = kk[:, used:used + APPEND_BULK], vv[:, used:used + APPEND_BULK]
                     t = time.perf_counter()
                     attn.append(ks, vs)
+                    tc = time.perf_counter()
                     attn.synchronize()
                     times.append((time.perf_counter() - t) * 1e6)
+                    calls.append((tc - t) * 1e6)
                     used += APPEND_BULK
-                return float(np.median(times))
+                return (float(np.median(times)), [round(x, 1) for x in times],
+                        [round(x, 1) for x in calls])
 
-            bulk_host_us = bulk(kn, vn)
-            bulk_dev_us = bulk(kd, vd)
+            bulk_host_us, bulk_host_each, bulk_host_calls = bulk(kn, vn)
+            bulk_dev_us, bulk_dev_each, bulk_dev_calls = bulk(kd, vd)
             host_ref, dev_ref = (base_us + mid_us) / 2, (mid_us + after_us) / 2
             log(f"decode loop: step {base_us:.1f} / {mid_us:.1f} / {after_us:.1f} µs (local "
                 f"window {p.local} / +{loop_steps} / +{2 * loop_steps}); with a 1-token host "
@@ -769,6 +774,10 @@ def main() -> int:
                 "bulk_tokens": APPEND_BULK,
                 "bulk_host_us": round(bulk_host_us, 1),
                 "bulk_device_us": round(bulk_dev_us, 1),
+                "bulk_host_each_us": bulk_host_each,
+                "bulk_host_call_us": bulk_host_calls,
+                "bulk_device_each_us": bulk_dev_each,
+                "bulk_device_call_us": bulk_dev_calls,
                 "appended": used,
                 "note": "decode loop per iteration: append 1 token, bind the query (8 KiB "
                         "upload; a host token rides along and the step's first kernel packs "
@@ -776,7 +785,8 @@ def main() -> int:
                         "loop_steps iterations, no host sync; *_over_step = against the mean "
                         "of the same loop without appends just before and after (the step "
                         "grows with the local window); bulk = median wall time of 3 appends of "
-                        "bulk_tokens, incl. host sync",
+                        "bulk_tokens, incl. host sync (*_each_us: every append in order; "
+                        "*_call_us: the append call alone, before the sync)",
             }
 
     sl_bytes, top_bytes = kv_gather_bytes(top_gpu, p)

@@ -169,8 +169,8 @@ int skv_debug_ids(void *handle, uint32_t *host_out);
  * step about 1 %); any other reader of the records (the dense decode, a
  * record readback, kernel timing, graph capture, another append) packs them
  * first.  Longer host appends are copied into pinned host slots of up to
- * 1024 tokens, which the pack kernel reads over the bus.  skv_append_device reads k and v on the handle's
- * stream; the allocations it has accepted (the last 8) are remembered, and
+ * 256 tokens, which the pack kernel reads over the bus.  skv_append_device
+ * reads k and v on the handle's stream; the allocations it has accepted (the last 8) are remembered, and
  * arrays inside one of them are not queried again.  Enqueued on the
  * handle's stream; fails with SKV_EINVAL, the cache unchanged, when n < 1,
  * n exceeds the capacity left or a device array is not such memory. */

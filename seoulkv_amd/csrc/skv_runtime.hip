@@ -50,7 +50,7 @@ struct Arena {
   }
 };
 
-constexpr int APPEND_CHUNK = 1024;  // tokens per host-append staging round
+constexpr int APPEND_CHUNK = 256;   // tokens per host-append staging round
 constexpr int Q_RING = 16;          // query staging slots (host run-ahead, in steps)
 constexpr int Q_MARK = 8;           // uploads per completion event of the staging ring
 
@@ -763,6 +763,13 @@ static int create_impl(const skv_index_desc* ix, const uint16_t* k_bf16, const u
     fail(h, SKV_EHIP, "pinned query staging failed");
     return bail(SKV_EHIP);
   }
+  // write every pinned staging page once now: the first CPU write into a
+  // fresh pinned page faults (measured ~100 us per 256 KiB, against ~5 us
+  // for a rewrite), a cost that would otherwise fall on the first binds and
+  // appends
+  memset(h->q_host, 0, (size_t)Q_RING * h->q_slot * 2);
+  if (h->append_host)
+    memset(h->append_host, 0, (size_t)2 * 2 * G * std::min(cap_app, APPEND_CHUNK) * D * 2);
 
   build_meta(h);
   *handle_out = h;

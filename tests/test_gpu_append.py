@@ -156,9 +156,9 @@ def test_append_with_graph_mode():
 
 
 def test_host_append_over_several_staging_chunks():
-    """A host append of 2100 tokens is staged in 1024-token rounds (three
-    rounds here): every record lands at its row and the step over the grown
-    cache equals the oracle's."""
+    """A host append of 2100 tokens is staged in 256-token rounds (nine
+    rounds here, through two alternating pinned slots): every record lands
+    at its row and the step over the grown cache equals the oracle's."""
     index, k, v, qs = case(**P)
     q = qs[0]
     n = 2100
