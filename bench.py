@@ -740,8 +740,14 @@ def main() -> int:
                 # call's own time before the host sync), µs
                 nonlocal used
                 times, calls = [], []
-                for _ in range(APPEND_BULK_REPS):
-                    ks, vs = kk[:, used:used + APPEND_BULK], vv[:, used:used + APPEND_BULK]
+                # the K/V of each append made contiguous before the clock
+                # starts (as the 1-token loop's slices): the timed call is
+                # the append, not the caller's copy into fresh pages
+                parts = [(kk[:, u:u + APPEND_BULK].contiguous(), vv[:, u:u + APPEND_BULK].contiguous())
+                         for u in range(used, used + APPEND_BULK_REPS * APPEND_BULK, APPEND_BULK)]
+                if kk.is_cuda:
+                    torch.cuda.synchronize()
+                for ks, vs in parts:
                     t = time.perf_counter()
                     attn.append(ks, vs)
                     tc = time.perf_counter()
@@ -785,8 +791,9 @@ def main() -> int:
                         "loop_steps iterations, no host sync; *_over_step = against the mean "
                         "of the same loop without appends just before and after (the step "
                         "grows with the local window); bulk = median wall time of 3 appends of "
-                        "bulk_tokens, incl. host sync (*_each_us: every append in order; "
-                        "*_call_us: the append call alone, before the sync)",
+                        "bulk_tokens (their K/V made contiguous before timing), incl. host sync "
+                        "(*_each_us: every append in order; *_call_us: the append call alone, "
+                        "before the sync)",
             }
 
     sl_bytes, top_bytes = kv_gather_bytes(top_gpu, p)
