@@ -179,6 +179,38 @@ def test_host_append_over_several_staging_chunks():
         rt.close()
 
 
+def test_host_appends_at_the_staging_slot_boundaries():
+    """Host appends of 255, 256, 257, 511, 512 and 513 tokens in a row: one
+    slot not quite full, exactly full, a second chunk of one token, both
+    slots, and a third chunk that reuses the first slot once the pack kernel
+    that read it has finished.  Every record lands at its row (FP8 bytes
+    against torch's cast) and the step over the grown cache equals the
+    oracle's."""
+    index, k, v, qs = case(**P)
+    q = qs[1]
+    sizes = (255, 256, 257, 511, 512, 513)
+    total = sum(sizes)
+    rt = _hip.Runtime(0, k, v, index, pool_min=0, pool_capacity=None, debug=True,
+                      append_capacity=total)
+    try:
+        ks, vs = [], []
+        for i, n in enumerate(sizes):
+            kn, vn = new_tokens(q, n, seed=40 + i)
+            print(f"[gpu] host append of {n} tokens", flush=True)
+            rt.append(kn, vn)
+            ks.append(kn)
+            vs.append(vn)
+        check_step(rt, q, ks, vs, "slot-boundary appends")
+        kb, vb = bits(torch.cat(ks, 1)), bits(torch.cat(vs, 1))
+        for g in range(4):
+            rec = rt.read_stage("kv8", g).reshape(-1, 512)
+            assert rec.shape[0] == P["context"] + total
+            np.testing.assert_array_equal(rec[P["context"]:, 256:], fp8_bytes(kb[g]))
+            np.testing.assert_array_equal(rec[P["context"]:, :256], fp8_bytes(vb[g]))
+    finally:
+        rt.close()
+
+
 @pytest.mark.parametrize("paged", [False, True])
 def test_decode_loop_folds_small_host_appends_into_the_step(paged):
     """A decoder's loop: append the decoded token from the host, bind the next
