@@ -1042,8 +1042,9 @@ static int append_tokens(Handle* h, const uint16_t* k, const uint16_t* v, int n,
   } else {
     // chunks of the caller's [G][n][D] arrays gathered into a pinned slot as
     // [K: G][c][D] then [V: G][c][D]; the pack kernel reads the slot over
-    // the bus (no copy engine: its latency varied by milliseconds between
-    // machines), and the slot is reused once that kernel has finished
+    // the bus (no device staging buffer and no copy-engine transfer, whose
+    // first use in a process took milliseconds), and the slot is reused once
+    // that kernel has finished
     const int chunk = std::min(h->append_capacity, APPEND_CHUNK);
     for (int t0 = 0; t0 < n; t0 += chunk) {
       const int c = std::min(chunk, n - t0);
