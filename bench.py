@@ -373,6 +373,7 @@ def time_steps(inst, stream, steps: int, warmup: int) -> float:
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    inst._run_bound()  # untimed lead step (see the main timed loop)
     start.record(stream)
     for _ in range(steps):
         inst._run_bound()
@@ -559,6 +560,13 @@ def main() -> int:
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
+        # one untimed step between the synchronize and the start event (here
+        # and in every timed loop below): the timed steps then follow queued
+        # work, so the window holds their device time, not the idle GPU's
+        # wait for the host's first launches (~28 us over the window, which
+        # a 20-step run would spread as +1.4 us per step; the host's own cost
+        # is host_inclusive_us)
+        attn._run_bound()
         start.record(stream)
         for _ in range(args.steps):
             attn._run_bound()
@@ -584,6 +592,7 @@ def main() -> int:
             inst._run_bound()
         torch.cuda.synchronize()
         n_cold = max(N_COLD, (args.steps // N_COLD) * N_COLD)
+        cold[-1]._run_bound()  # untimed lead step (the last instance, just used)
         start.record(stream)
         for i in range(n_cold):
             cold[i % N_COLD]._run_bound()
@@ -650,6 +659,7 @@ def main() -> int:
         for _ in range(args.warmup):
             paged._run_bound()
         torch.cuda.synchronize()
+        paged._run_bound()  # untimed lead step
         start.record(stream)
         for _ in range(args.steps):
             paged._run_bound()
